@@ -1,0 +1,347 @@
+"""Benchmark of the quantized-weight path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu]
+
+Headline (one JSON line on stdout): MatMulNBits q4 decode GEMV throughput in GB/s at M=1 on
+the Qwen3-0.6B projection shapes (block 32, f16 activations and scales, packed zero points).
+One step is one decode step's 196 projection GEMVs (28 layers x q, k, v, o, gate, up, down),
+each layer with its own weights; consecutive steps rotate over 4 copies of the 28 layers
+(1.02 GB of packed weights, 4x the 256 MB last-level cache) so the bytes come from HBM.
+Each step is one HIP graph of 196 launches on the library's stream; the timed region is K
+replays between two HIP events. GB/s counts the algorithmic bytes of each call: packed
+weights + scales + packed zero points + A + Y.
+
+The same line carries the M = 4/8/16 decode sweep, the prefill GEMM at SmolLM3-3B shapes
+(M = 256 and 2048, block 128, TFLOP/s), the large-vocabulary GatherBlockQuantized and lm_head,
+the roofline of the dominant kernel, and a CPU baseline: the reference's EXLA-CPU path after
+move/2 (weights dequantized once to f16, then an f32-accumulating GEMV on host threads),
+restated in C (oracle/oracle.c) and timed on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+# Qwen3-0.6B decode projections: (name, K, N)
+QWEN3_06B = [("q", 1024, 2048), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 2048, 1024),
+             ("gate", 1024, 3072), ("up", 1024, 3072), ("down", 3072, 1024)]
+QWEN3_LAYERS = 28
+# SmolLM3-3B prefill projections: (name, K, N)
+SMOLLM3_3B = [("attn 2048->2048", 2048, 2048), ("mlp 2048->11008", 2048, 11008), ("mlp 11008->2048", 11008, 2048)]
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def nbits_bytes(k, n, m, bits=4, bs=32, scale_bytes=2, zp=True, a_bytes=2, y_bytes=2):
+    """Algorithmic bytes of one MatMulNBits call."""
+    blocks = -(-k // bs)
+    total = n * blocks * bs * bits // 8 + n * blocks * scale_bytes
+    if zp:
+        total += n * (-(-blocks * bits // 8))
+    return total + m * k * a_bytes + m * n * y_bytes
+
+
+def make_weight_parts(rng, k, n, bits=4, bs=32, scale_mul=0.01):
+    blocks = -(-k // bs)
+    b = rng.integers(0, 256, (n, blocks, bs * bits // 8), dtype=np.uint8)
+    scales = (np.abs(rng.standard_normal(n * blocks, dtype=np.float32)) * scale_mul + 1e-4).astype(np.float16)
+    zp = rng.integers(0, 256, n * (-(-blocks * bits // 8)), dtype=np.uint8)
+    return b, scales, zp
+
+
+class Timer:
+    """HIP events on the library's stream."""
+
+    def __init__(self, ctx):
+        from transmuter_amd._lib import lib
+
+        self.ctx, self.lib = ctx, lib()
+        self.a, self.b = ctypes.c_void_p(), ctypes.c_void_p()
+        ctx.check(self.lib.tmh_event_create(ctx.handle, ctypes.byref(self.a)))
+        ctx.check(self.lib.tmh_event_create(ctx.handle, ctypes.byref(self.b)))
+
+    def start(self):
+        self.ctx.check(self.lib.tmh_event_record(self.ctx.handle, self.a, None))
+
+    def stop_ms(self) -> float:
+        self.ctx.check(self.lib.tmh_event_record(self.ctx.handle, self.b, None))
+        ms = ctypes.c_float()
+        self.ctx.check(self.lib.tmh_event_elapsed(self.ctx.handle, self.a, self.b, ctypes.byref(ms)))
+        return ms.value
+
+
+class Graph:
+    """A HIP graph recorded from calls on the library's stream."""
+
+    def __init__(self, ctx, record):
+        from transmuter_amd._lib import lib
+
+        self.ctx, self.lib = ctx, lib()
+        ctx.check(self.lib.tmh_graph_begin(ctx.handle, None))
+        try:
+            record()
+        finally:
+            self.exec = ctypes.c_void_p()
+            ctx.check(self.lib.tmh_graph_end(ctx.handle, None, ctypes.byref(self.exec)))
+
+    def launch(self):
+        self.ctx.check(self.lib.tmh_graph_launch(self.ctx.handle, self.exec, None))
+
+    def destroy(self):
+        self.ctx.check(self.lib.tmh_graph_destroy(self.ctx.handle, self.exec))
+
+
+def matmul_call(ctx, w, a, y, m):
+    from transmuter_amd._lib import F16, lib
+
+    ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, a.ptr, F16, m, w.k, None, 0, y.ptr, F16, w.n, None))
+
+
+def time_graphs(ctx, graphs, steps, warmup):
+    for i in range(warmup):
+        graphs[i % len(graphs)].launch()
+    ctx.synchronize()
+    t = Timer(ctx)
+    t.start()
+    for i in range(steps):
+        graphs[i % len(graphs)].launch()
+    return t.stop_ms()
+
+
+# ---------------------------------------------------------------- decode sweep (headline)
+
+
+def decode_sweep(ctx, steps, warmup, sets, ms):
+    from transmuter_amd import PackedWeight
+
+    rng = np.random.default_rng(20260101)
+    log(f"decode: packing {sets} x {QWEN3_LAYERS} layers of Qwen3-0.6B q4 weights")
+    t0 = time.time()
+    weights = []  # weights[s][layer][proj]
+    for s in range(sets):
+        layer_ws = []
+        for _layer in range(QWEN3_LAYERS):
+            row = []
+            for _name, k, n in QWEN3_06B:
+                b, sc, zp = make_weight_parts(rng, k, n)
+                row.append(PackedWeight.upload(ctx, b, sc, zp, k=k, n=n, bits=4, block_size=32, weight_dtype="f16"))
+            layer_ws.append(row)
+        weights.append(layer_ws)
+    log(f"decode: packed {sum(w.device_bytes() for ls in weights for l in ls for w in l) / 1e9:.2f} GB "
+        f"in {time.time() - t0:.1f} s")
+    results = {}
+    for m in ms:
+        a = {k: ctx.put(rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)) for k in (1024, 2048, 3072)}
+        y = {n: ctx.empty((m, n), "f16") for n in (1024, 2048, 3072)}
+        graphs = []
+        for s in range(sets):
+            def record(s=s):
+                for layer in range(QWEN3_LAYERS):
+                    for (_name, k, n), w in zip(QWEN3_06B, weights[s][layer]):
+                        matmul_call(ctx, w, a[k], y[n], m)
+            graphs.append(Graph(ctx, record))
+        step_bytes = QWEN3_LAYERS * sum(nbits_bytes(k, n, m) for _name, k, n in QWEN3_06B)
+        step_flops = QWEN3_LAYERS * sum(2 * m * k * n for _name, k, n in QWEN3_06B)
+        ms_total = time_graphs(ctx, graphs, steps, warmup)
+        ms_step = ms_total / steps
+        launches = steps * QWEN3_LAYERS * len(QWEN3_06B)
+        results[m] = {
+            "M": m, "gbs": step_bytes / (ms_step * 1e-3) / 1e9, "ms_per_step": ms_step,
+            "tflops": step_flops / (ms_step * 1e-3) / 1e12, "tokens_per_s": m * 1e3 / ms_step,
+            "us_per_launch": ms_total * 1e3 / launches, "bytes_per_launch": step_bytes / (QWEN3_LAYERS * len(QWEN3_06B)),
+            "step_bytes": step_bytes,
+        }
+        log(f"decode M={m}: {ms_step * 1e3:.1f} us/step, {results[m]['gbs']:.0f} GB/s, "
+            f"{results[m]['us_per_launch']:.2f} us/launch")
+        for g in graphs:
+            g.destroy()
+    for ls in weights:
+        for layer in ls:
+            for w in layer:
+                w.free()
+    return results
+
+
+# ---------------------------------------------------------------- prefill GEMM
+
+
+def prefill(ctx, reps, ms_list):
+    from transmuter_amd import PackedWeight
+
+    rng = np.random.default_rng(3)
+    out = {}
+    ws = []
+    for _name, k, n in SMOLLM3_3B:
+        b, sc, zp = make_weight_parts(rng, k, n, bs=128, scale_mul=0.005)
+        ws.append(PackedWeight.upload(ctx, b, sc, zp, k=k, n=n, bits=4, block_size=128, weight_dtype="f16"))
+    for m in ms_list:
+        per = []
+        for (name, k, n), w in zip(SMOLLM3_3B, ws):
+            a = ctx.put(rng.standard_normal((m, k), dtype=np.float32).astype(np.float16))
+            y = ctx.empty((m, n), "f16")
+            g = Graph(ctx, lambda w=w, a=a, y=y: matmul_call(ctx, w, a, y, m))
+            ms_total = time_graphs(ctx, [g], reps, 3)
+            g.destroy()
+            us = ms_total * 1e3 / reps
+            flops = 2 * m * k * n
+            per.append({"proj": name, "M": m, "us": us, "tflops": flops / (us * 1e-6) / 1e12})
+            log(f"prefill {name} M={m}: {us:.1f} us, {per[-1]['tflops']:.1f} TFLOP/s")
+        flops = sum(2 * m * k * n for _name, k, n in SMOLLM3_3B)
+        us = sum(p["us"] for p in per)
+        out[m] = {"tflops": flops / (us * 1e-6) / 1e12, "per_projection": per}
+    for w in ws:
+        w.free()
+    return out
+
+
+# ---------------------------------------------------------------- large vocabulary
+
+
+def large_vocab(ctx, reps):
+    from transmuter_amd import PackedWeight
+    from transmuter_amd._lib import F16, S64, U8, lib
+
+    rng = np.random.default_rng(4)
+    vocab, hidden = 151936, 1024
+    b, sc, zp = make_weight_parts(rng, hidden, vocab)
+    w = PackedWeight.upload(ctx, b, sc, zp, k=hidden, n=vocab, bits=4, block_size=32, weight_dtype="f16")
+    a = ctx.put(rng.standard_normal((8, hidden), dtype=np.float32).astype(np.float16))
+    y = ctx.empty((8, vocab), "f16")
+    g = Graph(ctx, lambda: matmul_call(ctx, w, a, y, 8))
+    us = time_graphs(ctx, [g], reps, 3) * 1e3 / reps
+    g.destroy()
+    lm_bytes = nbits_bytes(hidden, vocab, 8)
+    table = ctx.put(b.reshape(vocab, -1))
+    scales = ctx.put(sc.reshape(vocab, -1))
+    zps = ctx.put(zp.reshape(vocab, -1))
+    ids = ctx.put(rng.integers(0, vocab, (8, 512)).astype(np.int64))
+    out = ctx.empty((8, 512, hidden), "f16")
+
+    def gather():
+        ctx.check(lib().tmh_gather_block_quantized(ctx.handle, table.ptr, U8, vocab, hidden // 2, ids.ptr, S64, 4096,
+                                                   scales.ptr, F16, hidden // 32, zps.ptr, U8, 4, out.ptr, None))
+
+    g2 = Graph(ctx, gather)
+    us_g = time_graphs(ctx, [g2], reps, 3) * 1e3 / reps
+    g2.destroy()
+    g_bytes = 4096 * (hidden // 2 + hidden // 32 * 2 + hidden // 64 + 8) + 4096 * hidden * 2
+    w.free()
+    log(f"lm_head M=8: {us:.1f} us, {lm_bytes / us / 1e3:.0f} GB/s; gather: {us_g:.1f} us, {g_bytes / us_g / 1e3:.0f} GB/s")
+    return {"lm_head_M8": {"us": us, "gbs": lm_bytes / (us * 1e-6) / 1e9},
+            "gather_8x512": {"us": us_g, "gbs": g_bytes / (us_g * 1e-6) / 1e9}}
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+
+def cpu_baseline(seconds=10.0):
+    """The reference's EXLA-CPU path after move/2 restated in C: the q4 weights of a sample of
+    layers dequantized once to f16 (the scales' type), then Y = A . W^T with f32 accumulation on
+    host threads. Timed over whole decode steps of the sample; reported in the same GB/s
+    (algorithmic q4 bytes) as the GPU."""
+    from oracle import coracle
+
+    threads = min(16, os.cpu_count() or 1)
+    rng = np.random.default_rng(5)
+    layers = 2
+    ws = []
+    for _layer in range(layers):
+        for _name, k, n in QWEN3_06B:
+            b, sc, zp = make_weight_parts(rng, k, n)
+            w16 = coracle.dequantize_nbits(b, sc.astype(np.float32), zp, k, n, 4, 32, out_f16=True)
+            ws.append((k, n, w16))
+    a = {k: rng.standard_normal((1, k), dtype=np.float32) for k in (1024, 2048, 3072)}
+    step_bytes = layers * sum(nbits_bytes(k, n, 1) for _name, k, n in QWEN3_06B)
+    for k, _n, w16 in ws:  # warm-up
+        coracle.gemm(a[k], w16, threads)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        for k, _n, w16 in ws:
+            coracle.gemm(a[k], w16, threads)
+        done += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    gbs = done * step_bytes / elapsed / 1e9
+    log(f"cpu baseline: {done} samples in {elapsed:.1f} s, {gbs:.2f} GB/s on {threads} threads")
+    return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{layers} of 28 Qwen3-0.6B layers (14 q4 GEMVs, M=1) per sample, weights dequantized "
+                      f"once to f16, f32-accumulating GEMV on {threads} threads, {done} samples in {elapsed:.1f} s",
+            "ms_per_decode_step_28_layers": elapsed / done * 1e3 * 28 / layers}
+
+
+# ---------------------------------------------------------------- main
+
+
+def main():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--sets", type=int, default=4, help="weight copies the decode steps rotate over")
+    p.add_argument("--quick", action="store_true", help="decode M=1 only")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path runs on one GPU, "
+              "and its multi-GPU sharding is a design in DESIGN.md, not a measured run)", file=sys.stderr)
+        sys.exit(2)
+
+    from transmuter_amd import Context
+
+    ctx = Context(0)
+    ms = [1] if args.quick else [1, 4, 8, 16]
+    dec = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms)
+    extra = {}
+    if not args.quick:
+        extra["prefill"] = prefill(ctx, 20, [256, 2048])
+        extra["large_vocab"] = large_vocab(ctx, 50)
+    head = dec[1]
+    roofline = {
+        "bound": "hbm", "kernel": "k_gemv_f16<4,1,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
+        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "traffic": None,
+    }
+    roofline["frac"] = roofline["achieved"] / HBM_PEAK_GBS
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": "MatMulNBits q4: GB/s @M=1 and TFLOP/s @M=2048, % of MI355X roofline",
+        "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic (seeded random q4 weights, N(0,1) activations)",
+        "config": {"workload": "Qwen3-0.6B q4 decode projection sweep (28 layers x q,k,v,o,gate,up,down; block 32; "
+                               "f16 A and scales; packed zero points), M=1, 4 rotating weight copies",
+                   "M": 1, "layers": QWEN3_LAYERS, "weight_copies": args.sets, "parallelism": "single GPU"},
+        "tokens_per_s": head["tokens_per_s"],
+        "decode_sweep": {str(m): {k: v for k, v in r.items() if k in ("gbs", "tflops", "ms_per_step", "us_per_launch",
+                                                                      "tokens_per_s")} for m, r in dec.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    if "prefill" in extra:
+        line["prefill"] = {str(m): v for m, v in extra["prefill"].items()}
+        line["prefill_tflops_M2048"] = extra["prefill"][2048]["tflops"]
+        line["prefill_frac_M2048"] = extra["prefill"][2048]["tflops"] / MFMA_F16_PEAK_TFLOPS
+        line["large_vocab"] = extra["large_vocab"]
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,228 @@
+/*
+ * transmuter_hip.h - C ABI of the MI355X (gfx950) library behind Transmuter's quantized-weight
+ * operators: com.microsoft MatMulNBits, GatherBlockQuantized, DequantizeLinear and
+ * MatMulInteger (and the grouped-expert QMoE products).
+ *
+ * The reference (georgeguimaraes/transmuter) has no native code of its own: its operators are
+ * Elixir functions over Nx (lib/transmuter/ops/quantized.ex). These entry points are what a
+ * NIF bound by those handlers calls. Each declaration names the reference function whose
+ * arithmetic it replaces.
+ *
+ * Conventions
+ *  - Every call returns a tmh_status; 0 is success. On failure tmh_last_error() holds a
+ *    message. TMH_ERR_INVALID and TMH_ERR_UNSUPPORTED are the cases the reference raises
+ *    ArgumentError for (quantized.ex:33-34, :53-57); a NIF maps them to that exception.
+ *  - Pointers named d_* are device pointers (from tmh_alloc or any HIP allocation on the
+ *    context's device); pointers named h_* are host pointers the caller owns.
+ *  - Element types use ONNX TensorProto.DataType codes (tmh_dtype).
+ *  - `stream` is a hipStream_t; NULL means the context's own stream. Calls are asynchronous
+ *    on that stream unless stated otherwise.
+ *  - Shapes are int64_t element counts; no call reads or writes outside the extents given.
+ */
+#ifndef TRANSMUTER_HIP_H
+#define TRANSMUTER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TMH_ABI_VERSION 1
+
+typedef enum {
+  TMH_OK = 0,
+  TMH_ERR_INVALID = 1,     /* bad argument: sizes, types, null pointers */
+  TMH_ERR_UNSUPPORTED = 2, /* valid ONNX that this path does not run (g_idx, gather_axis != 0) */
+  TMH_ERR_DEVICE = 3,      /* a HIP runtime error */
+  TMH_ERR_OOM = 4,         /* device memory exhausted */
+  TMH_ERR_NO_DEVICE = 5    /* no usable gfx950 device */
+} tmh_status;
+
+/* ONNX TensorProto.DataType codes (lib/transmuter/ops.ex:700-713). */
+typedef enum {
+  TMH_F32 = 1,
+  TMH_U8 = 2,
+  TMH_S8 = 3,
+  TMH_U16 = 4,
+  TMH_S16 = 5,
+  TMH_S32 = 6,
+  TMH_S64 = 7,
+  TMH_F16 = 10,
+  TMH_BF16 = 16
+} tmh_dtype;
+
+/* Zero points of a MatMulNBits weight (quantized.ex:306-325): none (2^(bits-1)), packed
+ * integers (rows of ceil(blocks*bits/8) bytes, lowest bits first), or one float per block. */
+typedef enum { TMH_ZP_NONE = 0, TMH_ZP_PACKED = 1, TMH_ZP_FLOAT = 2 } tmh_zp_kind;
+
+/* Quantization parameter layout of DequantizeLinear (quantized.ex:328-353). */
+typedef enum { TMH_QPARAM_TENSOR = 0, TMH_QPARAM_AXIS = 1, TMH_QPARAM_BLOCKED = 2 } tmh_qparam_mode;
+
+typedef struct tmh_ctx tmh_ctx;       /* one device, one stream, the last error */
+typedef struct tmh_weight tmh_weight; /* a device-resident packed MatMulNBits weight */
+
+/* ------------------------------------------------------------------ context and memory */
+
+/* The ABI version this library implements (TMH_ABI_VERSION). */
+int tmh_abi_version(void);
+
+/* Number of HIP devices visible to the process. Fails with TMH_ERR_NO_DEVICE when none. */
+int tmh_device_count(int* count);
+
+/* Creates a context on `device`: sets it current for the calling thread and creates a stream.
+ * Fails with TMH_ERR_NO_DEVICE when the device is not a gfx950 GPU. */
+int tmh_ctx_create(int device, tmh_ctx** out);
+void tmh_ctx_destroy(tmh_ctx* ctx);
+
+/* The last error message of `ctx`, or of the calling thread when ctx is NULL. Never NULL. */
+const char* tmh_last_error(const tmh_ctx* ctx);
+
+/* The context's hipStream_t. */
+void* tmh_ctx_stream(tmh_ctx* ctx);
+
+/* Device memory of the context's device. tmh_alloc of 0 bytes gives NULL and succeeds. */
+int tmh_alloc(tmh_ctx* ctx, size_t bytes, void** d_out);
+int tmh_free(tmh_ctx* ctx, void* d_ptr);
+
+/* Synchronous copies: host to device, device to host (after the context's stream drains). */
+int tmh_upload(tmh_ctx* ctx, void* d_dst, const void* h_src, size_t bytes);
+int tmh_download(tmh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes);
+
+/* Blocks until the stream (NULL: the context's) has finished its work. */
+int tmh_synchronize(tmh_ctx* ctx, void* stream);
+
+/* HIP events for timing on a stream. tmh_event_elapsed waits for `end`. */
+int tmh_event_create(tmh_ctx* ctx, void** event_out);
+int tmh_event_destroy(tmh_ctx* ctx, void* event);
+int tmh_event_record(tmh_ctx* ctx, void* event, void* stream);
+int tmh_event_elapsed(tmh_ctx* ctx, void* start, void* end, float* ms_out);
+
+/* HIP graphs: capture the calls made on `stream` between begin and end into an executable
+ * graph, then replay it. Every compute call of this library is capture-safe (no allocation,
+ * no memset, no host synchronisation). */
+int tmh_graph_begin(tmh_ctx* ctx, void* stream);
+int tmh_graph_end(tmh_ctx* ctx, void* stream, void** graph_exec_out);
+int tmh_graph_launch(tmh_ctx* ctx, void* graph_exec, void* stream);
+int tmh_graph_destroy(tmh_ctx* ctx, void* graph_exec);
+
+/* ------------------------------------------------------------------ MatMulNBits */
+
+/*
+ * Uploads one MatMulNBits weight and keeps it on the device in the library's tiled layout.
+ * Replaces the load-time weight preparation of Transmuter.move/2 (lib/transmuter.ex:1104-1182,
+ * dequantized_weight/6 at :1230-1240) and of Transmuter.EMLX.weight/6 (lib/transmuter/emlx.ex:
+ * 104-148): the weight is packed once, not dequantized to floats.
+ *
+ *  h_b           B, u8 [N, blocks, block_size*bits/8], blocks = ceil(K/block_size)
+ *  h_scales      [N*blocks] of scales_dtype (F32, F16 or BF16)
+ *  h_zero_points none (NULL), packed u8 [N*ceil(blocks*bits/8)], or [N*blocks] floats of
+ *                zp_dtype, per zp_kind
+ *  weight_dtype  the type the weights dequantize in (F32, F16 or BF16): the scales' type
+ *                after :compute_type on the moved path, A's type in the graph (quantized.ex:42)
+ *  bits          2, 4 or 8; block_size a power of two >= 16 (nbits_sizes/1, quantized.ex:226)
+ * Sizes must match exactly; counts are element counts.
+ */
+int tmh_weight_upload_nbits(tmh_ctx* ctx, const uint8_t* h_b, size_t b_bytes, const void* h_scales,
+                            int scales_dtype, size_t scales_count, const void* h_zero_points,
+                            int zp_kind, int zp_dtype, size_t zp_count, int64_t K, int64_t N,
+                            int bits, int block_size, int weight_dtype, tmh_weight** out);
+void tmh_weight_free(tmh_weight* w);
+
+/*
+ * The host half of tmh_weight_upload_nbits: validates the same arguments and writes the
+ * tiled weights, the per-block scales (weight_dtype) and the zero points (u8 for packed, f32
+ * for float zero points) into caller buffers, without touching a device. With all three
+ * buffers NULL it only stores the byte counts; otherwise *q_bytes, *scale_bytes and
+ * *zero_bytes give the buffer capacities on entry and the bytes written on return. A NIF can
+ * pack on a host thread and upload later. No reference counterpart beyond move/2's
+ * dequantized_weight/6 (lib/transmuter.ex:1230-1240), whose device work this avoids.
+ */
+int tmh_pack_nbits_host(const uint8_t* h_b, size_t b_bytes, const void* h_scales, int scales_dtype,
+                        size_t scales_count, const void* h_zero_points, int zp_kind, int zp_dtype,
+                        size_t zp_count, int64_t K, int64_t N, int bits, int block_size,
+                        int weight_dtype, void* h_q, size_t* q_bytes, void* h_scale,
+                        size_t* scale_bytes, void* h_zero, size_t* zero_bytes);
+
+/* K, N, bits, block_size, the weight type and the device bytes the weight holds. */
+int tmh_weight_info(const tmh_weight* w, int64_t* K, int64_t* N, int* bits, int* block_size,
+                    int* weight_dtype, size_t* device_bytes);
+
+/*
+ * The {N, K} float weights of `w` in out_dtype, row-major, bit-exact to
+ * Quantized.dequantize_weight/4 (quantized.ex:234-240; unpack packed.ex:9-23, zero points
+ * quantized.ex:306-325, (q - zero) * scale packed.ex:28-36) computed in out_dtype.
+ */
+int tmh_dequantize_nbits(tmh_ctx* ctx, const tmh_weight* w, void* d_out, int out_dtype, void* stream);
+
+/*
+ * Y = A . W^T (+ bias): MatMulNBits (quantized.ex:30-46) over a packed weight.
+ *  d_a    [M, K] of a_dtype (F32, F16, BF16), rows lda elements apart (lda >= K)
+ *  d_bias NULL or [N] of bias_dtype
+ *  d_y    [M, N] of y_dtype, rows ldy elements apart (ldy >= N)
+ * The sums accumulate in f32 and round once to y_dtype. M >= 0 (M == 0 does nothing).
+ */
+int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
+                     int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype,
+                     int64_t ldy, void* stream);
+
+/* ------------------------------------------------------------------ GatherBlockQuantized */
+
+/*
+ * GatherBlockQuantized with gather_axis 0 and the quantize axis last (quantized.ex:49-66):
+ * out[i, :] = (unpack(data[ids[i], :]) - zero) * scale per block, in scales_dtype, bit-exact.
+ *  d_data        [rows, row_bytes] of data_dtype: U8 (unsigned values) or S8 (int4 values,
+ *                sign extended; 8-bit signed data when bits == 8)
+ *  d_ids         [n_ids] of ids_dtype (S32 or S64); a negative id counts from the end
+ *                (-rows..-1); ids outside [-rows, rows) clamp to [0, rows-1], as an XLA
+ *                gather clamps its start indices
+ *  d_scales      [rows, blocks] of scales_dtype (F32, F16, BF16)
+ *  d_zero_points NULL (0 for S8 data, 2^(bits-1) for U8) or packed [rows, zp_row_bytes]
+ *                (U8 or S8, zp_row_bytes = ceil(blocks*bits/8))
+ *  d_out         [n_ids, row_bytes*8/bits] of scales_dtype
+ * row_bytes*8/bits must be a multiple of blocks.
+ */
+int tmh_gather_block_quantized(tmh_ctx* ctx, const void* d_data, int data_dtype, int64_t rows,
+                               int64_t row_bytes, const void* d_ids, int ids_dtype, int64_t n_ids,
+                               const void* d_scales, int scales_dtype, int64_t blocks,
+                               const void* d_zero_points, int zp_dtype, int bits, void* d_out,
+                               void* stream);
+
+/* ------------------------------------------------------------------ DequantizeLinear */
+
+/*
+ * DequantizeLinear (quantized.ex:70-84 with expand_quant_param/3 at :328-353), bit-exact:
+ * integer x subtracts the zero point in s32, float x in f32; the value converts to f32, is
+ * multiplied by the f32 scale and rounds to scale_dtype.
+ * x is viewed as [outer, dim, inner], dim being the quantization axis. The scale (and zero
+ * point) is one value (TMH_QPARAM_TENSOR), [dim] (TMH_QPARAM_AXIS) or
+ * [outer, ceil(dim/block_size), inner] (TMH_QPARAM_BLOCKED).
+ *  x_dtype     U8, S8, U16, S16, S32, F16, F32 (or BF16)
+ *  scale_dtype F32, F16, BF16; zero NULL or of zero_dtype (integer types, or float for float x)
+ */
+int tmh_dequantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t outer, int64_t dim,
+                          int64_t inner, const void* d_scale, int scale_dtype, const void* d_zero,
+                          int zero_dtype, int mode, int64_t block_size, void* d_y, void* stream);
+
+/* ------------------------------------------------------------------ MatMulInteger */
+
+/*
+ * MatMulInteger (quantized.ex:105-110; exact sums of NN.integer_product/5, nn.ex:537-555):
+ * y[b, m, n] = sum_k (a[b, m, k] - a_zero[m]) * (b[(b,) k, n] - b_zero[n]) as s32
+ * (two's complement, as the reference's s32 additions).
+ *  d_a [batch, M, K] U8 or S8; d_b [K, N] (b_batched 0) or [batch, K, N] (1), U8 or S8
+ *  d_a_zero NULL, one value or [M] (a_zero_count 1 or M), of a's type
+ *  d_b_zero NULL, one value or [N] (b_zero_count 1 or N), of b's type
+ *  d_y [batch, M, N] S32
+ */
+int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d_b, int b_dtype,
+                       const void* d_a_zero, int64_t a_zero_count, const void* d_b_zero,
+                       int64_t b_zero_count, int64_t batch, int64_t M, int64_t K, int64_t N,
+                       int b_batched, void* d_y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRANSMUTER_HIP_H */

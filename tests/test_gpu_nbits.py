@@ -1,0 +1,164 @@
+"""MatMulNBits on the GPU against the oracle: dequantized weights bit-exactly, Y within the
+stated tolerance (max |Y - Y_ref| / max |Y_ref|: 1e-3 for f32 A, 1e-2 for f16 A, 2e-2 for bf16
+A, whose output rounds to 8 significant bits). Seeds and shapes are printed before each case."""
+
+import zlib
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from synth import nbits_weight
+from transmuter_amd import PackedWeight
+from transmuter_amd.quantized import matmul_nbits
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-3, "f16": 1e-2, "bf16": 2e-2}
+NP = {"f32": np.float32, "f16": np.float16}
+
+
+def host_float(x, dtype):
+    return o.bf16_round(x) if dtype == "bf16" else np.asarray(x).astype(NP[dtype])
+
+
+def as_f64(x, dtype):
+    return o.bf16_to_f32(x).astype(np.float64) if dtype == "bf16" else np.asarray(x, np.float64)
+
+
+def rel_err(y, ref):
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+DEQUANT_CASES = [
+    # bits, block, zp kind, K, N, scale type, weight type
+    (4, 32, "packed", 1024, 40, "f16", "f16"),
+    (4, 32, "none", 72, 17, "f32", "f32"),
+    (4, 16, "packed", 96, 33, "f16", "f16"),
+    (4, 16, "float", 64, 8, "f32", "f16"),
+    (4, 128, "packed", 1000, 24, "f16", "f16"),
+    (4, 256, "packed", 512, 40, "f32", "f32"),
+    (8, 32, "packed", 256, 19, "f16", "f16"),
+    (8, 128, "none", 384, 16, "f32", "bf16"),
+    (8, 16, "float", 48, 5, "f16", "f32"),
+    (2, 16, "packed", 64, 9, "f32", "f32"),
+    (2, 64, "none", 320, 31, "f16", "f16"),
+    (4, 64, "packed", 200, 50, "bf16", "bf16"),
+]
+
+
+@pytest.mark.parametrize("case", DEQUANT_CASES, ids=lambda c: "b{}_bs{}_{}_K{}_N{}_{}_{}".format(*c))
+def test_dequantize_bit_exact(ctx, case):
+    bits, bs, zp, k, n, sdt, wdt = case
+    print(f"dequant {case}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    b, s32, z = nbits_weight(rng, k, n, bits, bs, zp=zp, scale_dtype=np.float32)
+    scales = host_float(s32, sdt)
+    w = PackedWeight.upload(ctx, b, scales, z, k=k, n=n, bits=bits, block_size=bs, weight_dtype=wdt,
+                            scales_dtype=sdt)
+    got = w.dequantize().numpy()
+    ref = o.dequantize_weight(b, as_f64(scales, sdt).astype(np.float32), z, k, n, bits, bs, wdt)
+    ref = o.export(ref, wdt)
+    assert got.shape == (n, k)
+    assert np.array_equal(got.view(np.uint8), np.ascontiguousarray(ref).view(np.uint8))
+    w.free()
+
+
+MATMUL_CASES = [
+    # bits, block, zp, K, N, M list, A type, scale type, bias
+    (4, 32, "packed", 1024, 96, [1, 2, 5, 16, 17, 31, 33, 64, 65, 130], "f16", "f16", None),
+    (4, 32, "packed", 72, 16, [1, 6, 70], "f16", "f16", "f16"),
+    (4, 16, "packed", 256, 40, [1, 16, 40, 100], "f16", "f16", None),
+    (4, 128, "packed", 2048, 64, [1, 8, 256], "f16", "f16", "f32"),
+    (4, 256, "none", 512, 40, [3, 129], "f16", "f16", None),
+    (8, 32, "packed", 512, 48, [1, 4, 66], "f16", "f16", None),
+    (8, 128, "none", 1000, 20, [2, 200], "f16", "f16", "f16"),
+    (2, 16, "packed", 256, 24, [1, 20, 80], "f16", "f16", None),
+    (4, 32, "none", 1024, 48, [1, 3, 20], "f32", "f32", None),
+    (4, 32, "float", 64, 8, [6, 17], "f32", "f32", "f32"),
+    (4, 64, "packed", 192, 30, [1, 9], "bf16", "bf16", "bf16"),
+    (4, 32, "packed", 128, 16, [1, 5], "f32", "f16", None),
+    (8, 16, "packed", 64, 8, [4], "f16", "f32", None),
+    (4, 32, "float", 256, 32, [1, 18], "f16", "f16", None),
+]
+
+
+@pytest.mark.parametrize("case", MATMUL_CASES, ids=lambda c: "b{}_bs{}_{}_K{}_N{}_{}_{}_{}".format(
+    c[0], c[1], c[2], c[3], c[4], c[6], c[7], c[8]))
+def test_matmul_matches_oracle(ctx, case):
+    bits, bs, zp, k, n, ms, adt, sdt, bias_dt = case
+    rng = np.random.default_rng(zlib.crc32(repr(case[:5]).encode()))
+    b, s32, z = nbits_weight(rng, k, n, bits, bs, zp=zp, scale_dtype=np.float32)
+    scales = host_float(s32, sdt)
+    w = PackedWeight.upload(ctx, b, scales, z, k=k, n=n, bits=bits, block_size=bs, weight_dtype=sdt,
+                            scales_dtype=sdt)
+    bias = host_float(rng.standard_normal(n).astype(np.float32), bias_dt) if bias_dt else None
+    for m in ms:
+        print(f"matmul {case} M={m}", flush=True)
+        a = host_float(rng.standard_normal((m, k)).astype(np.float32), adt)
+        a_d = ctx.put(a, adt)
+        bias_d = ctx.put(bias, bias_dt) if bias is not None else None
+        y = matmul_nbits(a_d, w, bias_d)
+        got = as_f64(y.numpy(), y.dtype)
+        ref = o.matmul_nbits(a, b, as_f64(scales, sdt).astype(np.float32), z, bias, k=k, n=n, bits=bits,
+                             block_size=bs, weight_dtype=sdt)
+        ref_dtype = "bf16" if ref.dtype == np.uint16 else ("f16" if ref.dtype == np.float16 else "f32")
+        assert y.dtype == ref_dtype
+        err = rel_err(got, as_f64(ref, ref_dtype))
+        assert err <= TOL[adt], f"M={m}: relative error {err}"
+    w.free()
+
+
+def test_matmul_f16_fast_path_is_near_exact(ctx):
+    """The MFMA path sums exact f16 products in f32: against the f64 sum of the same f16
+    weights its error is a few f16 output roundings, far inside the 1e-2 bar."""
+    rng = np.random.default_rng(11)
+    k, n, m = 3072, 256, 16
+    b, s, z = nbits_weight(rng, k, n, 4, 32, zp="packed")
+    w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=4, block_size=32, weight_dtype="f16")
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    y = matmul_nbits(ctx.put(a), w).numpy().astype(np.float64)
+    wf = o.dequantize_weight(b, s, z, k, n, 4, 32, o.F16).astype(np.float64)
+    ref = a.astype(np.float64) @ wf.T
+    assert np.abs(y - ref).max() <= 2 * np.abs(ref).max() * 2.0 ** -11
+
+
+def test_matmul_zero_rows_is_a_no_op(ctx):
+    rng = np.random.default_rng(12)
+    b, s, z = nbits_weight(rng, 64, 16, 4, 32)
+    w = PackedWeight.upload(ctx, b, s, z, k=64, n=16, bits=4, block_size=32, weight_dtype="f16")
+    y = matmul_nbits(ctx.put(np.zeros((0, 64), np.float16)), w)
+    assert y.shape == (0, 16)
+
+
+def test_lda_ldy_strides(ctx):
+    """Rows of A and Y with gaps (lda > K, ldy > N) through the C ABI."""
+    import ctypes
+
+    from transmuter_amd._lib import F16, lib
+
+    rng = np.random.default_rng(13)
+    k, n, m, lda, ldy = 256, 32, 5, 264, 40
+    b, s, z = nbits_weight(rng, k, n, 4, 32)
+    w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=4, block_size=32, weight_dtype="f16")
+    a_full = rng.standard_normal((m, lda)).astype(np.float16)
+    a_d = ctx.put(a_full)
+    y_d = ctx.put(np.full((m, ldy), 7, np.float16))
+    ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, a_d.ptr, F16, m, lda, None, 0, y_d.ptr, F16, ldy, None))
+    y = y_d.numpy()
+    ref = o.matmul_nbits(a_full[:, :k], b, s, z, k=k, n=n, bits=4, block_size=32)
+    assert rel_err(y[:, :n].astype(np.float64), ref.astype(np.float64)) <= 1e-2
+    assert np.all(y[:, n:] == 7)
+    del ctypes
+
+
+def test_y_type_must_follow_the_reference(ctx):
+    from transmuter_amd._lib import F32, TmhArgumentError, lib
+
+    rng = np.random.default_rng(14)
+    b, s, z = nbits_weight(rng, 64, 16, 4, 32)
+    w = PackedWeight.upload(ctx, b, s, z, k=64, n=16, bits=4, block_size=32, weight_dtype="f16")
+    a_d = ctx.put(np.zeros((1, 64), np.float16))
+    y_d = ctx.empty((1, 16), "f32")
+    with pytest.raises(TmhArgumentError, match="Y must be f16"):
+        ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, a_d.ptr, 10, 1, 64, None, 0, y_d.ptr, F32, 16, None))

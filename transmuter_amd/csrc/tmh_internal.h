@@ -1,0 +1,92 @@
+// Internal declarations shared by the translation units of libtmhip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "../../include/transmuter_hip.h"
+
+struct tmh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string error;
+  int num_cus = 0;
+};
+
+// Tiled device layout of a MatMulNBits weight.
+//
+// Rows are grouped in tiles of 16 (one MFMA column block); each row's packed bytes are cut in
+// chunks of 64 bytes (CW = 512/bits weights). One (tile, chunk) holds 16 rows x 64 bytes =
+// 1 KiB, stored so that lane l = 16*g + r of a wavefront loads 16 contiguous bytes at offset
+// 16*l: row r of the tile, bytes 16*g .. 16*g+15 of the chunk. A wavefront's 16-byte load
+// therefore reads 1 KiB contiguously, and lane l holds the MFMA B-operand data of column r
+// for k-group g.
+//
+// Within each 32-bit word the sub-byte values are reordered so that value 2j sits at bits
+// j*bits and value 2j+1 at bits 16 + j*bits: ((x >> j*bits) & mask16) is the pair
+// (value 2j, value 2j+1), one per 16-bit half. 8-bit weights keep their byte order.
+//
+// Per (tile, chunk) the scales and zero points of the blocks each row touches are stored as
+// params[tile][chunk][j][r], j < nbc = max(1, CW / block_size): block j of the chunk's row r.
+struct tmh_weight {
+  int device = 0;
+  int64_t K = 0, N = 0;
+  int bits = 4, block_size = 32;
+  int64_t blocks = 0;   // ceil(K / block_size)
+  int64_t row_bytes = 0;  // blocks * block_size * bits / 8
+  int64_t nchunks = 0;  // ceil(row_bytes / 64)
+  int64_t ntiles = 0;   // ceil(N / 16)
+  int nbc = 1;          // parameter entries per row per chunk
+  int wdtype = TMH_F16; // dequantization type (F32, F16, BF16)
+  int zp_kind = TMH_ZP_NONE;
+  uint8_t* d_q = nullptr;   // ntiles*nchunks*1024 bytes
+  void* d_scale = nullptr;  // ntiles*nchunks*nbc*16 values of wdtype
+  void* d_zero = nullptr;   // u8 (packed zero points) or f32 (float zero points), same layout
+  size_t device_bytes = 0;
+};
+
+namespace tmh {
+
+constexpr int kTileRows = 16;
+constexpr int kChunkBytes = 64;
+
+inline int chunk_weights(int bits) { return kChunkBytes * 8 / bits; }
+
+inline int dtype_size(int dt) {
+  switch (dt) {
+    case TMH_F32: case TMH_S32: return 4;
+    case TMH_F16: case TMH_BF16: case TMH_U16: case TMH_S16: return 2;
+    case TMH_U8: case TMH_S8: return 1;
+    case TMH_S64: return 8;
+    default: return 0;
+  }
+}
+
+inline bool is_float_dtype(int dt) { return dt == TMH_F32 || dt == TMH_F16 || dt == TMH_BF16; }
+
+const char* dtype_name(int dt);
+
+// Error bookkeeping: the message goes to the context, or to a thread-local slot.
+int fail(tmh_ctx* ctx, int status, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+int check_hip(tmh_ctx* ctx, hipError_t err, const char* what);
+hipStream_t pick_stream(tmh_ctx* ctx, void* stream);
+int use_device(tmh_ctx* ctx);
+int check_launch(tmh_ctx* ctx, const char* kernel);
+
+// Host conversions (round to nearest even).
+float f16_to_f32(uint16_t h);
+uint16_t f32_to_f16(float f);
+float bf16_to_f32(uint16_t h);
+uint16_t f32_to_bf16(float f);
+float load_float(const void* p, int dt, size_t i);  // host read of a float array element
+
+}  // namespace tmh
+
+#define TMH_TRY(expr)          \
+  do {                         \
+    int _st = (expr);          \
+    if (_st != TMH_OK) return _st; \
+  } while (0)

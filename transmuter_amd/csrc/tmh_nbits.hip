@@ -1,0 +1,806 @@
+// MatMulNBits on gfx950: the packed-weight store, its dequantization, and Y = A . W^T.
+//
+// Reference arithmetic (georgeguimaraes/transmuter):
+//   lib/transmuter/ops/quantized.ex:30-46    MatMulNBits handler
+//   lib/transmuter/ops/quantized.ex:226-240  nbits_sizes/1, dequantize_weight/4
+//   lib/transmuter/ops/quantized.ex:294-325  unpack/2 (sign), block_zero_points/5
+//   lib/transmuter/ops/packed.ex:9-36        unpack/2 (lowest bits first), dequantize/3
+//   lib/transmuter.ex:1104-1240              move/2: packs each weight once at load
+//
+// Kernels
+//   k_dequant         the {N, K} weights, bit-exact, in any float type
+//   k_gemv_f16        f16 A and f16 weights, M <= 16*MT per block row: every lane unpacks its
+//                     16 bytes in registers into exact f16 weights (q - zero) * scale and feeds
+//                     v_mfma_f32_16x16x32_f16; four wavefronts split K and add through LDS
+//   k_gemm_f16        the same fragments for larger M, 128x128 tiles per workgroup
+//   k_matmul_general  any float types and float zero points, f32 FMA on the vector ALUs
+#include <algorithm>
+#include <cstdio>
+#include <vector>
+
+#include "tmh_device.h"
+#include "tmh_internal.h"
+
+using namespace tmh;
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+
+int ilog2(int v) {
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return s;
+}
+
+// ------------------------------------------------------------------ host repack
+
+// Position of value i of a 32-bit word in the tiled layout (see tmh_weight).
+inline int value_pos(int bits, int i) { return bits == 8 ? 8 * i : (i & 1) * 16 + (i >> 1) * bits; }
+
+uint32_t reorder_word(uint32_t natural, int bits) {
+  if (bits == 8) return natural;
+  const int count = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  uint32_t out = 0;
+  for (int i = 0; i < count; ++i) out |= ((natural >> (i * bits)) & mask) << value_pos(bits, i);
+  return out;
+}
+
+// Zero point of block b of row n from packed rows of ceil(blocks*bits/8) bytes, lowest bits
+// first (quantized.ex:316-323).
+uint8_t packed_zero(const uint8_t* zp, int64_t zrow, int bits, int64_t n, int64_t b) {
+  const int64_t bit = b * bits;
+  const uint8_t byte = zp[n * zrow + bit / 8];
+  return static_cast<uint8_t>((byte >> (bit % 8)) & ((1 << bits) - 1));
+}
+
+float round_host(float x, int dt) {
+  if (dt == TMH_F16) return f16_to_f32(f32_to_f16(x));
+  if (dt == TMH_BF16) return bf16_to_f32(f32_to_bf16(x));
+  return x;
+}
+
+void store_host(void* p, int dt, size_t i, float v) {
+  if (dt == TMH_F16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_f16(v);
+  } else if (dt == TMH_BF16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  } else {
+    static_cast<float*>(p)[i] = v;
+  }
+}
+
+int merge_float(int a, int b) {
+  if (a == b) return a;
+  return TMH_F32;
+}
+
+// ------------------------------------------------------------------ kernels
+
+// The {N, K} weights in OUT, computed in OUT from the stored scales (type WDT) and zero points.
+template <int BITS, int WDT, int OUT, int ZK>
+__global__ __launch_bounds__(256) void k_dequant(const uint4_t* __restrict__ qt,
+                                                 const void* __restrict__ sc,
+                                                 const void* __restrict__ zp, void* __restrict__ out,
+                                                 int64_t N, int64_t K, int64_t nchunks, int nbc,
+                                                 int bsc_shift, int64_t total_lanes) {
+  constexpr int CW = 512 / BITS;
+  constexpr int GW = CW / 4;
+  constexpr int PER_WORD = 32 / BITS;
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= total_lanes) return;
+  const int lane = static_cast<int>(id & 63);
+  const int64_t tc = id >> 6;
+  const int64_t t = tc / nchunks;
+  const int64_t c = tc - t * nchunks;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t n = t * 16 + r;
+  if (n >= N) return;
+  const uint4_t w = qt[id];
+#pragma unroll
+  for (int wi = 0; wi < 4; ++wi) {
+#pragma unroll
+    for (int v = 0; v < PER_WORD; ++v) {
+      const int woff = g * GW + wi * PER_WORD + v;
+      const int64_t k = c * CW + woff;
+      if (k >= K) continue;
+      const int64_t p = (tc * nbc + (woff >> bsc_shift)) * 16 + r;
+      const float s = round_to<OUT>(load_as_f32<WDT>(sc, p));
+      float z;
+      if constexpr (ZK == TMH_ZP_PACKED) {
+        z = static_cast<float>(static_cast<const uint8_t*>(zp)[p]);
+      } else if constexpr (ZK == TMH_ZP_FLOAT) {
+        z = round_to<OUT>(static_cast<const float*>(zp)[p]);
+      } else {
+        z = static_cast<float>(1 << (BITS - 1));
+      }
+      const float q = static_cast<float>(word_value<BITS>(w[wi], v));
+      store_as<OUT>(out, n * K + k, dequant_value<OUT>(q, z, s));
+    }
+  }
+}
+
+// Eight exact f16 weights (q - zero) * scale of MFMA step i of a lane, from its 16 bytes.
+// zz holds 1024 + zero (f16, both halves) and ss the scale (both halves); a 16-bit half
+// 0x6400 | q is the f16 number 1024 + q, so (0x6400 | q) - zz is q - zero exactly.
+template <int BITS>
+__device__ __forceinline__ half8_t unpack_step(const uint4_t& w, int i, half2_t zz, half2_t ss) {
+  uint32_t pr[4];
+  if constexpr (BITS == 4) {
+    const uint32_t x = w[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pr[j] = ((x >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+  } else if constexpr (BITS == 8) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t x = w[2 * i + h];
+      pr[2 * h] = (x & 0xFFu) | ((x << 8) & 0x00FF0000u) | 0x64006400u;
+      pr[2 * h + 1] = ((x >> 16) & 0xFFu) | ((x >> 8) & 0x00FF0000u) | 0x64006400u;
+    }
+  } else {  // 2 bits: step i uses half of word i/2
+    const uint32_t x = w[i >> 1] >> (8 * (i & 1));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pr[j] = ((x >> (2 * j)) & 0x00030003u) | 0x64006400u;
+  }
+  half8_t out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const half2_t q = __builtin_bit_cast(half2_t, pr[j]);
+    const half2_t wv = (q - zz) * ss;
+    out[2 * j] = wv[0];
+    out[2 * j + 1] = wv[1];
+  }
+  return out;
+}
+
+// Eight f16 values of A row m at columns k..k+7 (zeros outside the matrix).
+__device__ __forceinline__ half8_t load_a8(const _Float16* __restrict__ A, int64_t m, int64_t M,
+                                           int64_t k, int64_t K, int64_t lda, bool vec) {
+  half8_t a = {};
+  if (m >= M || k >= K) return a;
+  const _Float16* p = A + m * lda + k;
+  if (vec && k + 8 <= K) {
+    a = *reinterpret_cast<const half8_t*>(p);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = (k + e < K) ? p[e] : static_cast<_Float16>(0.0f);
+  }
+  return a;
+}
+
+// Scale and 1024 + zero of parameter entry p, as f16 pairs.
+template <bool HAS_ZP, int BITS>
+__device__ __forceinline__ void load_params(const uint16_t* __restrict__ sc,
+                                            const uint8_t* __restrict__ zp, int64_t p, half2_t& ss,
+                                            half2_t& zz) {
+  const uint32_t s = sc[p];
+  ss = __builtin_bit_cast(half2_t, s | (s << 16));
+  uint32_t z;
+  if constexpr (HAS_ZP) {
+    z = 0x6400u + zp[p];
+  } else {
+    z = 0x6400u + (1u << (BITS - 1));
+  }
+  zz = __builtin_bit_cast(half2_t, z | (z << 16));
+}
+
+// Adds the partial sums of the four wavefronts and writes rows m0.. of one 16-column tile.
+template <int MT>
+__device__ __forceinline__ void gemv_epilogue(float4_t (&acc)[MT], float4_t* red, int64_t t,
+                                              int64_t m0, int64_t M, int64_t N,
+                                              const void* __restrict__ bias, int bias_dt,
+                                              void* __restrict__ Y, int y_dt, int dot_dt,
+                                              int64_t ldy) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) red[(wave * MT + mt) * 64 + lane] = acc[mt];
+  __syncthreads();
+  // Wave w finishes m-tiles w, w+4, ...
+  for (int mt = wave; mt < MT; mt += kWaves) {
+    float4_t s = red[(0 * MT + mt) * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) s += red[(w * MT + mt) * 64 + lane];
+    const int64_t n = t * 16 + (lane & 15);
+    if (n >= N) continue;
+    const float b = bias ? load_float_rt(bias, bias_dt, n) : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t m = m0 + mt * 16 + 4 * (lane >> 4) + e;
+      if (m >= M) continue;
+      float v = s[e];
+      if (dot_dt == DT_F16) v = round_to<DT_F16>(v);
+      if (bias) v += b;
+      store_float_rt(Y, y_dt, m * ldy + n, v);
+    }
+  }
+}
+
+template <int BITS, int MT, bool HAS_ZP, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemv_f16(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, bool a_vec,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt,
+    int64_t ldy, int64_t N, int64_t nchunks, int nbc, int bsc_shift) {
+  constexpr int CW = 512 / BITS;
+  constexpr int GW = CW / 4;
+  constexpr int STEPS = GW / 8;
+  __shared__ float4_t red[kWaves * MT * 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t t = blockIdx.x;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 16 * MT;
+  const int64_t per = (nchunks + kWaves - 1) / kWaves;
+  const int64_t c0 = wave * per;
+  const int64_t c1 = c0 + per < nchunks ? c0 + per : nchunks;
+  float4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int64_t c = c0; c < c1; ++c) {
+    const int64_t tc = t * nchunks + c;
+    const uint4_t w = qt[tc * 64 + lane];
+    const int64_t kbase = c * CW + g * GW;
+    half2_t ss, zz;
+    if constexpr (!SPLIT) load_params<HAS_ZP, BITS>(sc, zp, (tc * nbc + ((g * GW) >> bsc_shift)) * 16 + r, ss, zz);
+#pragma unroll
+    for (int i = 0; i < STEPS; ++i) {
+      if constexpr (SPLIT)
+        load_params<HAS_ZP, BITS>(sc, zp, (tc * nbc + ((g * GW + 8 * i) >> bsc_shift)) * 16 + r, ss, zz);
+      const half8_t b = unpack_step<BITS>(w, i, zz, ss);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const half8_t a = load_a8(A, m0 + mt * 16 + r, M, kbase + 8 * i, K, lda, a_vec);
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[mt], 0, 0, 0);
+      }
+    }
+  }
+  gemv_epilogue<MT>(acc, red, t, m0, M, N, bias, bias_dt, Y, y_dt, dot_dt, ldy);
+}
+
+// 128 x 128 output tile per workgroup: wave (wm, wn) computes rows 64*wm.. and columns
+// 64*wn.. (four 16-row tiles by four 16-column tiles) over all of K.
+template <int BITS, bool HAS_ZP, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemm_f16(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, bool a_vec,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt,
+    int64_t ldy, int64_t N, int64_t ntiles, int64_t nchunks, int nbc, int bsc_shift) {
+  constexpr int CW = 512 / BITS;
+  constexpr int GW = CW / 4;
+  constexpr int STEPS = GW / 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 8 + wn * 4;  // first 16-column tile
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 128 + wm * 64;
+  float4_t acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int64_t c = 0; c < nchunks; ++c) {
+    uint4_t w[4];
+    int64_t tcs[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int64_t t = t0 + nt < ntiles ? t0 + nt : ntiles - 1;
+      tcs[nt] = t * nchunks + c;
+      w[nt] = qt[tcs[nt] * 64 + lane];
+    }
+    const int64_t kbase = c * CW + g * GW;
+    half2_t ss[4], zz[4];
+    if constexpr (!SPLIT) {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        load_params<HAS_ZP, BITS>(sc, zp, (tcs[nt] * nbc + ((g * GW) >> bsc_shift)) * 16 + r, ss[nt], zz[nt]);
+    }
+#pragma unroll
+    for (int i = 0; i < STEPS; ++i) {
+      half8_t bf[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        if constexpr (SPLIT)
+          load_params<HAS_ZP, BITS>(sc, zp, (tcs[nt] * nbc + ((g * GW + 8 * i) >> bsc_shift)) * 16 + r, ss[nt], zz[nt]);
+        bf[nt] = unpack_step<BITS>(w[nt], i, zz[nt], ss[nt]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const half8_t a = load_a8(A, m0 + mt * 16 + r, M, kbase + 8 * i, K, lda, a_vec);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bf[nt], acc[mt][nt], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int64_t n = (t0 + nt) * 16 + r;
+    if (t0 + nt >= ntiles || n >= N) continue;
+    const float b = bias ? load_float_rt(bias, bias_dt, n) : 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t m = m0 + mt * 16 + 4 * g + e;
+        if (m >= M) continue;
+        float v = acc[mt][nt][e];
+        if (dot_dt == DT_F16) v = round_to<DT_F16>(v);
+        if (bias) v += b;
+        store_float_rt(Y, y_dt, m * ldy + n, v);
+      }
+    }
+  }
+}
+
+// Any float types: the weights dequantize bit-exactly in WDT, then f32 FMA with A.
+// Block (t, y): rows 4*y .. 4*y+3 of A against the 16 columns of tile t.
+constexpr int kGeneralRows = 4;
+
+template <int BITS, int WDT, int ZK>
+__global__ __launch_bounds__(256) void k_matmul_general(
+    const uint4_t* __restrict__ qt, const void* __restrict__ sc, const void* __restrict__ zp,
+    const void* __restrict__ A, int a_dt, int64_t M, int64_t K, int64_t lda,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt,
+    int64_t ldy, int64_t N, int64_t nchunks, int nbc, int bsc_shift) {
+  constexpr int CW = 512 / BITS;
+  constexpr int GW = CW / 4;
+  constexpr int PER_WORD = 32 / BITS;
+  __shared__ float red[kWaves][kGeneralRows][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t t = blockIdx.x;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kGeneralRows;
+  const int64_t mcount = M - m0 < kGeneralRows ? M - m0 : kGeneralRows;
+  float acc[kGeneralRows] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t c = wave; c < nchunks; c += kWaves) {
+    const int64_t tc = t * nchunks + c;
+    const uint4_t w = qt[tc * 64 + lane];
+    for (int e = 0; e < GW; ++e) {
+      const int64_t k = c * CW + g * GW + e;
+      if (k >= K) break;
+      const int woff = g * GW + e;
+      const int64_t p = (tc * nbc + (woff >> bsc_shift)) * 16 + r;
+      const float s = load_as_f32<WDT>(sc, p);
+      float z;
+      if constexpr (ZK == TMH_ZP_PACKED) {
+        z = static_cast<float>(static_cast<const uint8_t*>(zp)[p]);
+      } else if constexpr (ZK == TMH_ZP_FLOAT) {
+        z = static_cast<const float*>(zp)[p];
+      } else {
+        z = static_cast<float>(1 << (BITS - 1));
+      }
+      const uint32_t word = w[e / PER_WORD];
+      const float wv = dequant_value<WDT>(static_cast<float>(word_value<BITS>(word, e % PER_WORD)), z, s);
+#pragma unroll
+      for (int mm = 0; mm < kGeneralRows; ++mm)
+        if (mm < mcount) acc[mm] = fmaf(load_float_rt(A, a_dt, (m0 + mm) * lda + k), wv, acc[mm]);
+    }
+  }
+#pragma unroll
+  for (int mm = 0; mm < kGeneralRows; ++mm) {
+    float v = acc[mm];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (g == 0) red[wave][mm][r] = v;
+  }
+  __syncthreads();
+  if (wave == 0 && g == 0) {
+    const int64_t n = t * 16 + r;
+    if (n < N) {
+      const float b = bias ? load_float_rt(bias, bias_dt, n) : 0.0f;
+      for (int mm = 0; mm < mcount; ++mm) {
+        float v = red[0][mm][r] + red[1][mm][r] + red[2][mm][r] + red[3][mm][r];
+        if (dot_dt == DT_F16) v = round_to<DT_F16>(v);
+        else if (dot_dt == DT_BF16) v = round_to<DT_BF16>(v);
+        if (bias) v += b;
+        store_float_rt(Y, y_dt, (m0 + mm) * ldy + n, v);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ launch helpers
+
+template <int BITS, int WDT, int OUT>
+void launch_dequant_zk(const tmh_weight* w, void* out, hipStream_t s, int bsc_shift) {
+  const int64_t lanes = w->ntiles * w->nchunks * 64;
+  const dim3 grid(static_cast<unsigned>((lanes + 255) / 256));
+  const auto* qt = reinterpret_cast<const uint4_t*>(w->d_q);
+  switch (w->zp_kind) {
+    case TMH_ZP_PACKED:
+      k_dequant<BITS, WDT, OUT, TMH_ZP_PACKED><<<grid, 256, 0, s>>>(qt, w->d_scale, w->d_zero, out, w->N, w->K, w->nchunks, w->nbc, bsc_shift, lanes);
+      break;
+    case TMH_ZP_FLOAT:
+      k_dequant<BITS, WDT, OUT, TMH_ZP_FLOAT><<<grid, 256, 0, s>>>(qt, w->d_scale, w->d_zero, out, w->N, w->K, w->nchunks, w->nbc, bsc_shift, lanes);
+      break;
+    default:
+      k_dequant<BITS, WDT, OUT, TMH_ZP_NONE><<<grid, 256, 0, s>>>(qt, w->d_scale, w->d_zero, out, w->N, w->K, w->nchunks, w->nbc, bsc_shift, lanes);
+  }
+}
+
+template <int BITS, int WDT>
+void launch_dequant_out(const tmh_weight* w, void* out, int out_dt, hipStream_t s, int bsc_shift) {
+  switch (out_dt) {
+    case TMH_F16: launch_dequant_zk<BITS, WDT, DT_F16>(w, out, s, bsc_shift); break;
+    case TMH_BF16: launch_dequant_zk<BITS, WDT, DT_BF16>(w, out, s, bsc_shift); break;
+    default: launch_dequant_zk<BITS, WDT, DT_F32>(w, out, s, bsc_shift);
+  }
+}
+
+template <int BITS>
+void launch_dequant_bits(const tmh_weight* w, void* out, int out_dt, hipStream_t s, int bsc_shift) {
+  switch (w->wdtype) {
+    case TMH_F16: launch_dequant_out<BITS, DT_F16>(w, out, out_dt, s, bsc_shift); break;
+    case TMH_BF16: launch_dequant_out<BITS, DT_BF16>(w, out, out_dt, s, bsc_shift); break;
+    default: launch_dequant_out<BITS, DT_F32>(w, out, out_dt, s, bsc_shift);
+  }
+}
+
+struct MatArgs {
+  const void* a;
+  int a_dt;
+  int64_t M, lda;
+  bool a_vec;
+  const void* bias;
+  int bias_dt;
+  void* y;
+  int y_dt, dot_dt;
+  int64_t ldy;
+};
+
+int bsc_shift_of(const tmh_weight* w) {
+  const int cw = chunk_weights(w->bits);
+  return ilog2(std::min(w->block_size, cw));
+}
+
+// True when a lane's k-group of one chunk spans more than one block (parameters per step).
+bool split_params(const tmh_weight* w) { return w->block_size < chunk_weights(w->bits) / 4; }
+
+template <int BITS, int MT, bool HAS_ZP, bool SPLIT>
+void launch_gemv(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  const int64_t mblocks = (a.M + 16 * MT - 1) / (16 * MT);
+  const dim3 grid(static_cast<unsigned>(w->ntiles), static_cast<unsigned>(mblocks));
+  k_gemv_f16<BITS, MT, HAS_ZP, SPLIT><<<grid, kThreads, 0, s>>>(
+      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+      static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda,
+      a.a_vec, a.bias, a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->nchunks, w->nbc,
+      bsc_shift_of(w));
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT>
+void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((w->ntiles + 7) / 8), static_cast<unsigned>((a.M + 127) / 128));
+  k_gemm_f16<BITS, HAS_ZP, SPLIT><<<grid, kThreads, 0, s>>>(
+      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+      static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda,
+      a.a_vec, a.bias, a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc,
+      bsc_shift_of(w));
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT>
+void launch_fast_variant(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  if (a.M <= 16) {
+    launch_gemv<BITS, 1, HAS_ZP, SPLIT>(w, a, s);
+  } else if (a.M <= 32) {
+    launch_gemv<BITS, 2, HAS_ZP, SPLIT>(w, a, s);
+  } else if (a.M <= 64 || BITS == 2) {
+    launch_gemv<BITS, 4, HAS_ZP, SPLIT>(w, a, s);
+  } else {
+    launch_gemm<BITS, HAS_ZP, SPLIT>(w, a, s);
+  }
+}
+
+template <int BITS>
+void launch_fast_bits(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  const bool zp = w->zp_kind == TMH_ZP_PACKED;
+  const bool split = split_params(w);
+  if (zp && split) launch_fast_variant<BITS, true, true>(w, a, s);
+  else if (zp) launch_fast_variant<BITS, true, false>(w, a, s);
+  else if (split) launch_fast_variant<BITS, false, true>(w, a, s);
+  else launch_fast_variant<BITS, false, false>(w, a, s);
+}
+
+template <int BITS, int WDT>
+void launch_general_wd(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(w->ntiles), static_cast<unsigned>((a.M + kGeneralRows - 1) / kGeneralRows));
+  const auto* qt = reinterpret_cast<const uint4_t*>(w->d_q);
+  const int shift = bsc_shift_of(w);
+#define TMH_GENERAL(ZK)                                                                        \
+  k_matmul_general<BITS, WDT, ZK><<<grid, kThreads, 0, s>>>(                                   \
+      qt, w->d_scale, w->d_zero, a.a, a.a_dt, a.M, w->K, a.lda, a.bias, a.bias_dt, a.y, a.y_dt, \
+      a.dot_dt, a.ldy, w->N, w->nchunks, w->nbc, shift)
+  switch (w->zp_kind) {
+    case TMH_ZP_PACKED: TMH_GENERAL(TMH_ZP_PACKED); break;
+    case TMH_ZP_FLOAT: TMH_GENERAL(TMH_ZP_FLOAT); break;
+    default: TMH_GENERAL(TMH_ZP_NONE);
+  }
+#undef TMH_GENERAL
+}
+
+template <int BITS>
+void launch_general_bits(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  switch (w->wdtype) {
+    case TMH_F16: launch_general_wd<BITS, DT_F16>(w, a, s); break;
+    case TMH_BF16: launch_general_wd<BITS, DT_BF16>(w, a, s); break;
+    default: launch_general_wd<BITS, DT_F32>(w, a, s);
+  }
+}
+
+// Validated sizes of one weight's tiled layout.
+struct PackPlan {
+  int64_t K, N, blocks, row_bytes, nchunks, ntiles, zrow;
+  int bits, block_size, cw, bsc, nbc, wdtype, zp_kind, zp_dtype, scales_dtype;
+  size_t q_bytes, scale_bytes, zero_bytes;
+};
+
+int plan_nbits(tmh_ctx* ctx, const uint8_t* h_b, size_t b_bytes, const void* h_scales, int scales_dtype,
+               size_t scales_count, const void* h_zero_points, int zp_kind, int zp_dtype, size_t zp_count,
+               int64_t K, int64_t N, int bits, int block_size, int weight_dtype, PackPlan* p) {
+  if (bits != 2 && bits != 4 && bits != 8)
+    return fail(ctx, TMH_ERR_INVALID, "MatMulNBits bits must be 2, 4 or 8, got %d", bits);
+  if (block_size < 16 || (block_size & (block_size - 1)) != 0)
+    return fail(ctx, TMH_ERR_INVALID, "MatMulNBits block_size must be a power of two >= 16, got %d", block_size);
+  if (K <= 0 || N <= 0)
+    return fail(ctx, TMH_ERR_INVALID, "MatMulNBits K and N must be positive, got K=%lld N=%lld", (long long)K, (long long)N);
+  if (K > (int64_t(1) << 31) || N > (int64_t(1) << 31))
+    return fail(ctx, TMH_ERR_INVALID, "MatMulNBits K and N must be at most 2^31");
+  if (!is_float_dtype(scales_dtype))
+    return fail(ctx, TMH_ERR_INVALID, "scales must be f32, f16 or bf16, got %s", dtype_name(scales_dtype));
+  if (!is_float_dtype(weight_dtype))
+    return fail(ctx, TMH_ERR_INVALID, "the weight type must be f32, f16 or bf16, got %s", dtype_name(weight_dtype));
+  if (!h_b || !h_scales) return fail(ctx, TMH_ERR_INVALID, "B and scales must not be NULL");
+  const int64_t blocks = (K + block_size - 1) / block_size;
+  const int64_t row_bytes = blocks * block_size * bits / 8;
+  if (static_cast<int64_t>(b_bytes) != N * row_bytes)
+    return fail(ctx, TMH_ERR_INVALID,
+                "B holds %zu bytes; N=%lld rows of %lld blocks of %d %d-bit weights need %lld", b_bytes,
+                (long long)N, (long long)blocks, block_size, bits, (long long)(N * row_bytes));
+  if (static_cast<int64_t>(scales_count) != N * blocks)
+    return fail(ctx, TMH_ERR_INVALID, "scales hold %zu values; N*blocks is %lld", scales_count, (long long)(N * blocks));
+  const int64_t zrow = (blocks * bits + 7) / 8;
+  if (zp_kind == TMH_ZP_PACKED) {
+    if (zp_dtype != TMH_U8) return fail(ctx, TMH_ERR_INVALID, "packed zero points must be u8, got %s", dtype_name(zp_dtype));
+    if (!h_zero_points) return fail(ctx, TMH_ERR_INVALID, "zero points are NULL");
+    if (static_cast<int64_t>(zp_count) != N * zrow)
+      return fail(ctx, TMH_ERR_INVALID, "packed zero points hold %zu bytes; N rows of %lld bytes need %lld", zp_count,
+                  (long long)zrow, (long long)(N * zrow));
+  } else if (zp_kind == TMH_ZP_FLOAT) {
+    if (!is_float_dtype(zp_dtype))
+      return fail(ctx, TMH_ERR_INVALID, "float zero points must be f32, f16 or bf16, got %s", dtype_name(zp_dtype));
+    if (!h_zero_points) return fail(ctx, TMH_ERR_INVALID, "zero points are NULL");
+    if (static_cast<int64_t>(zp_count) != N * blocks)
+      return fail(ctx, TMH_ERR_INVALID, "float zero points hold %zu values; N*blocks is %lld", zp_count, (long long)(N * blocks));
+  } else if (zp_kind != TMH_ZP_NONE) {
+    return fail(ctx, TMH_ERR_INVALID, "unknown zero point kind %d", zp_kind);
+  }
+  p->K = K;
+  p->N = N;
+  p->bits = bits;
+  p->block_size = block_size;
+  p->blocks = blocks;
+  p->row_bytes = row_bytes;
+  p->zrow = zrow;
+  p->nchunks = (row_bytes + kChunkBytes - 1) / kChunkBytes;
+  p->ntiles = (N + kTileRows - 1) / kTileRows;
+  p->cw = chunk_weights(bits);
+  p->bsc = std::min(block_size, p->cw);
+  p->nbc = p->cw / p->bsc;
+  p->wdtype = weight_dtype;
+  p->zp_kind = zp_kind;
+  p->zp_dtype = zp_dtype;
+  p->scales_dtype = scales_dtype;
+  const int64_t n_params = p->ntiles * p->nchunks * p->nbc * 16;
+  p->q_bytes = static_cast<size_t>(p->ntiles * p->nchunks * 1024);
+  p->scale_bytes = static_cast<size_t>(n_params * dtype_size(weight_dtype));
+  p->zero_bytes = zp_kind == TMH_ZP_PACKED ? static_cast<size_t>(n_params)
+                  : zp_kind == TMH_ZP_FLOAT ? static_cast<size_t>(n_params) * sizeof(float) : 0;
+  return TMH_OK;
+}
+
+// Fills the tiled weights, scales and zero points of a validated plan.
+void fill_nbits(const PackPlan& p, const uint8_t* h_b, const void* h_scales, const void* h_zero_points,
+                uint8_t* q, void* scale, void* zero) {
+  std::memset(q, 0, p.q_bytes);
+  for (int64_t t = 0; t < p.ntiles; ++t) {
+    for (int64_t c = 0; c < p.nchunks; ++c) {
+      uint8_t* dst = q + (t * p.nchunks + c) * 1024;
+      for (int l = 0; l < 64; ++l) {
+        const int r = l & 15, g = l >> 4;
+        const int64_t n = t * 16 + r;
+        const int64_t off = c * kChunkBytes + g * 16;
+        uint8_t bytes[16] = {0};
+        if (n < p.N)
+          for (int i = 0; i < 16; ++i)
+            if (off + i < p.row_bytes) bytes[i] = h_b[n * p.row_bytes + off + i];
+        for (int wd = 0; wd < 4; ++wd) {
+          uint32_t x;
+          std::memcpy(&x, bytes + 4 * wd, 4);
+          x = reorder_word(x, p.bits);
+          std::memcpy(dst + l * 16 + 4 * wd, &x, 4);
+        }
+      }
+    }
+  }
+  const auto* zp8 = static_cast<const uint8_t*>(h_zero_points);
+  auto* zero8 = static_cast<uint8_t*>(zero);
+  auto* zerof = static_cast<float*>(zero);
+  for (int64_t t = 0; t < p.ntiles; ++t) {
+    for (int64_t c = 0; c < p.nchunks; ++c) {
+      for (int j = 0; j < p.nbc; ++j) {
+        const int64_t b = (c * p.cw + static_cast<int64_t>(j) * p.bsc) / p.block_size;
+        for (int r = 0; r < 16; ++r) {
+          const int64_t n = t * 16 + r;
+          const size_t e = static_cast<size_t>(((t * p.nchunks + c) * p.nbc + j) * 16 + r);
+          const bool valid = n < p.N && b < p.blocks;
+          // The scales in the weight type (the Nx.as_type/2 of dequantize_weight/4).
+          const float s = valid ? round_host(load_float(h_scales, p.scales_dtype, static_cast<size_t>(n * p.blocks + b)), p.wdtype) : 0.0f;
+          store_host(scale, p.wdtype, e, s);
+          if (p.zp_kind == TMH_ZP_PACKED) {
+            zero8[e] = !valid ? static_cast<uint8_t>(1 << (p.bits - 1))
+                       : p.bits == 8 ? zp8[n * p.zrow + b] : packed_zero(zp8, p.zrow, p.bits, n, b);
+          } else if (p.zp_kind == TMH_ZP_FLOAT) {
+            zerof[e] = valid ? round_host(load_float(h_zero_points, p.zp_dtype, static_cast<size_t>(n * p.blocks + b)), p.wdtype) : 0.0f;
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int tmh_pack_nbits_host(const uint8_t* h_b, size_t b_bytes, const void* h_scales, int scales_dtype,
+                        size_t scales_count, const void* h_zero_points, int zp_kind, int zp_dtype,
+                        size_t zp_count, int64_t K, int64_t N, int bits, int block_size, int weight_dtype,
+                        void* h_q, size_t* q_bytes, void* h_scale, size_t* scale_bytes, void* h_zero,
+                        size_t* zero_bytes) {
+  PackPlan p;
+  TMH_TRY(plan_nbits(nullptr, h_b, b_bytes, h_scales, scales_dtype, scales_count, h_zero_points, zp_kind, zp_dtype,
+                     zp_count, K, N, bits, block_size, weight_dtype, &p));
+  if (!q_bytes || !scale_bytes || !zero_bytes) return fail(nullptr, TMH_ERR_INVALID, "the size outputs must not be NULL");
+  const bool query = !h_q && !h_scale && !h_zero;
+  if (!query) {
+    if (!h_q || !h_scale || (p.zero_bytes && !h_zero))
+      return fail(nullptr, TMH_ERR_INVALID, "pass every output buffer, or none to query the sizes");
+    if (*q_bytes < p.q_bytes || *scale_bytes < p.scale_bytes || *zero_bytes < p.zero_bytes)
+      return fail(nullptr, TMH_ERR_INVALID, "an output buffer is too small: need %zu, %zu and %zu bytes", p.q_bytes,
+                  p.scale_bytes, p.zero_bytes);
+    fill_nbits(p, h_b, h_scales, h_zero_points, static_cast<uint8_t*>(h_q), h_scale, h_zero);
+  }
+  *q_bytes = p.q_bytes;
+  *scale_bytes = p.scale_bytes;
+  *zero_bytes = p.zero_bytes;
+  return TMH_OK;
+}
+
+int tmh_weight_upload_nbits(tmh_ctx* ctx, const uint8_t* h_b, size_t b_bytes, const void* h_scales,
+                            int scales_dtype, size_t scales_count, const void* h_zero_points,
+                            int zp_kind, int zp_dtype, size_t zp_count, int64_t K, int64_t N,
+                            int bits, int block_size, int weight_dtype, tmh_weight** out) {
+  if (!ctx) return fail(nullptr, TMH_ERR_INVALID, "the context is NULL");
+  if (!out) return fail(ctx, TMH_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  PackPlan p;
+  TMH_TRY(plan_nbits(ctx, h_b, b_bytes, h_scales, scales_dtype, scales_count, h_zero_points, zp_kind, zp_dtype,
+                     zp_count, K, N, bits, block_size, weight_dtype, &p));
+  TMH_TRY(use_device(ctx));
+  std::vector<uint8_t> q(p.q_bytes), scale(p.scale_bytes), zero(p.zero_bytes);
+  fill_nbits(p, h_b, h_scales, h_zero_points, q.data(), scale.data(), zero.data());
+
+  tmh_weight* w = new tmh_weight();
+  w->device = ctx->device;
+  w->K = p.K;
+  w->N = p.N;
+  w->bits = p.bits;
+  w->block_size = p.block_size;
+  w->blocks = p.blocks;
+  w->row_bytes = p.row_bytes;
+  w->nchunks = p.nchunks;
+  w->ntiles = p.ntiles;
+  w->nbc = p.nbc;
+  w->wdtype = p.wdtype;
+  w->zp_kind = p.zp_kind;
+  int st = TMH_OK;
+  auto copy = [&](void** dst, const std::vector<uint8_t>& src) {
+    if (st != TMH_OK || src.empty()) return;
+    st = check_hip(ctx, hipMalloc(dst, src.size()), "hipMalloc (weight)");
+    if (st == TMH_OK)
+      st = check_hip(ctx, hipMemcpy(*dst, src.data(), src.size(), hipMemcpyHostToDevice), "hipMemcpy (weight)");
+  };
+  copy(reinterpret_cast<void**>(&w->d_q), q);
+  copy(&w->d_scale, scale);
+  copy(&w->d_zero, zero);
+  if (st != TMH_OK) {
+    tmh_weight_free(w);
+    return st;
+  }
+  w->device_bytes = q.size() + scale.size() + zero.size();
+  *out = w;
+  return TMH_OK;
+}
+
+void tmh_weight_free(tmh_weight* w) {
+  if (!w) return;
+  int prev = 0;
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(w->device);
+  if (w->d_q) (void)hipFree(w->d_q);
+  if (w->d_scale) (void)hipFree(w->d_scale);
+  if (w->d_zero) (void)hipFree(w->d_zero);
+  (void)hipSetDevice(prev);
+  delete w;
+}
+
+int tmh_weight_info(const tmh_weight* w, int64_t* K, int64_t* N, int* bits, int* block_size,
+                    int* weight_dtype, size_t* device_bytes) {
+  if (!w) return fail(nullptr, TMH_ERR_INVALID, "the weight is NULL");
+  if (K) *K = w->K;
+  if (N) *N = w->N;
+  if (bits) *bits = w->bits;
+  if (block_size) *block_size = w->block_size;
+  if (weight_dtype) *weight_dtype = w->wdtype;
+  if (device_bytes) *device_bytes = w->device_bytes;
+  return TMH_OK;
+}
+
+int tmh_dequantize_nbits(tmh_ctx* ctx, const tmh_weight* w, void* d_out, int out_dtype, void* stream) {
+  TMH_TRY(use_device(ctx));
+  if (!w) return fail(ctx, TMH_ERR_INVALID, "the weight is NULL");
+  if (w->device != ctx->device) return fail(ctx, TMH_ERR_INVALID, "the weight lives on device %d, the context on %d", w->device, ctx->device);
+  if (!d_out) return fail(ctx, TMH_ERR_INVALID, "the output is NULL");
+  if (!is_float_dtype(out_dtype)) return fail(ctx, TMH_ERR_INVALID, "the output type must be f32, f16 or bf16, got %s", dtype_name(out_dtype));
+  hipStream_t s = pick_stream(ctx, stream);
+  const int shift = bsc_shift_of(w);
+  switch (w->bits) {
+    case 2: launch_dequant_bits<2>(w, d_out, out_dtype, s, shift); break;
+    case 4: launch_dequant_bits<4>(w, d_out, out_dtype, s, shift); break;
+    default: launch_dequant_bits<8>(w, d_out, out_dtype, s, shift);
+  }
+  return check_launch(ctx, "k_dequant");
+}
+
+int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
+                     int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype,
+                     int64_t ldy, void* stream) {
+  TMH_TRY(use_device(ctx));
+  if (!w) return fail(ctx, TMH_ERR_INVALID, "the weight is NULL");
+  if (w->device != ctx->device) return fail(ctx, TMH_ERR_INVALID, "the weight lives on device %d, the context on %d", w->device, ctx->device);
+  if (M < 0) return fail(ctx, TMH_ERR_INVALID, "M must not be negative, got %lld", (long long)M);
+  if (!is_float_dtype(a_dtype)) return fail(ctx, TMH_ERR_INVALID, "A must be f32, f16 or bf16, got %s", dtype_name(a_dtype));
+  if (!is_float_dtype(y_dtype)) return fail(ctx, TMH_ERR_INVALID, "Y must be f32, f16 or bf16, got %s", dtype_name(y_dtype));
+  if (d_bias && !is_float_dtype(bias_dtype)) return fail(ctx, TMH_ERR_INVALID, "the bias must be f32, f16 or bf16, got %s", dtype_name(bias_dtype));
+  if (lda < w->K) return fail(ctx, TMH_ERR_INVALID, "lda %lld is below K %lld", (long long)lda, (long long)w->K);
+  if (ldy < w->N) return fail(ctx, TMH_ERR_INVALID, "ldy %lld is below N %lld", (long long)ldy, (long long)w->N);
+  // Nx.dot/4 gives the merged type of A and W; the bias then merges again (quantized.ex:44-45).
+  const int dot_dt = merge_float(a_dtype, w->wdtype);
+  const int expect = d_bias ? merge_float(dot_dt, bias_dtype) : dot_dt;
+  if (y_dtype != expect)
+    return fail(ctx, TMH_ERR_INVALID, "Y must be %s for A %s, weights %s%s%s", dtype_name(expect), dtype_name(a_dtype),
+                dtype_name(w->wdtype), d_bias ? " and bias " : "", d_bias ? dtype_name(bias_dtype) : "");
+  if (M == 0) return TMH_OK;
+  if (!d_a || !d_y) return fail(ctx, TMH_ERR_INVALID, "A and Y must not be NULL");
+  if (M > (int64_t(1) << 31) / 2) return fail(ctx, TMH_ERR_INVALID, "M is too large");
+  hipStream_t s = pick_stream(ctx, stream);
+  MatArgs a{d_a, a_dtype, M, lda, (reinterpret_cast<uintptr_t>(d_a) % 16 == 0) && (lda % 8 == 0),
+            d_bias, bias_dtype, d_y, y_dtype, dot_dt, ldy};
+  const bool fast = a_dtype == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT;
+  if (fast) {
+    switch (w->bits) {
+      case 2: launch_fast_bits<2>(w, a, s); break;
+      case 4: launch_fast_bits<4>(w, a, s); break;
+      default: launch_fast_bits<8>(w, a, s);
+    }
+    return check_launch(ctx, "k_gemv_f16/k_gemm_f16");
+  }
+  switch (w->bits) {
+    case 2: launch_general_bits<2>(w, a, s); break;
+    case 4: launch_general_bits<4>(w, a, s); break;
+    default: launch_general_bits<8>(w, a, s);
+  }
+  return check_launch(ctx, "k_matmul_general");
+}
+
+}  // extern "C"

@@ -1,0 +1,253 @@
+// Context, memory, events, graphs and error reporting of the C ABI.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "tmh_internal.h"
+
+namespace tmh {
+
+static thread_local std::string g_thread_error;
+
+const char* dtype_name(int dt) {
+  switch (dt) {
+    case TMH_F32: return "f32";
+    case TMH_F16: return "f16";
+    case TMH_BF16: return "bf16";
+    case TMH_U8: return "u8";
+    case TMH_S8: return "s8";
+    case TMH_U16: return "u16";
+    case TMH_S16: return "s16";
+    case TMH_S32: return "s32";
+    case TMH_S64: return "s64";
+    default: return "unknown type";
+  }
+}
+
+int fail(tmh_ctx* ctx, int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->error = buf;
+  g_thread_error = buf;
+  return status;
+}
+
+int check_hip(tmh_ctx* ctx, hipError_t err, const char* what) {
+  if (err == hipSuccess) return TMH_OK;
+  const int status = err == hipErrorOutOfMemory ? TMH_ERR_OOM : TMH_ERR_DEVICE;
+  return fail(ctx, status, "%s: %s", what, hipGetErrorString(err));
+}
+
+int use_device(tmh_ctx* ctx) {
+  if (!ctx) return fail(nullptr, TMH_ERR_INVALID, "the context is NULL");
+  return check_hip(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+}
+
+hipStream_t pick_stream(tmh_ctx* ctx, void* stream) {
+  return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+}
+
+int check_launch(tmh_ctx* ctx, const char* kernel) {
+  return check_hip(ctx, hipGetLastError(), kernel);
+}
+
+float f16_to_f32(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+
+uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+float bf16_to_f32(uint16_t h) {
+  const uint32_t u = static_cast<uint32_t>(h) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+float load_float(const void* p, int dt, size_t i) {
+  switch (dt) {
+    case TMH_F16: return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    case TMH_BF16: return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    default: return static_cast<const float*>(p)[i];
+  }
+}
+
+}  // namespace tmh
+
+using namespace tmh;
+
+extern "C" {
+
+int tmh_abi_version(void) { return TMH_ABI_VERSION; }
+
+int tmh_device_count(int* count) {
+  if (!count) return fail(nullptr, TMH_ERR_INVALID, "count is NULL");
+  *count = 0;
+  int n = 0;
+  hipError_t err = hipGetDeviceCount(&n);
+  if (err != hipSuccess || n == 0) {
+    (void)hipGetLastError();
+    return fail(nullptr, TMH_ERR_NO_DEVICE, "no HIP device: %s",
+                err == hipSuccess ? "none visible" : hipGetErrorString(err));
+  }
+  *count = n;
+  return TMH_OK;
+}
+
+int tmh_ctx_create(int device, tmh_ctx** out) {
+  if (!out) return fail(nullptr, TMH_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  TMH_TRY(tmh_device_count(&n));
+  if (device < 0 || device >= n)
+    return fail(nullptr, TMH_ERR_INVALID, "device %d is out of range (%d devices)", device, n);
+  hipDeviceProp_t prop;
+  hipError_t err = hipGetDeviceProperties(&prop, device);
+  if (err != hipSuccess) return check_hip(nullptr, err, "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(nullptr, TMH_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950",
+                device, prop.gcnArchName);
+  err = hipSetDevice(device);
+  if (err != hipSuccess) return check_hip(nullptr, err, "hipSetDevice");
+  tmh_ctx* ctx = new tmh_ctx();
+  ctx->device = device;
+  ctx->num_cus = prop.multiProcessorCount;
+  err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (err != hipSuccess) {
+    delete ctx;
+    return check_hip(nullptr, err, "hipStreamCreateWithFlags");
+  }
+  *out = ctx;
+  return TMH_OK;
+}
+
+void tmh_ctx_destroy(tmh_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) {
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamDestroy(ctx->stream);
+  }
+  delete ctx;
+}
+
+const char* tmh_last_error(const tmh_ctx* ctx) {
+  if (ctx) return ctx->error.c_str();
+  return g_thread_error.c_str();
+}
+
+void* tmh_ctx_stream(tmh_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+int tmh_alloc(tmh_ctx* ctx, size_t bytes, void** d_out) {
+  TMH_TRY(use_device(ctx));
+  if (!d_out) return fail(ctx, TMH_ERR_INVALID, "d_out is NULL");
+  *d_out = nullptr;
+  if (bytes == 0) return TMH_OK;
+  return check_hip(ctx, hipMalloc(d_out, bytes), "hipMalloc");
+}
+
+int tmh_free(tmh_ctx* ctx, void* d_ptr) {
+  TMH_TRY(use_device(ctx));
+  if (!d_ptr) return TMH_OK;
+  return check_hip(ctx, hipFree(d_ptr), "hipFree");
+}
+
+int tmh_upload(tmh_ctx* ctx, void* d_dst, const void* h_src, size_t bytes) {
+  TMH_TRY(use_device(ctx));
+  if (bytes == 0) return TMH_OK;
+  if (!d_dst || !h_src) return fail(ctx, TMH_ERR_INVALID, "tmh_upload: NULL pointer");
+  TMH_TRY(check_hip(ctx, hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, ctx->stream),
+                    "hipMemcpyAsync H2D"));
+  return check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+int tmh_download(tmh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes) {
+  TMH_TRY(use_device(ctx));
+  if (bytes == 0) return TMH_OK;
+  if (!h_dst || !d_src) return fail(ctx, TMH_ERR_INVALID, "tmh_download: NULL pointer");
+  TMH_TRY(check_hip(ctx, hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream),
+                    "hipMemcpyAsync D2H"));
+  return check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+int tmh_synchronize(tmh_ctx* ctx, void* stream) {
+  TMH_TRY(use_device(ctx));
+  return check_hip(ctx, hipStreamSynchronize(pick_stream(ctx, stream)), "hipStreamSynchronize");
+}
+
+int tmh_event_create(tmh_ctx* ctx, void** event_out) {
+  TMH_TRY(use_device(ctx));
+  if (!event_out) return fail(ctx, TMH_ERR_INVALID, "event_out is NULL");
+  hipEvent_t ev;
+  TMH_TRY(check_hip(ctx, hipEventCreate(&ev), "hipEventCreate"));
+  *event_out = ev;
+  return TMH_OK;
+}
+
+int tmh_event_destroy(tmh_ctx* ctx, void* event) {
+  TMH_TRY(use_device(ctx));
+  if (!event) return TMH_OK;
+  return check_hip(ctx, hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+}
+
+int tmh_event_record(tmh_ctx* ctx, void* event, void* stream) {
+  TMH_TRY(use_device(ctx));
+  if (!event) return fail(ctx, TMH_ERR_INVALID, "event is NULL");
+  return check_hip(ctx, hipEventRecord(static_cast<hipEvent_t>(event), pick_stream(ctx, stream)),
+                   "hipEventRecord");
+}
+
+int tmh_event_elapsed(tmh_ctx* ctx, void* start, void* end, float* ms_out) {
+  TMH_TRY(use_device(ctx));
+  if (!start || !end || !ms_out) return fail(ctx, TMH_ERR_INVALID, "tmh_event_elapsed: NULL");
+  TMH_TRY(check_hip(ctx, hipEventSynchronize(static_cast<hipEvent_t>(end)), "hipEventSynchronize"));
+  return check_hip(ctx,
+                   hipEventElapsedTime(ms_out, static_cast<hipEvent_t>(start),
+                                       static_cast<hipEvent_t>(end)),
+                   "hipEventElapsedTime");
+}
+
+int tmh_graph_begin(tmh_ctx* ctx, void* stream) {
+  TMH_TRY(use_device(ctx));
+  return check_hip(ctx, hipStreamBeginCapture(pick_stream(ctx, stream), hipStreamCaptureModeThreadLocal),
+                   "hipStreamBeginCapture");
+}
+
+int tmh_graph_end(tmh_ctx* ctx, void* stream, void** graph_exec_out) {
+  TMH_TRY(use_device(ctx));
+  if (!graph_exec_out) return fail(ctx, TMH_ERR_INVALID, "graph_exec_out is NULL");
+  *graph_exec_out = nullptr;
+  hipGraph_t graph = nullptr;
+  TMH_TRY(check_hip(ctx, hipStreamEndCapture(pick_stream(ctx, stream), &graph), "hipStreamEndCapture"));
+  hipGraphExec_t exec = nullptr;
+  hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  TMH_TRY(check_hip(ctx, err, "hipGraphInstantiate"));
+  *graph_exec_out = exec;
+  return TMH_OK;
+}
+
+int tmh_graph_launch(tmh_ctx* ctx, void* graph_exec, void* stream) {
+  TMH_TRY(use_device(ctx));
+  if (!graph_exec) return fail(ctx, TMH_ERR_INVALID, "graph_exec is NULL");
+  return check_hip(ctx, hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), pick_stream(ctx, stream)),
+                   "hipGraphLaunch");
+}
+
+int tmh_graph_destroy(tmh_ctx* ctx, void* graph_exec) {
+  TMH_TRY(use_device(ctx));
+  if (!graph_exec) return TMH_OK;
+  return check_hip(ctx, hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+}
+
+}  // extern "C"

@@ -1,0 +1,143 @@
+"""Device context and device-resident tensors over the C ABI of libtmhip.
+
+Types are named as Nx names them ("f32", "f16", "bf16", "u8", "s8", "s32", "s64", ...). bf16
+host arrays are uint16 bit patterns.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+
+NX_TO_TMH = {
+    "f32": _lib.F32, "f16": _lib.F16, "bf16": _lib.BF16,
+    "u8": _lib.U8, "s8": _lib.S8, "u16": _lib.U16, "s16": _lib.S16,
+    "s32": _lib.S32, "s64": _lib.S64,
+}
+NX_TO_NUMPY = {
+    "f32": np.float32, "f16": np.float16, "bf16": np.uint16,
+    "u8": np.uint8, "s8": np.int8, "u16": np.uint16, "s16": np.int16,
+    "s32": np.int32, "s64": np.int64,
+}
+NUMPY_TO_NX = {
+    np.dtype(np.float32): "f32", np.dtype(np.float16): "f16",
+    np.dtype(np.uint8): "u8", np.dtype(np.int8): "s8", np.dtype(np.uint16): "u16",
+    np.dtype(np.int16): "s16", np.dtype(np.int32): "s32", np.dtype(np.int64): "s64",
+}
+FLOAT_TYPES = ("f32", "f16", "bf16")
+
+
+def nx_type(array: np.ndarray) -> str:
+    try:
+        return NUMPY_TO_NX[np.asarray(array).dtype]
+    except KeyError:
+        raise TypeError(f"no device type for {np.asarray(array).dtype}") from None
+
+
+def merge_types(a: str, b: str) -> str:
+    """Nx.Type.merge/2 for the float types the operators produce."""
+    return a if a == b else "f32"
+
+
+class Context:
+    """One device and its stream (tmh_ctx)."""
+
+    def __init__(self, device: int = 0):
+        handle = ctypes.c_void_p()
+        check(lib().tmh_ctx_create(device, ctypes.byref(handle)))
+        self.handle = handle
+        self.device = device
+
+    @property
+    def stream(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(lib().tmh_ctx_stream(self.handle))
+
+    def check(self, status: int) -> None:
+        check(status, self.handle)
+
+    def alloc(self, nbytes: int) -> ctypes.c_void_p:
+        ptr = ctypes.c_void_p()
+        self.check(lib().tmh_alloc(self.handle, nbytes, ctypes.byref(ptr)))
+        return ptr
+
+    def free(self, ptr) -> None:
+        self.check(lib().tmh_free(self.handle, ptr))
+
+    def empty(self, shape, dtype: str) -> "DeviceTensor":
+        shape = tuple(int(s) for s in shape)
+        nbytes = math.prod(shape) * np.dtype(NX_TO_NUMPY[dtype]).itemsize
+        return DeviceTensor(self, self.alloc(nbytes), shape, dtype, nbytes)
+
+    def put(self, array: np.ndarray, dtype: str | None = None) -> "DeviceTensor":
+        """Copies a host array to the device. `dtype` names bf16 for uint16 bit patterns."""
+        host = np.ascontiguousarray(array)
+        dtype = dtype or nx_type(host)
+        t = self.empty(host.shape, dtype)
+        if t.nbytes:
+            self.check(lib().tmh_upload(self.handle, t.ptr, host.ctypes.data_as(ctypes.c_void_p), t.nbytes))
+        return t
+
+    def synchronize(self) -> None:
+        self.check(lib().tmh_synchronize(self.handle, None))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().tmh_ctx_destroy(self.handle)
+            self.handle = None
+
+
+class DeviceTensor:
+    """A device buffer with a shape and an Nx type, owned by this object."""
+
+    def __init__(self, ctx: Context, ptr, shape, dtype: str, nbytes: int):
+        self.ctx = ctx
+        self.ptr = ptr
+        self.shape = tuple(shape)
+        self.dtype = dtype
+        self.nbytes = nbytes
+
+    @property
+    def size(self) -> int:
+        return math.prod(self.shape)
+
+    @property
+    def tmh_dtype(self) -> int:
+        return NX_TO_TMH[self.dtype]
+
+    def numpy(self) -> np.ndarray:
+        host = np.empty(self.shape, dtype=NX_TO_NUMPY[self.dtype])
+        if self.nbytes:
+            self.ctx.check(lib().tmh_download(self.ctx.handle, host.ctypes.data_as(ctypes.c_void_p),
+                                              self.ptr, self.nbytes))
+        return host
+
+    def reshape(self, shape) -> "DeviceTensor":
+        """A view with another shape over the same buffer (the view does not own it)."""
+        shape = tuple(int(s) for s in shape)
+        if math.prod(shape) != self.size:
+            raise ValueError(f"cannot reshape {self.shape} to {shape}")
+        view = DeviceTensor(self.ctx, self.ptr, shape, self.dtype, self.nbytes)
+        view._base = self
+        view._owner = False
+        return view
+
+    def free(self) -> None:
+        if getattr(self, "_owner", True) and self.ptr:
+            self.ctx.free(self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            if getattr(self, "_owner", True) and self.ptr and self.ctx.handle:
+                lib().tmh_free(self.ctx.handle, self.ptr)
+                self.ptr = None
+        except Exception:
+            pass
+
+    def __repr__(self) -> str:
+        return f"DeviceTensor({self.shape}, {self.dtype})"

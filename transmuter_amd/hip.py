@@ -1,0 +1,140 @@
+"""Load-time weight preparation on the HIP backend: the hooks `Transmuter.move/2` calls.
+
+`Transmuter.move/2` (lib/transmuter.ex:1104-1182) picks a triple {compatible?, weight,
+evaluate} by backend; `Transmuter.EMLX` (lib/transmuter/emlx.ex:86-161) is the one device-
+packed precedent. This module is the third branch, with the same signatures:
+
+    compatible(node) -> bool
+    weight(node, b, scales, zero_points, model, backend) -> PackedWeight
+    evaluate(t) -> t
+
+and `move(model, ctx)` restates the node rewrite of move/2 over this package's model record:
+each packable, compatible MatMulNBits node reads [A, "<B>:packed", "", "", ...] afterwards, the
+weight is packed once per distinct B, and the B, scales and zero points no other node or graph
+output reads leave the params and static values. A second move leaves the model as it is.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field, replace
+
+import numpy as np
+
+from .device import Context, DeviceTensor
+from .packed import PackedWeight
+from .quantized import nbits_sizes
+
+
+@dataclass
+class Model:
+    """The parts of a loaded model that move/2 reads and writes (lib/transmuter.ex:186-242):
+    the nodes in order, the params (device values), the static (host) values, the graph
+    outputs, and :compute_type."""
+
+    nodes: list
+    params: dict = field(default_factory=dict)
+    static: dict = field(default_factory=dict)
+    outputs: list = field(default_factory=list)
+    compute_type: str | None = None
+    backend: object = None
+
+
+def upcast(value, compute_type: str | None):
+    """`Transmuter.upcast/2` (lib/transmuter.ex:1323-1327): f16 and bf16 values take the
+    compute type; other values stay as they are. Returns (value, type)."""
+    if value is None:
+        return None, None
+    arr = np.asarray(value)
+    dtype = "f16" if arr.dtype == np.float16 else ("f32" if arr.dtype == np.float32 else None)
+    if compute_type and dtype in ("f16", "bf16") and compute_type != dtype:
+        return arr.astype(np.float32), "f32"
+    return arr, dtype
+
+
+def compatible(node) -> bool:
+    """A MatMulNBits weight the library packs: 2, 4 or 8 bits and a power-of-two block of at
+    least 16 weights (any K; the last block may be partial). Compare
+    Transmuter.EMLX.compatible?/1 (emlx.ex:94-99), which also requires K % block_size == 0."""
+    k, n, bits, block = nbits_sizes(node)
+    return bits in (2, 4, 8) and block is not None and block >= 16 and block & (block - 1) == 0 \
+        and k > 0 and n > 0
+
+
+def packable(node, model: Model) -> bool:
+    """`packable?/2` (lib/transmuter.ex:1209-1216): scales named, no g_idx, bits in {2,4,8}, and a
+    B param of exactly N*K*bits/8 u8 bytes."""
+    if node.op_type != "MatMulNBits" or len(node.input) < 3:
+        return False
+    _a, b, scales, *rest = node.input
+    k, n, bits, _block = nbits_sizes(node)
+    g_idx = rest[1] if len(rest) > 1 else ""
+    value = model.params.get(b)
+    if scales == "" or g_idx != "" or bits not in (2, 4, 8) or value is None:
+        return False
+    if isinstance(value, PackedWeight):
+        return False
+    arr = np.asarray(value) if not isinstance(value, DeviceTensor) else None
+    dtype = value.dtype if isinstance(value, DeviceTensor) else ("u8" if arr.dtype == np.uint8 else None)
+    size = value.size if isinstance(value, DeviceTensor) else arr.size
+    return dtype == "u8" and size * 8 == n * k * bits
+
+
+def weight(node, b, scales, zero_points, model: Model, backend: Context) -> PackedWeight:
+    """The packed weight of a MatMulNBits node: its dequantization type is the scales' type
+    after :compute_type (dequantized_weight/6, lib/transmuter.ex:1230-1240)."""
+    k, n, bits, block = nbits_sizes(node)
+    scales, stype = upcast(scales.numpy() if isinstance(scales, DeviceTensor) else scales, model.compute_type)
+    return PackedWeight.upload(backend, b, scales, zero_points, k=k, n=n, bits=bits, block_size=block,
+                               weight_dtype=stype)
+
+
+def evaluate(t):
+    """Finishes a value made on the device: waits until its copies are done."""
+    if isinstance(t, (PackedWeight, DeviceTensor)):
+        t.ctx.synchronize()
+    return t
+
+
+def _packed_name(b: str) -> str:
+    return b + ":packed"
+
+
+def _packed_inputs(inputs: list, model: Model) -> list:
+    """The inputs of a packed node: the weight in place of B, no scales and zero points
+    (packed_inputs/2, lib/transmuter.ex:1185-1193)."""
+    a, b, *rest = inputs
+    name = _packed_name(b)
+    if name in model.params or name in model.static:
+        raise ValueError(f"the model already has a value named {name}")
+    out = [a, name, *rest]
+    while len(out) < 4:
+        out.append("")
+    out[2] = ""
+    out[3] = ""
+    return out
+
+
+def move(model: Model, ctx: Context) -> Model:
+    """`Transmuter.move/2` (lib/transmuter.ex:1104-1182) with the HIP hooks."""
+    packed = [node for node in model.nodes if packable(node, model) and compatible(node)]
+    packed_outputs = {node.output[0] for node in packed}
+    nodes = [replace(node, input=_packed_inputs(node.input, model)) if node.output and node.output[0] in packed_outputs
+             else node for node in model.nodes]
+    used = set(model.outputs)
+    for node in nodes:
+        used.update(node.input)
+    freed = {name for node in packed for name in node.input[1:4] if name and name not in used}
+    values = {**model.static, **model.params}
+    weights = {}
+    for node in packed:
+        b_name = node.input[1]
+        if _packed_name(b_name) in weights:
+            continue
+        scales = values[node.input[2]]
+        zp_name = node.input[3] if len(node.input) > 3 else ""
+        zero_points = values.get(zp_name) if zp_name else None
+        weights[_packed_name(b_name)] = evaluate(weight(node, values[b_name], scales, zero_points, model, ctx))
+    params = {name: value for name, value in model.params.items() if name not in freed}
+    params.update(weights)
+    static = {name: value for name, value in model.static.items() if name not in freed}
+    return replace(model, nodes=nodes, params=params, static=static, backend=ctx)

@@ -1,0 +1,99 @@
+"""Device-resident MatMulNBits weights (tmh_weight handles).
+
+A `PackedWeight` is what `Transmuter.move/2` stores under "<B>:packed" on this backend
+(lib/transmuter.ex:1155-1164): the packed bytes, scales and zero points of one weight, kept
+packed on the device. Like the MLX quantized tensor of `Transmuter.EMLX.weight/6`
+(lib/transmuter/emlx.ex:104-148) it presents as an {N, K} weight, so the MatMulNBits handler
+takes its fast branch (`Nx.shape(b) == {n, k}`, lib/transmuter/ops/quantized.ex:39-42).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import lib
+from .device import FLOAT_TYPES, NX_TO_TMH, Context, DeviceTensor, nx_type
+
+
+def _host(x, name: str):
+    """A host array of a weight part: numpy as is; a DeviceTensor is copied back."""
+    if x is None:
+        return None, None
+    if isinstance(x, DeviceTensor):
+        return np.ascontiguousarray(x.numpy()), x.dtype
+    arr = np.ascontiguousarray(x)
+    return arr, nx_type(arr)
+
+
+class PackedWeight:
+    """One MatMulNBits weight on the device, in the library's tiled layout."""
+
+    def __init__(self, ctx: Context, handle: ctypes.c_void_p, k: int, n: int, bits: int, block_size: int,
+                 dtype: str):
+        self.ctx = ctx
+        self.handle = handle
+        self.k, self.n, self.bits, self.block_size = k, n, bits, block_size
+        self.dtype = dtype  # the type the weights dequantize in
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self.n, self.k)
+
+    @classmethod
+    def upload(cls, ctx: Context, b, scales, zero_points, *, k: int, n: int, bits: int, block_size: int,
+               weight_dtype: str, scales_dtype: str | None = None, zero_points_dtype: str | None = None
+               ) -> "PackedWeight":
+        """Packs B [N, blocks, block_size*bits/8] (u8), scales [N*blocks] and zero points (none,
+        packed u8 rows, or floats) into a device weight whose values dequantize in weight_dtype.
+        bf16 host arrays are uint16 bit patterns and need scales_dtype / zero_points_dtype."""
+        if weight_dtype not in FLOAT_TYPES:
+            raise ValueError(f"weight type must be one of {FLOAT_TYPES}, got {weight_dtype}")
+        hb, bdt = _host(b, "B")
+        if bdt != "u8":
+            raise _lib.TmhArgumentError(_lib.ERR_INVALID, f"MatMulNBits B must be u8 bytes, got {bdt}")
+        hs, sdt = _host(scales, "scales")
+        sdt = scales_dtype or sdt
+        hz, zdt = _host(zero_points, "zero_points")
+        if hz is None:
+            zp_kind, zdt = _lib.ZP_NONE, "u8"
+        else:
+            zdt = zero_points_dtype or zdt
+            zp_kind = _lib.ZP_FLOAT if zdt in FLOAT_TYPES else _lib.ZP_PACKED
+        handle = ctypes.c_void_p()
+        status = lib().tmh_weight_upload_nbits(
+            ctx.handle, hb.ctypes.data_as(ctypes.c_void_p), hb.nbytes,
+            hs.ctypes.data_as(ctypes.c_void_p), NX_TO_TMH[sdt], hs.size,
+            hz.ctypes.data_as(ctypes.c_void_p) if hz is not None else None, zp_kind, NX_TO_TMH[zdt],
+            hz.size if hz is not None else 0, k, n, bits, block_size, NX_TO_TMH[weight_dtype],
+            ctypes.byref(handle))
+        ctx.check(status)
+        return cls(ctx, handle, k, n, bits, block_size, weight_dtype)
+
+    def device_bytes(self) -> int:
+        size = ctypes.c_size_t()
+        _lib.check(lib().tmh_weight_info(self.handle, None, None, None, None, None, ctypes.byref(size)))
+        return size.value
+
+    def dequantize(self, dtype: str | None = None, stream=None) -> DeviceTensor:
+        """The {N, K} float weights (tmh_dequantize_nbits), in `dtype` (default: its own type)."""
+        dtype = dtype or self.dtype
+        out = self.ctx.empty((self.n, self.k), dtype)
+        self.ctx.check(lib().tmh_dequantize_nbits(self.ctx.handle, self.handle, out.ptr, NX_TO_TMH[dtype], stream))
+        return out
+
+    def free(self) -> None:
+        if self.handle:
+            lib().tmh_weight_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def __repr__(self) -> str:
+        return f"PackedWeight(N={self.n}, K={self.k}, bits={self.bits}, block_size={self.block_size}, {self.dtype})"
