@@ -86,12 +86,17 @@ class Timer:
 
 
 class Graph:
-    """A HIP graph recorded from calls on the library's stream."""
+    """A HIP graph recorded from calls on the library's stream. With USE_GRAPHS off (the
+    --no-graph flag, for tracers that do not follow graph launches) the calls are replayed
+    directly on the stream instead."""
 
     def __init__(self, ctx, record):
         from transmuter_amd._lib import lib
 
-        self.ctx, self.lib = ctx, lib()
+        self.ctx, self.lib, self.record = ctx, lib(), record
+        self.exec = None
+        if not USE_GRAPHS:
+            return
         ctx.check(self.lib.tmh_graph_begin(ctx.handle, None))
         try:
             record()
@@ -100,10 +105,17 @@ class Graph:
             ctx.check(self.lib.tmh_graph_end(ctx.handle, None, ctypes.byref(self.exec)))
 
     def launch(self):
-        self.ctx.check(self.lib.tmh_graph_launch(self.ctx.handle, self.exec, None))
+        if self.exec is None:
+            self.record()
+        else:
+            self.ctx.check(self.lib.tmh_graph_launch(self.ctx.handle, self.exec, None))
 
     def destroy(self):
-        self.ctx.check(self.lib.tmh_graph_destroy(self.ctx.handle, self.exec))
+        if self.exec is not None:
+            self.ctx.check(self.lib.tmh_graph_destroy(self.ctx.handle, self.exec))
+
+
+USE_GRAPHS = True
 
 
 def matmul_call(ctx, w, a, y, m):
@@ -126,7 +138,9 @@ def time_graphs(ctx, graphs, steps, warmup):
 # ---------------------------------------------------------------- decode sweep (headline)
 
 
-def decode_sweep(ctx, steps, warmup, sets, ms):
+def decode_sweep(ctx, steps, warmup, sets, ms, merged=False):
+    """merged: q/k/v and gate/up run as one call each over concatenated weights, as the
+    reference's move/2 + Fusion.matmuls/2 leave a Qwen3 layer (4 calls instead of 7)."""
     from transmuter_amd import PackedWeight
 
     rng = np.random.default_rng(20260101)
@@ -141,6 +155,9 @@ def decode_sweep(ctx, steps, warmup, sets, ms):
                 b, sc, zp = make_weight_parts(rng, k, n)
                 row.append(PackedWeight.upload(ctx, b, sc, zp, k=k, n=n, bits=4, block_size=32, weight_dtype="f16"))
             layer_ws.append(row)
+        if merged:
+            layer_ws = [[PackedWeight.concat(row[0:3]), row[3], PackedWeight.concat(row[4:6]), row[6]]
+                        for row in layer_ws]
         weights.append(layer_ws)
     log(f"decode: packed {sum(w.device_bytes() for ls in weights for l in ls for w in l) / 1e9:.2f} GB "
         f"in {time.time() - t0:.1f} s")
@@ -148,25 +165,28 @@ def decode_sweep(ctx, steps, warmup, sets, ms):
     for m in ms:
         a = {k: ctx.put(rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)) for k in (1024, 2048, 3072)}
         y = {n: ctx.empty((m, n), "f16") for n in (1024, 2048, 3072)}
+        for n in (4096, 6144):
+            y[n] = ctx.empty((m, n), "f16")
         graphs = []
         for s in range(sets):
             def record(s=s):
                 for layer in range(QWEN3_LAYERS):
-                    for (_name, k, n), w in zip(QWEN3_06B, weights[s][layer]):
-                        matmul_call(ctx, w, a[k], y[n], m)
+                    for w in weights[s][layer]:
+                        matmul_call(ctx, w, a[w.k], y[w.n], m)
             graphs.append(Graph(ctx, record))
-        step_bytes = QWEN3_LAYERS * sum(nbits_bytes(k, n, m) for _name, k, n in QWEN3_06B)
+        step_bytes = QWEN3_LAYERS * sum(nbits_bytes(w.k, w.n, m) for w in weights[0][0])
         step_flops = QWEN3_LAYERS * sum(2 * m * k * n for _name, k, n in QWEN3_06B)
         ms_total = time_graphs(ctx, graphs, steps, warmup)
         ms_step = ms_total / steps
-        launches = steps * QWEN3_LAYERS * len(QWEN3_06B)
+        per_layer = len(weights[0][0])
+        launches = steps * QWEN3_LAYERS * per_layer
         results[m] = {
             "M": m, "gbs": step_bytes / (ms_step * 1e-3) / 1e9, "ms_per_step": ms_step,
             "tflops": step_flops / (ms_step * 1e-3) / 1e12, "tokens_per_s": m * 1e3 / ms_step,
-            "us_per_launch": ms_total * 1e3 / launches, "bytes_per_launch": step_bytes / (QWEN3_LAYERS * len(QWEN3_06B)),
+            "us_per_launch": ms_total * 1e3 / launches, "bytes_per_launch": step_bytes / (QWEN3_LAYERS * per_layer),
             "step_bytes": step_bytes,
         }
-        log(f"decode M={m}: {ms_step * 1e3:.1f} us/step, {results[m]['gbs']:.0f} GB/s, "
+        log(f"decode{' merged' if merged else ''} M={m}: {ms_step * 1e3:.1f} us/step, {results[m]['gbs']:.0f} GB/s, "
             f"{results[m]['us_per_launch']:.2f} us/launch")
         for g in graphs:
             g.destroy()
@@ -297,7 +317,10 @@ def main():
     p.add_argument("--quick", action="store_true", help="decode M=1 only")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--no-graph", action="store_true", help="launch each call on the stream, no HIP graphs")
     args = p.parse_args()
+    global USE_GRAPHS
+    USE_GRAPHS = not args.no_graph
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path runs on one GPU, "
               "and its multi-GPU sharding is a design in DESIGN.md, not a measured run)", file=sys.stderr)
@@ -308,6 +331,7 @@ def main():
     ctx = Context(0)
     ms = [1] if args.quick else [1, 4, 8, 16]
     dec = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms)
+    dec_merged = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms, merged=True)
     extra = {}
     if not args.quick:
         extra["prefill"] = prefill(ctx, 20, [256, 2048])
@@ -331,6 +355,9 @@ def main():
         "tokens_per_s": head["tokens_per_s"],
         "decode_sweep": {str(m): {k: v for k, v in r.items() if k in ("gbs", "tflops", "ms_per_step", "us_per_launch",
                                                                       "tokens_per_s")} for m, r in dec.items()},
+        "decode_merged_qkv_gateup": {str(m): {k: v for k, v in r.items() if k in ("gbs", "ms_per_step", "us_per_launch",
+                                                                                  "tokens_per_s")}
+                                     for m, r in dec_merged.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

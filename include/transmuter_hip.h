@@ -90,6 +90,12 @@ int tmh_free(tmh_ctx* ctx, void* d_ptr);
 int tmh_upload(tmh_ctx* ctx, void* d_dst, const void* h_src, size_t bytes);
 int tmh_download(tmh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes);
 
+/* Copies `rows` rows of width_bytes between device buffers with row pitches (bytes):
+ * the Split that Fusion.matmuls/2 puts after a merged matmul (lib/transmuter/fusion.ex:
+ * 495-507) takes column ranges of the merged output this way. Asynchronous. */
+int tmh_copy_2d(tmh_ctx* ctx, void* d_dst, size_t dst_pitch, const void* d_src, size_t src_pitch,
+                size_t width_bytes, size_t rows, void* stream);
+
 /* Blocks until the stream (NULL: the context's) has finished its work. */
 int tmh_synchronize(tmh_ctx* ctx, void* stream);
 
@@ -144,6 +150,16 @@ int tmh_pack_nbits_host(const uint8_t* h_b, size_t b_bytes, const void* h_scales
                         size_t zp_count, int64_t K, int64_t N, int bits, int block_size,
                         int weight_dtype, void* h_q, size_t* q_bytes, void* h_scale,
                         size_t* scale_bytes, void* h_zero, size_t* zero_bytes);
+
+/*
+ * One weight whose rows are the rows of parts[0], then parts[1], ...: the packed form of the
+ * weight concatenation of Fusion.matmuls/2 (lib/transmuter/fusion.ex:430-539), which merges
+ * the MatMulNBits that read one input (q/k/v, gate/up) into one matmul over [sum N, K]. The
+ * parts must share K, bits, block_size, weight type and zero point kind; 1 <= count <= 8.
+ * The parts stay valid (the caller frees them). Synchronous on the context's stream.
+ */
+int tmh_weight_concat_nbits(tmh_ctx* ctx, const tmh_weight* const* parts, int count,
+                            tmh_weight** out);
 
 /* K, N, bits, block_size, the weight type and the device bytes the weight holds. */
 int tmh_weight_info(const tmh_weight* w, int64_t* K, int64_t* N, int* bits, int* block_size,

@@ -41,6 +41,8 @@ SIGNATURES = {
     "tmh_upload": (_i, [_vp, _vp, _vp, _sz]),
     "tmh_download": (_i, [_vp, _vp, _vp, _sz]),
     "tmh_synchronize": (_i, [_vp, _vp]),
+    "tmh_copy_2d": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _vp]),
+    "tmh_weight_concat_nbits": (_i, [_vp, ctypes.POINTER(_vp), _i, ctypes.POINTER(_vp)]),
     "tmh_event_create": (_i, [_vp, ctypes.POINTER(_vp)]),
     "tmh_event_destroy": (_i, [_vp, _vp]),
     "tmh_event_record": (_i, [_vp, _vp, _vp]),

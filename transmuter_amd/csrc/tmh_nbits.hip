@@ -26,6 +26,7 @@ using namespace tmh;
 namespace {
 
 constexpr int kWaves = 4;
+constexpr int kMaxConcat = 8;
 constexpr int kThreads = 64 * kWaves;
 
 int ilog2(int v) {
@@ -186,9 +187,9 @@ __device__ __forceinline__ void load_params(const uint16_t* __restrict__ sc,
   zz = __builtin_bit_cast(half2_t, z | (z << 16));
 }
 
-// Adds the partial sums of the four wavefronts and writes rows m0.. of one 16-column tile.
+// Adds the partial sums of the block's wavefronts and writes rows m0.. of one 16-column tile.
 template <int MT>
-__device__ __forceinline__ void gemv_epilogue(float4_t (&acc)[MT], float4_t* red, int64_t t,
+__device__ __forceinline__ void gemv_epilogue(float4_t (&acc)[MT], float4_t* red, int nwaves, int64_t t,
                                               int64_t m0, int64_t M, int64_t N,
                                               const void* __restrict__ bias, int bias_dt,
                                               void* __restrict__ Y, int y_dt, int dot_dt,
@@ -197,11 +198,10 @@ __device__ __forceinline__ void gemv_epilogue(float4_t (&acc)[MT], float4_t* red
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) red[(wave * MT + mt) * 64 + lane] = acc[mt];
   __syncthreads();
-  // Wave w finishes m-tiles w, w+4, ...
-  for (int mt = wave; mt < MT; mt += kWaves) {
-    float4_t s = red[(0 * MT + mt) * 64 + lane];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) s += red[(w * MT + mt) * 64 + lane];
+  // Wave w finishes m-tiles w, w + nwaves, ...
+  for (int mt = wave; mt < MT; mt += nwaves) {
+    float4_t s = red[mt * 64 + lane];
+    for (int w = 1; w < nwaves; ++w) s += red[(w * MT + mt) * 64 + lane];
     const int64_t n = t * 16 + (lane & 15);
     if (n >= N) continue;
     const float b = bias ? load_float_rt(bias, bias_dt, n) : 0.0f;
@@ -217,45 +217,88 @@ __device__ __forceinline__ void gemv_epilogue(float4_t (&acc)[MT], float4_t* red
   }
 }
 
-template <int BITS, int MT, bool HAS_ZP, bool SPLIT>
-__global__ __launch_bounds__(256) void k_gemv_f16(
+// Eight f16 values of A row m at columns k..k+7 when A rows are 16-byte aligned and K is a
+// multiple of 8: one unconditional 16-byte load (of row 0 when out of range, then zeroed), so
+// the loads of a round can all issue before the first one is used.
+__device__ __forceinline__ half8_t load_a8_fast(const _Float16* __restrict__ A, int64_t m, int64_t M,
+                                                int64_t k, int64_t K, int64_t lda) {
+  const bool ok = m < M && k < K;
+  const half8_t v = *reinterpret_cast<const half8_t*>(A + (ok ? m * lda + k : 0));
+  return ok ? v : half8_t{};
+}
+
+// One workgroup per 16-column tile (and per 16*MT rows of A). Its nwaves = blockDim.x / 64
+// wavefronts split K: wave w takes chunks w*U .. w*U+U-1, then w*U + nwaves*U.., and issues
+// the U weight loads of a round, their parameters and (a_fast) their A fragments together,
+// so a small GEMV has its whole weight in flight at once instead of one chunk per latency.
+template <int BITS, int MT, bool HAS_ZP, bool SPLIT, int U>
+__global__ __launch_bounds__(1024) void k_gemv_f16(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
-    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, bool a_vec,
+    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, bool a_fast,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt,
     int64_t ldy, int64_t N, int64_t nchunks, int nbc, int bsc_shift) {
   constexpr int CW = 512 / BITS;
   constexpr int GW = CW / 4;
   constexpr int STEPS = GW / 8;
-  __shared__ float4_t red[kWaves * MT * 64];
+  constexpr bool HOIST = MT * U * STEPS <= 16;
+  extern __shared__ float4_t red[];
+  const int nwaves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int64_t t = blockIdx.x;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 16 * MT;
-  const int64_t per = (nchunks + kWaves - 1) / kWaves;
-  const int64_t c0 = wave * per;
-  const int64_t c1 = c0 + per < nchunks ? c0 + per : nchunks;
   float4_t acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  for (int64_t c = c0; c < c1; ++c) {
-    const int64_t tc = t * nchunks + c;
-    const uint4_t w = qt[tc * 64 + lane];
-    const int64_t kbase = c * CW + g * GW;
-    half2_t ss, zz;
-    if constexpr (!SPLIT) load_params<HAS_ZP, BITS>(sc, zp, (tc * nbc + ((g * GW) >> bsc_shift)) * 16 + r, ss, zz);
+  for (int64_t base = static_cast<int64_t>(wave) * U; base < nchunks; base += static_cast<int64_t>(nwaves) * U) {
+    uint4_t w[U];
+    half2_t ss[U], zz[U];
 #pragma unroll
-    for (int i = 0; i < STEPS; ++i) {
-      if constexpr (SPLIT)
-        load_params<HAS_ZP, BITS>(sc, zp, (tc * nbc + ((g * GW + 8 * i) >> bsc_shift)) * 16 + r, ss, zz);
-      const half8_t b = unpack_step<BITS>(w, i, zz, ss);
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = base + u < nchunks ? base + u : nchunks - 1;
+      w[u] = qt[(t * nchunks + c) * 64 + lane];
+      if constexpr (!SPLIT)
+        load_params<HAS_ZP, BITS>(sc, zp, ((t * nchunks + c) * nbc + ((g * GW) >> bsc_shift)) * 16 + r, ss[u], zz[u]);
+    }
+    half8_t af[HOIST ? U : 1][HOIST ? STEPS : 1][HOIST ? MT : 1];
+    if constexpr (HOIST) {
+      if (a_fast) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const half8_t a = load_a8(A, m0 + mt * 16 + r, M, kbase + 8 * i, K, lda, a_vec);
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[mt], 0, 0, 0);
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int i = 0; i < STEPS; ++i)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              af[u][i][mt] = load_a8_fast(A, m0 + mt * 16 + r, M, (base + u) * CW + g * GW + 8 * i,
+                                          base + u < nchunks ? K : 0, lda);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = base + u;
+      if (c >= nchunks) break;
+      const int64_t kbase = c * CW + g * GW;
+#pragma unroll
+      for (int i = 0; i < STEPS; ++i) {
+        if constexpr (SPLIT)
+          load_params<HAS_ZP, BITS>(sc, zp, ((t * nchunks + c) * nbc + ((g * GW + 8 * i) >> bsc_shift)) * 16 + r,
+                                    ss[u], zz[u]);
+        const half8_t b = unpack_step<BITS>(w[u], i, zz[u], ss[u]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          half8_t a;
+          if constexpr (HOIST) {
+            a = a_fast ? af[u][i][mt] : load_a8(A, m0 + mt * 16 + r, M, kbase + 8 * i, K, lda, false);
+          } else {
+            a = a_fast ? load_a8_fast(A, m0 + mt * 16 + r, M, kbase + 8 * i, K, lda)
+                       : load_a8(A, m0 + mt * 16 + r, M, kbase + 8 * i, K, lda, false);
+          }
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[mt], 0, 0, 0);
+        }
       }
     }
   }
-  gemv_epilogue<MT>(acc, red, t, m0, M, N, bias, bias_dt, Y, y_dt, dot_dt, ldy);
+  gemv_epilogue<MT>(acc, red, nwaves, t, m0, M, N, bias, bias_dt, Y, y_dt, dot_dt, ldy);
 }
 
 // 128 x 128 output tile per workgroup: wave (wm, wn) computes rows 64*wm.. and columns
@@ -457,15 +500,30 @@ int bsc_shift_of(const tmh_weight* w) {
 // True when a lane's k-group of one chunk spans more than one block (parameters per step).
 bool split_params(const tmh_weight* w) { return w->block_size < chunk_weights(w->bits) / 4; }
 
-template <int BITS, int MT, bool HAS_ZP, bool SPLIT>
-void launch_gemv(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+template <int BITS, int MT, bool HAS_ZP, bool SPLIT, int U>
+void launch_gemv_u(const tmh_weight* w, const MatArgs& a, hipStream_t s, int waves) {
   const int64_t mblocks = (a.M + 16 * MT - 1) / (16 * MT);
   const dim3 grid(static_cast<unsigned>(w->ntiles), static_cast<unsigned>(mblocks));
-  k_gemv_f16<BITS, MT, HAS_ZP, SPLIT><<<grid, kThreads, 0, s>>>(
+  const size_t lds = static_cast<size_t>(waves) * MT * 64 * sizeof(float4_t);
+  k_gemv_f16<BITS, MT, HAS_ZP, SPLIT, U><<<grid, 64 * waves, lds, s>>>(
       reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
       static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda,
       a.a_vec, a.bias, a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->nchunks, w->nbc,
       bsc_shift_of(w));
+}
+
+// Chunks per wavefront round (U) and wavefronts per block: up to 16 wavefronts, each with
+// 1, 2 or 4 chunk loads in flight, so that K of up to 64 chunks needs one round.
+template <int BITS, int MT, bool HAS_ZP, bool SPLIT>
+void launch_gemv(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  const int64_t c = w->nchunks;
+  if (c <= 16) {
+    launch_gemv_u<BITS, MT, HAS_ZP, SPLIT, 1>(w, a, s, static_cast<int>(c));
+  } else if (c <= 32) {
+    launch_gemv_u<BITS, MT, HAS_ZP, SPLIT, 2>(w, a, s, static_cast<int>((c + 1) / 2));
+  } else {
+    launch_gemv_u<BITS, MT, HAS_ZP, SPLIT, 4>(w, a, s, static_cast<int>(std::min<int64_t>(16, (c + 3) / 4)));
+  }
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
@@ -648,6 +706,51 @@ void fill_nbits(const PackPlan& p, const uint8_t* h_b, const void* h_scales, con
   }
 }
 
+
+// Concatenation of packed weights along N: output lane-slot (t, c, l) holds row n = 16t + l%16,
+// taken from the part that owns n (its local row n - first[p]), same chunk and k-group.
+struct ConcatParts {
+  const uint8_t* q[kMaxConcat];
+  const uint8_t* scale[kMaxConcat];
+  const uint8_t* zero[kMaxConcat];
+  int64_t first[kMaxConcat + 1];  // first row of each part; first[count] = total N
+  int count;
+};
+
+__global__ __launch_bounds__(256) void k_concat_tiles(ConcatParts parts, uint8_t* __restrict__ q,
+                                                      uint8_t* __restrict__ scale, uint8_t* __restrict__ zero,
+                                                      int64_t nchunks, int nbc, int scale_bytes, int zero_bytes,
+                                                      int64_t lanes_total) {
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= lanes_total) return;
+  const int lane = static_cast<int>(id & 63);
+  const int64_t tc = id >> 6;
+  const int64_t t = tc / nchunks;
+  const int64_t c = tc - t * nchunks;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t n = t * 16 + r;
+  int p = 0;
+  while (p + 1 < parts.count && n >= parts.first[p + 1]) ++p;
+  const bool valid = n < parts.first[parts.count];
+  const int64_t ln = n - parts.first[p];
+  const int64_t st = ln >> 4;
+  const int sr = static_cast<int>(ln & 15);
+  const int64_t src_tc = st * nchunks + c;
+  uint4_t v = {0u, 0u, 0u, 0u};
+  if (valid) v = reinterpret_cast<const uint4_t*>(parts.q[p])[src_tc * 64 + 16 * g + sr];
+  reinterpret_cast<uint4_t*>(q)[id] = v;
+  // Parameters: slot (t, c, j, r) for j < nbc, written by the lanes with g == 0.
+  if (g != 0) return;
+  for (int j = 0; j < nbc; ++j) {
+    const int64_t dst = (tc * nbc + j) * 16 + r;
+    const int64_t src = (src_tc * nbc + j) * 16 + sr;
+    for (int b = 0; b < scale_bytes; ++b)
+      scale[dst * scale_bytes + b] = valid ? parts.scale[p][src * scale_bytes + b] : 0;
+    for (int b = 0; b < zero_bytes; ++b)
+      zero[dst * zero_bytes + b] = valid ? parts.zero[p][src * zero_bytes + b] : 0;
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -734,6 +837,67 @@ void tmh_weight_free(tmh_weight* w) {
   delete w;
 }
 
+int tmh_weight_concat_nbits(tmh_ctx* ctx, const tmh_weight* const* parts, int count, tmh_weight** out) {
+  TMH_TRY(use_device(ctx));
+  if (!out) return fail(ctx, TMH_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  if (!parts || count < 1 || count > kMaxConcat)
+    return fail(ctx, TMH_ERR_INVALID, "concatenation takes 1 to %d weights, got %d", kMaxConcat, count);
+  const tmh_weight* w0 = parts[0];
+  if (!w0) return fail(ctx, TMH_ERR_INVALID, "weight 0 is NULL");
+  ConcatParts cp{};
+  cp.count = count;
+  int64_t total = 0;
+  for (int i = 0; i < count; ++i) {
+    const tmh_weight* w = parts[i];
+    if (!w) return fail(ctx, TMH_ERR_INVALID, "weight %d is NULL", i);
+    if (w->device != ctx->device) return fail(ctx, TMH_ERR_INVALID, "weight %d lives on device %d", i, w->device);
+    if (w->K != w0->K || w->bits != w0->bits || w->block_size != w0->block_size || w->wdtype != w0->wdtype ||
+        w->zp_kind != w0->zp_kind)
+      return fail(ctx, TMH_ERR_INVALID,
+                  "weight %d differs from weight 0 in K, bits, block_size, weight type or zero point kind", i);
+    cp.q[i] = w->d_q;
+    cp.scale[i] = static_cast<const uint8_t*>(w->d_scale);
+    cp.zero[i] = static_cast<const uint8_t*>(w->d_zero);
+    cp.first[i] = total;
+    total += w->N;
+  }
+  cp.first[count] = total;
+  if (total > (int64_t(1) << 31)) return fail(ctx, TMH_ERR_INVALID, "the concatenated N is too large");
+  tmh_weight* w = new tmh_weight(*w0);
+  w->d_q = nullptr;
+  w->d_scale = nullptr;
+  w->d_zero = nullptr;
+  w->N = total;
+  w->ntiles = (total + kTileRows - 1) / kTileRows;
+  const int64_t n_params = w->ntiles * w->nchunks * w->nbc * 16;
+  const int scale_bytes = dtype_size(w->wdtype);
+  const int zero_bytes = w->zp_kind == TMH_ZP_PACKED ? 1 : w->zp_kind == TMH_ZP_FLOAT ? 4 : 0;
+  const size_t qb = static_cast<size_t>(w->ntiles * w->nchunks * 1024);
+  const size_t sb = static_cast<size_t>(n_params * scale_bytes);
+  const size_t zb = static_cast<size_t>(n_params * zero_bytes);
+  int st = check_hip(ctx, hipMalloc(reinterpret_cast<void**>(&w->d_q), qb), "hipMalloc (weight)");
+  if (st == TMH_OK) st = check_hip(ctx, hipMalloc(&w->d_scale, sb), "hipMalloc (weight)");
+  if (st == TMH_OK && zb) st = check_hip(ctx, hipMalloc(&w->d_zero, zb), "hipMalloc (weight)");
+  if (st != TMH_OK) {
+    tmh_weight_free(w);
+    return st;
+  }
+  const int64_t lanes = w->ntiles * w->nchunks * 64;
+  k_concat_tiles<<<static_cast<unsigned>((lanes + 255) / 256), 256, 0, ctx->stream>>>(
+      cp, w->d_q, static_cast<uint8_t*>(w->d_scale), static_cast<uint8_t*>(w->d_zero), w->nchunks, w->nbc,
+      scale_bytes, zero_bytes, lanes);
+  st = check_launch(ctx, "k_concat_tiles");
+  if (st == TMH_OK) st = check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (st != TMH_OK) {
+    tmh_weight_free(w);
+    return st;
+  }
+  w->device_bytes = qb + sb + zb;
+  *out = w;
+  return TMH_OK;
+}
+
 int tmh_weight_info(const tmh_weight* w, int64_t* K, int64_t* N, int* bits, int* block_size,
                     int* weight_dtype, size_t* device_bytes) {
   if (!w) return fail(nullptr, TMH_ERR_INVALID, "the weight is NULL");
@@ -784,7 +948,8 @@ int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_d
   if (!d_a || !d_y) return fail(ctx, TMH_ERR_INVALID, "A and Y must not be NULL");
   if (M > (int64_t(1) << 31) / 2) return fail(ctx, TMH_ERR_INVALID, "M is too large");
   hipStream_t s = pick_stream(ctx, stream);
-  MatArgs a{d_a, a_dtype, M, lda, (reinterpret_cast<uintptr_t>(d_a) % 16 == 0) && (lda % 8 == 0),
+  MatArgs a{d_a, a_dtype, M, lda,
+            (reinterpret_cast<uintptr_t>(d_a) % 16 == 0) && (lda % 8 == 0) && (w->K % 8 == 0),
             d_bias, bias_dtype, d_y, y_dtype, dot_dt, ldy};
   const bool fast = a_dtype == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT;
   if (fast) {

@@ -180,6 +180,19 @@ int tmh_download(tmh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes) {
   return check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
 }
 
+int tmh_copy_2d(tmh_ctx* ctx, void* d_dst, size_t dst_pitch, const void* d_src, size_t src_pitch,
+                size_t width_bytes, size_t rows, void* stream) {
+  TMH_TRY(use_device(ctx));
+  if (width_bytes == 0 || rows == 0) return TMH_OK;
+  if (!d_dst || !d_src) return fail(ctx, TMH_ERR_INVALID, "tmh_copy_2d: NULL pointer");
+  if (dst_pitch < width_bytes || src_pitch < width_bytes)
+    return fail(ctx, TMH_ERR_INVALID, "tmh_copy_2d: a pitch is below the row width");
+  return check_hip(ctx,
+                   hipMemcpy2DAsync(d_dst, dst_pitch, d_src, src_pitch, width_bytes, rows, hipMemcpyDeviceToDevice,
+                                    pick_stream(ctx, stream)),
+                   "hipMemcpy2DAsync");
+}
+
 int tmh_synchronize(tmh_ctx* ctx, void* stream) {
   TMH_TRY(use_device(ctx));
   return check_hip(ctx, hipStreamSynchronize(pick_stream(ctx, stream)), "hipStreamSynchronize");

@@ -137,4 +137,118 @@ def move(model: Model, ctx: Context) -> Model:
     params = {name: value for name, value in model.params.items() if name not in freed}
     params.update(weights)
     static = {name: value for name, value in model.static.items() if name not in freed}
-    return replace(model, nodes=nodes, params=params, static=static, backend=ctx)
+    # move/2 ends with Fusion.matmuls/2 (lib/transmuter.ex:1181).
+    return merge_matmuls(replace(model, nodes=nodes, params=params, static=static, backend=ctx))
+
+
+# ---------------------------------------------------------------- merged matmuls
+
+
+def _mergeable(node, model: Model, uses) -> bool:
+    """`Fusion.mergeable?/3` (lib/transmuter/fusion.ex:467-476) for packed MatMulNBits: a
+    non-empty input A, no other inputs (no bias), and an {N, K} packed weight read once."""
+    if node.op_type != "MatMulNBits" or len(node.input) < 2:
+        return False
+    a, w, *rest = node.input
+    weight = model.params.get(w)
+    k, n, _bits, _block = nbits_sizes(node)
+    return a != "" and all(x == "" for x in rest) and uses.get(w, 0) == 1 \
+        and isinstance(weight, PackedWeight) and weight.shape == (n, k)
+
+
+def merge_matmuls(model: Model) -> Model:
+    """`Fusion.matmuls/2` (lib/transmuter/fusion.ex:430-539) on this backend: the MatMulNBits
+    nodes that read one input merge into one MatMulNBits over the concatenated packed weights
+    (rows of the first, then the next, ...) and a Split of its output along the last axis.
+    The merged node keeps the first node's name and reads "<first B>:merged"."""
+    from collections import Counter
+
+    from .onnx_wire import ATTR_INT, ATTR_INTS, AttributeProto, NodeProto
+
+    uses = Counter(name for node in model.nodes for name in node.input)
+    uses.update(model.outputs)
+    groups: dict = {}
+    for node in model.nodes:
+        if _mergeable(node, model, uses):
+            weight = model.params[node.input[1]]
+            key = (node.op_type, node.input[0], weight.dtype, weight.k)
+            groups.setdefault(key, []).append(node)
+    params = dict(model.params)
+    replacements = {}
+    for group in groups.values():
+        if len(group) < 2:
+            continue
+        first = group[0]
+        weights = [params[node.input[1]] for node in group]
+        sizes = [w.n for w in weights]
+        name = first.input[1] + ":merged"
+        output = first.output[0] + ":merged"
+        if name in params:
+            raise ValueError(f"the model already has a param {name}")
+        attrs = [replace(a, i=sum(sizes)) if a.name == "N" else a for a in first.attribute]
+        merged = replace(first, input=[first.input[0], name, *first.input[2:]], output=[output], attribute=attrs)
+        split = NodeProto(op_type="Split", name=f"{first.name}:split", input=[output],
+                          output=[node.output[0] for node in group],
+                          attribute=[AttributeProto(name="axis", type=ATTR_INT, i=-1),
+                                     AttributeProto(name="split", type=ATTR_INTS, ints=list(sizes))])
+        for node in group:
+            params.pop(node.input[1])
+        params[name] = evaluate(PackedWeight.concat(weights))
+        replacements[id(first)] = [merged, split]
+        for node in group[1:]:
+            replacements[id(node)] = []
+    nodes = []
+    for node in model.nodes:
+        nodes.extend(replacements.get(id(node), [node]))
+    return replace(model, nodes=nodes, params=params)
+
+
+def split_last_axis(x: DeviceTensor, sizes: list[int]) -> list[DeviceTensor]:
+    """`Split` along the last axis on the device (tmh_copy_2d per part)."""
+    from ._lib import lib
+    from .device import NX_TO_NUMPY
+
+    total = x.shape[-1]
+    if sum(sizes) != total:
+        raise ValueError(f"split sizes {sizes} do not add up to {total}")
+    rows = x.size // total if total else 0
+    item = np.dtype(NX_TO_NUMPY[x.dtype]).itemsize
+    outs, offset = [], 0
+    for size in sizes:
+        out = x.ctx.empty(x.shape[:-1] + (size,), x.dtype)
+        if size and rows:
+            src = ctypes_offset(x.ptr, offset * item)
+            x.ctx.check(lib().tmh_copy_2d(x.ctx.handle, out.ptr, size * item, src, total * item, size * item, rows, None))
+        outs.append(out)
+        offset += size
+    return outs
+
+
+def ctypes_offset(ptr, nbytes: int):
+    import ctypes
+
+    return ctypes.c_void_p(ptr.value + nbytes)
+
+
+def run_nodes(model: Model, inputs: dict) -> dict:
+    """Walks the nodes in order, as `Transmuter.run_nodes/3` does (lib/transmuter.ex:647-684),
+    for graphs of this path: the quantized operators and the Splits of merged matmuls. Returns
+    every value the graph outputs name."""
+    from . import quantized
+
+    values = {**model.static, **model.params, **inputs}
+    for node in model.nodes:
+        args = [values[name] if name else None for name in node.input]
+        if node.op_type in quantized.op_types():
+            outs = quantized.apply(node, args)
+        elif node.op_type == "Split":
+            split = next(a for a in node.attribute if a.name == "split")
+            axis = next(a for a in node.attribute if a.name == "axis").i
+            if axis not in (-1, len(args[0].shape) - 1):
+                raise NotImplementedError("only Splits along the last axis run here")
+            outs = split_last_axis(args[0], list(split.ints))
+        else:
+            raise NotImplementedError(f"{node.op_type} stays on the Nx backend")
+        for name, value in zip(node.output, outs):
+            values[name] = value
+    return {name: values[name] for name in model.outputs}

@@ -72,6 +72,19 @@ class PackedWeight:
         ctx.check(status)
         return cls(ctx, handle, k, n, bits, block_size, weight_dtype)
 
+    @classmethod
+    def concat(cls, parts: list["PackedWeight"]) -> "PackedWeight":
+        """One weight with the rows of every part in order (tmh_weight_concat_nbits): the
+        concatenation of Fusion.matmuls/2 (lib/transmuter/fusion.ex:430-539), kept packed."""
+        if not parts:
+            raise ValueError("nothing to concatenate")
+        ctx = parts[0].ctx
+        handles = (ctypes.c_void_p * len(parts))(*[p.handle.value for p in parts])
+        handle = ctypes.c_void_p()
+        ctx.check(lib().tmh_weight_concat_nbits(ctx.handle, handles, len(parts), ctypes.byref(handle)))
+        p0 = parts[0]
+        return cls(ctx, handle, p0.k, sum(p.n for p in parts), p0.bits, p0.block_size, p0.dtype)
+
     def device_bytes(self) -> int:
         size = ctypes.c_size_t()
         _lib.check(lib().tmh_weight_info(self.handle, None, None, None, None, None, ctypes.byref(size)))
