@@ -376,6 +376,210 @@ __global__ __launch_bounds__(256) void k_gemm_f16(
   }
 }
 
+// Raw buffer resource over `bytes` bytes: a load whose VGPR offset is at or beyond `bytes`
+// returns zeros, so tiles past N need no address clamps or selects. Every in-range access of
+// these kernels stays inside its buffer.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// Prefill GEMM: 256 x 128 output tile per workgroup of four wavefronts, k-blocks of one
+// chunk (CW weights).
+//  - A: the k-block's 256 rows x CW f16 go global -> LDS by buffer_load ... lds (no VGPRs),
+//    double buffered, rows of CW*2 bytes whose 16-byte pieces are XOR-swizzled by row so the
+//    MFMA fragment reads of 16 rows hit distinct banks. Rows past M read row M-1 (their outputs
+//    are never stored). A partial last k-block goes through registers and is zeroed past K.
+//  - B: wavefront (wm, wn) computes rows 128*wm.. and columns 64*wn..; its four 16-column
+//    weight tiles and their scales and zero points are loaded one k-block ahead and dequantized
+//    in registers (exact f16), each fragment feeding eight v_mfma_f32_16x16x32_f16.
+constexpr int kGemmBM = 256;
+constexpr int kGemmBN = 128;
+
+template <int BITS>
+constexpr size_t gemm_lds_bytes() {
+  return 2 * static_cast<size_t>(kGemmBM) * (512 / BITS) * 2;
+}
+
+// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (buffer_load_dwordx4
+// ... lds: the data never passes through VGPRs). `lds` must be wavefront-uniform. The body
+// exists in the device pass only; the host pass of hipcc does not accept LDS address spaces.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, uint32_t voffset,
+                                          uint32_t soffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds), 16, voffset,
+                                           soffset, 0, 0);
+#endif
+}
+
+// Slot of 16-byte piece `piece` in LDS row `row` (q4 rows hold 16 pieces, q8 rows 8).
+template <int BITS>
+__device__ __forceinline__ int a_slot(int row, int piece) {
+  return BITS == 8 ? (piece ^ ((row >> 1) & 7)) : (piece ^ (row & 15));
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemm_lds(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
+    int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
+    int64_t nchunks, int nbc, int bsc_shift, int mblocks) {
+  constexpr int CW = 512 / BITS;
+  constexpr int GW = CW / 4;
+  constexpr int STEPS = GW / 8;
+  constexpr int ROWB = CW * 2;           // bytes per LDS row
+  constexpr int PPR = CW / 8;            // 16-byte pieces per row
+  constexpr int RPI = 64 / PPR;          // rows per wavefront load instruction
+  constexpr int LOADS = 64 / RPI;        // load instructions per wavefront per k-block (64 rows)
+  constexpr int NJ = SPLIT ? STEPS : 1;  // parameter entries per tile per k-block
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  // Consecutive workgroups take the m-blocks of one n-block, so each XCD keeps one m-block's
+  // A rows in its L2 while the weights stream past.
+  const int mb = static_cast<int>(blockIdx.x % static_cast<unsigned>(mblocks));
+  const int nb = static_cast<int>(blockIdx.x / static_cast<unsigned>(mblocks));
+  const int m0 = mb * kGemmBM;
+  const int t0 = nb * (kGemmBN / 16) + wn * 4;
+  const uint32_t nch = static_cast<uint32_t>(nchunks);
+
+  const auto a_rsrc = buffer_rsrc(A, static_cast<uint32_t>(M * lda * 2));
+  const auto q_rsrc = buffer_rsrc(qt, static_cast<uint32_t>(ntiles * nchunks * 1024));
+  const uint32_t n_params = static_cast<uint32_t>(ntiles * nchunks * nbc * 16);
+  const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+
+  // A loads of this wavefront: rows wave*64 + s*RPI + lane/PPR, LDS slot lane%PPR.
+  const int a_lrow = lane / PPR, a_lslot = lane % PPR;
+  uint32_t a_off[LOADS];
+#pragma unroll
+  for (int s2 = 0; s2 < LOADS; ++s2) {
+    const int row = wave * 64 + s2 * RPI + a_lrow;
+    const int piece = a_slot<BITS>(row, a_lslot);  // the swizzle is its own inverse
+    const int64_t grow = m0 + row < M ? m0 + row : M - 1;
+    a_off[s2] = (static_cast<uint32_t>(grow) * static_cast<uint32_t>(lda) + piece * 8) * 2;
+  }
+  auto load_a = [&](uint32_t kb, int buf) {
+    uint8_t* base = lds + buf * (kGemmBM * ROWB) + wave * 64 * ROWB;
+    if (static_cast<int64_t>(kb + 1) * CW <= K) {
+#pragma unroll
+      for (int s2 = 0; s2 < LOADS; ++s2)
+        lds_dma16(a_rsrc, base + s2 * RPI * ROWB, a_off[s2], kb * (CW * 2));
+    } else {
+      // A k-block that reaches past K: through registers, zero past K. The whole offset is in
+      // the VGPR operand so the buffer range check covers it.
+#pragma unroll
+      for (int s2 = 0; s2 < LOADS; ++s2) {
+        const int row = wave * 64 + s2 * RPI + a_lrow;
+        const int piece = a_slot<BITS>(row, a_lslot);
+        uint4_t v = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off[s2] + kb * (CW * 2), 0, 0);
+        if (static_cast<int64_t>(kb) * CW + piece * 8 >= K) v = uint4_t{0u, 0u, 0u, 0u};
+        *reinterpret_cast<uint4_t*>(base + (s2 * RPI + a_lrow) * ROWB + a_lslot * 16) = v;
+      }
+    }
+  };
+  // This wavefront's four weight tiles and their parameters; tiles past N read zeros.
+  uint32_t b_off[4], p_off[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const uint32_t t = static_cast<uint32_t>(t0 + nt);
+    b_off[nt] = (t * nch * 64 + lane) * 16;
+    p_off[nt] = (t * nch * nbc + ((g * GW) >> bsc_shift)) * 16 + r;
+  }
+  struct BStage {
+    uint4_t w[4];
+    uint32_t s[NJ][4];
+    uint32_t z[NJ][4];
+  };
+  auto load_b = [&](uint32_t kb, BStage& st) {
+    const uint32_t kofs = kb * static_cast<uint32_t>(nbc) * 16;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      st.w[nt] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, b_off[nt], kb * 1024, 0);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        uint32_t e = p_off[nt];
+        if constexpr (SPLIT) e += static_cast<uint32_t>(((g * GW + 8 * j) >> bsc_shift) - ((g * GW) >> bsc_shift)) * 16;
+        st.s[j][nt] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, kofs * 2, 0);
+        if constexpr (HAS_ZP) st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, kofs, 0);
+      }
+    }
+  };
+
+  float4_t acc[8][4];
+#pragma unroll
+  for (int a = 0; a < 8; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf, const BStage& st) {
+    const uint8_t* abase = lds + buf * (kGemmBM * ROWB) + (wm * 128 + r) * ROWB;
+#pragma unroll
+    for (int i = 0; i < STEPS; ++i) {
+      half8_t bf[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int j = SPLIT ? i : 0;
+        const uint32_t sv = st.s[j][nt];
+        const uint32_t zv = HAS_ZP ? 0x6400u + st.z[j][nt] : 0x6400u + (1u << (BITS - 1));
+        bf[nt] = unpack_step<BITS>(st.w[nt], i, __builtin_bit_cast(half2_t, zv | (zv << 16)),
+                                   __builtin_bit_cast(half2_t, sv | (sv << 16)));
+      }
+      const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const half8_t a = *reinterpret_cast<const half8_t*>(abase + mt * 16 * ROWB + slot);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bf[nt], acc[mt][nt], 0, 0, 0);
+      }
+    }
+  };
+
+  BStage cur, next;
+  load_a(0, 0);
+  load_b(0, cur);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (uint32_t kb = 0; kb < nch; ++kb) {
+    const int buf = static_cast<int>(kb & 1);
+    const bool more = kb + 1 < nch;
+    if (more) {
+      load_a(kb + 1, buf ^ 1);
+      load_b(kb + 1, next);
+    }
+    compute(buf, cur);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (more) cur = next;
+  }
+  const bool f16_out = y_dt == DT_F16 && dot_dt == DT_F16 && !bias;
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int64_t n = static_cast<int64_t>(t0 + nt) * 16 + r;
+    if (t0 + nt >= ntiles || n >= N) continue;
+    const float b = bias ? load_float_rt(bias, bias_dt, n) : 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t m = m0 + wm * 128 + mt * 16 + 4 * g + e;
+        if (m >= M) continue;
+        float v = acc[mt][nt][e];
+        if (f16_out) {
+          static_cast<_Float16*>(Y)[m * ldy + n] = static_cast<_Float16>(v);
+          continue;
+        }
+        if (dot_dt == DT_F16) v = round_to<DT_F16>(v);
+        if (bias) v += b;
+        store_float_rt(Y, y_dt, m * ldy + n, v);
+      }
+    }
+  }
+}
+
 // Any float types: the weights dequantize bit-exactly in WDT, then f32 FMA with A.
 // Block (t, y): rows 4*y .. 4*y+3 of A against the 16 columns of tile t.
 constexpr int kGeneralRows = 4;
@@ -537,6 +741,21 @@ void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
+void launch_gemm_lds(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  const int mblocks = static_cast<int>((a.M + kGemmBM - 1) / kGemmBM);
+  const int64_t nblocks = (w->ntiles * 16 + kGemmBN - 1) / kGemmBN;
+  const dim3 grid(static_cast<unsigned>(nblocks * mblocks));
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      static_cast<int>(gemm_lds_bytes<BITS>()));
+  (void)attr;
+  k_gemm_lds<BITS, HAS_ZP, SPLIT><<<grid, 256, gemm_lds_bytes<BITS>(), s>>>(
+      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+      static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
+      a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks);
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_fast_variant(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   if (a.M <= 16) {
     launch_gemv<BITS, 1, HAS_ZP, SPLIT>(w, a, s);
@@ -544,8 +763,13 @@ void launch_fast_variant(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
     launch_gemv<BITS, 2, HAS_ZP, SPLIT>(w, a, s);
   } else if (a.M <= 64 || BITS == 2) {
     launch_gemv<BITS, 4, HAS_ZP, SPLIT>(w, a, s);
-  } else {
-    launch_gemm<BITS, HAS_ZP, SPLIT>(w, a, s);
+  } else if constexpr (BITS != 2) {
+    const bool fits = a.M * a.lda * 2 < (int64_t(1) << 31) &&
+                      w->ntiles * w->nchunks * 1024 + 8 * w->nchunks * 1024 < (int64_t(1) << 31);
+    if (a.a_vec && fits)
+      launch_gemm_lds<BITS, HAS_ZP, SPLIT>(w, a, s);
+    else
+      launch_gemm<BITS, HAS_ZP, SPLIT>(w, a, s);
   }
 }
 
