@@ -80,6 +80,10 @@ MATMUL_CASES = [
     (4, 32, "packed", 128, 16, [1, 5], "f32", "f16", None),
     (8, 16, "packed", 64, 8, [4], "f16", "f32", None),
     (4, 32, "float", 256, 32, [1, 18], "f16", "f16", None),
+    # too few output tiles for the GPU: K splits across workgroups, partial sums reduce
+    (4, 128, "packed", 2048, 2048, [256, 300], "f16", "f16", None),
+    (4, 128, "packed", 2048, 1000, [260], "f16", "f16", "f16"),
+    (8, 64, "none", 1024, 520, [100], "f16", "f16", "f32"),
     # K beyond one round of wavefronts: 86 and 128 chunks per row
     (4, 128, "packed", 11008, 64, [1, 20, 70], "f16", "f16", None),
     (8, 32, "packed", 8192, 24, [1, 33], "f16", "f16", "f16"),

@@ -14,6 +14,8 @@ struct tmh_ctx {
   hipStream_t stream = nullptr;
   std::string error;
   int num_cus = 0;
+  void* ws = nullptr;  // workspace of split-K partial sums, grown on demand outside capture
+  size_t ws_bytes = 0;
 };
 
 // Tiled device layout of a MatMulNBits weight.
@@ -75,6 +77,9 @@ int check_hip(tmh_ctx* ctx, hipError_t err, const char* what);
 hipStream_t pick_stream(tmh_ctx* ctx, void* stream);
 int use_device(tmh_ctx* ctx);
 int check_launch(tmh_ctx* ctx, const char* kernel);
+// The context's workspace of at least `bytes` bytes for work on `stream`, or nullptr when it
+// would have to grow while the stream is being captured into a graph (or cannot grow).
+void* workspace(tmh_ctx* ctx, size_t bytes, hipStream_t stream);
 
 // Host conversions (round to nearest even).
 float f16_to_f32(uint16_t h);

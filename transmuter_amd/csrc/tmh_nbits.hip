@@ -123,6 +123,14 @@ __global__ __launch_bounds__(256) void k_dequant(const uint4_t* __restrict__ qt,
   }
 }
 
+// (x & mask) | orv in one v_and_or_b32: the mask comes from an SGPR and orv from a VGPR, which
+// the one-scalar-operand limit of VOP3 on this target allows (two literals would not).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t orv) {
+  uint32_t out;
+  asm volatile("v_and_or_b32 %0, %1, %2, %3" : "=v"(out) : "v"(x), "s"(mask), "v"(orv));
+  return out;
+}
+
 // Eight exact f16 weights (q - zero) * scale of MFMA step i of a lane, from its 16 bytes.
 // zz holds 1024 + zero (f16, both halves) and ss the scale (both halves); a 16-bit half
 // 0x6400 | q is the f16 number 1024 + q, so (0x6400 | q) - zz is q - zero exactly.
@@ -131,8 +139,9 @@ __device__ __forceinline__ half8_t unpack_step(const uint4_t& w, int i, half2_t 
   uint32_t pr[4];
   if constexpr (BITS == 4) {
     const uint32_t x = w[i];
+    const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pr[j] = ((x >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+    for (int j = 0; j < 4; ++j) pr[j] = and_or(x >> (4 * j), 0x000F000Fu, magic);
   } else if constexpr (BITS == 8) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -423,7 +432,8 @@ __global__ __launch_bounds__(256) void k_gemm_lds(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
     int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
-    int64_t nchunks, int nbc, int bsc_shift, int mblocks) {
+    int64_t nchunks, int nbc, int bsc_shift, int mblocks, int nblocks, int chunks_per_split,
+    float* __restrict__ ws) {
   constexpr int CW = 512 / BITS;
   constexpr int GW = CW / 4;
   constexpr int STEPS = GW / 8;
@@ -439,11 +449,18 @@ __global__ __launch_bounds__(256) void k_gemm_lds(
   const int wm = wave >> 1, wn = wave & 1;
   // Consecutive workgroups take the m-blocks of one n-block, so each XCD keeps one m-block's
   // A rows in its L2 while the weights stream past.
-  const int mb = static_cast<int>(blockIdx.x % static_cast<unsigned>(mblocks));
-  const int nb = static_cast<int>(blockIdx.x / static_cast<unsigned>(mblocks));
+  // With split K (ws != nullptr), workgroup blocks of mblocks*nblocks take consecutive ranges of
+  // chunks_per_split chunks and write f32 partial sums to ws[split][M][N].
+  const unsigned tiles = static_cast<unsigned>(mblocks) * static_cast<unsigned>(nblocks);
+  const int split = static_cast<int>(blockIdx.x / tiles);
+  const unsigned tile = blockIdx.x % tiles;
+  const int mb = static_cast<int>(tile % static_cast<unsigned>(mblocks));
+  const int nb = static_cast<int>(tile / static_cast<unsigned>(mblocks));
   const int m0 = mb * kGemmBM;
   const int t0 = nb * (kGemmBN / 16) + wn * 4;
   const uint32_t nch = static_cast<uint32_t>(nchunks);
+  const uint32_t kb0 = static_cast<uint32_t>(split) * static_cast<uint32_t>(chunks_per_split);
+  const uint32_t kb1 = kb0 + chunks_per_split < nch ? kb0 + chunks_per_split : nch;
 
   const auto a_rsrc = buffer_rsrc(A, static_cast<uint32_t>(M * lda * 2));
   const auto q_rsrc = buffer_rsrc(qt, static_cast<uint32_t>(ntiles * nchunks * 1024));
@@ -514,70 +531,114 @@ __global__ __launch_bounds__(256) void k_gemm_lds(
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
 
+  auto dequant = [&](const BStage& st, int i, half8_t (&bf)[4]) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int j = SPLIT ? i : 0;
+      const uint32_t sv = st.s[j][nt];
+      const uint32_t zv = HAS_ZP ? 0x6400u + st.z[j][nt] : 0x6400u + (1u << (BITS - 1));
+      bf[nt] = unpack_step<BITS>(st.w[nt], i, __builtin_bit_cast(half2_t, zv | (zv << 16)),
+                                 __builtin_bit_cast(half2_t, sv | (sv << 16)));
+    }
+  };
+  // Step i+1's weights dequantize while step i's MFMAs run.
   auto compute = [&](int buf, const BStage& st) {
     const uint8_t* abase = lds + buf * (kGemmBM * ROWB) + (wm * 128 + r) * ROWB;
+    half8_t bf[4], bn[4];
+    dequant(st, 0, bf);
 #pragma unroll
     for (int i = 0; i < STEPS; ++i) {
-      half8_t bf[4];
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int j = SPLIT ? i : 0;
-        const uint32_t sv = st.s[j][nt];
-        const uint32_t zv = HAS_ZP ? 0x6400u + st.z[j][nt] : 0x6400u + (1u << (BITS - 1));
-        bf[nt] = unpack_step<BITS>(st.w[nt], i, __builtin_bit_cast(half2_t, zv | (zv << 16)),
-                                   __builtin_bit_cast(half2_t, sv | (sv << 16)));
-      }
+      if (i + 1 < STEPS) dequant(st, i + 1, bn);
       const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) {
         const half8_t a = *reinterpret_cast<const half8_t*>(abase + mt * 16 * ROWB + slot);
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bf[nt], acc[mt][nt], 0, 0, 0);
+        for (int nt = 0; nt < 4; ++nt)  // weights as the first operand: lane holds 4 columns of one row
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[nt], a, acc[mt][nt], 0, 0, 0);
+      }
+      if (i + 1 < STEPS) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) bf[nt] = bn[nt];
       }
     }
   };
+  // Loads issued after the A tile of a k-block: its weights, scales and zero points. Waiting
+  // until only these are outstanding means the A tile has landed in LDS.
+  constexpr int B_LOADS = 4 + 4 * NJ + (HAS_ZP ? 4 * NJ : 0);
+  constexpr int WAIT_A = (B_LOADS & 15) | (7 << 4) | (15 << 8) | ((B_LOADS >> 4) << 14);
 
   BStage cur, next;
-  load_a(0, 0);
-  load_b(0, cur);
+  load_a(kb0, 0);
+  load_b(kb0, cur);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (uint32_t kb = 0; kb < nch; ++kb) {
-    const int buf = static_cast<int>(kb & 1);
-    const bool more = kb + 1 < nch;
+  for (uint32_t kb = kb0; kb < kb1; ++kb) {
+    const int buf = static_cast<int>((kb - kb0) & 1);
+    const bool more = kb + 1 < kb1;
     if (more) {
       load_a(kb + 1, buf ^ 1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the A loads ahead of the B loads (WAIT_A)
       load_b(kb + 1, next);
     }
     compute(buf, cur);
-    __builtin_amdgcn_s_waitcnt(0);
+    if (more) {
+      __builtin_amdgcn_s_waitcnt(WAIT_A);
+    }
     __syncthreads();
     if (more) cur = next;
   }
+  // Lane (16g + r) holds, for each (mt, nt), row mt*16 + r and the 4 columns nt*16 + 4g ...
   const bool f16_out = y_dt == DT_F16 && dot_dt == DT_F16 && !bias;
+  const bool vec_out = (ldy % 4) == 0;
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int64_t n = static_cast<int64_t>(t0 + nt) * 16 + r;
-    if (t0 + nt >= ntiles || n >= N) continue;
-    const float b = bias ? load_float_rt(bias, bias_dt, n) : 0.0f;
+  for (int mt = 0; mt < 8; ++mt) {
+    const int64_t m = m0 + wm * 128 + mt * 16 + r;
+    if (m >= M) continue;
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t m = m0 + wm * 128 + mt * 16 + 4 * g + e;
-        if (m >= M) continue;
-        float v = acc[mt][nt][e];
-        if (f16_out) {
-          static_cast<_Float16*>(Y)[m * ldy + n] = static_cast<_Float16>(v);
-          continue;
+    for (int nt = 0; nt < 4; ++nt) {
+      const int64_t n = static_cast<int64_t>(t0 + nt) * 16 + 4 * g;
+      if (n >= N) continue;
+      const float4_t v = acc[mt][nt];
+      if (ws) {
+        float* dst = ws + (static_cast<int64_t>(split) * M + m) * N + n;
+        if (n + 4 <= N && (N % 4) == 0) {
+          *reinterpret_cast<float4_t*>(dst) = v;
+        } else {
+          for (int e = 0; e < 4 && n + e < N; ++e) dst[e] = v[e];
         }
-        if (dot_dt == DT_F16) v = round_to<DT_F16>(v);
-        if (bias) v += b;
-        store_float_rt(Y, y_dt, m * ldy + n, v);
+        continue;
+      }
+      if (f16_out && vec_out && n + 4 <= N) {
+        const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
+        const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+        uint32_t pair[2] = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        *reinterpret_cast<uint2*>(static_cast<_Float16*>(Y) + m * ldy + n) = make_uint2(pair[0], pair[1]);
+        continue;
+      }
+      for (int e = 0; e < 4 && n + e < N; ++e) {
+        float x = v[e];
+        if (dot_dt == DT_F16) x = round_to<DT_F16>(x);
+        if (bias) x += load_float_rt(bias, bias_dt, n + e);
+        store_float_rt(Y, y_dt, m * ldy + n + e, x);
       }
     }
   }
+}
+
+// Split-K epilogue: Y = sum over the splits of ws[split][M][N] (in split order), rounded to the
+// dot type, plus the bias, in Y's type.
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits, int64_t M, int64_t N,
+                                                       const void* __restrict__ bias, int bias_dt, void* __restrict__ Y,
+                                                       int y_dt, int dot_dt, int64_t ldy) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i - m * N;
+  float v = ws[i];
+  for (int sp = 1; sp < splits; ++sp) v += ws[sp * M * N + i];
+  if (dot_dt == DT_F16) v = round_to<DT_F16>(v);
+  if (bias) v += load_float_rt(bias, bias_dt, n);
+  store_float_rt(Y, y_dt, m * ldy + n, v);
 }
 
 // Any float types: the weights dequantize bit-exactly in WDT, then f32 FMA with A.
@@ -740,11 +801,31 @@ void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
       bsc_shift_of(w));
 }
 
+// Split K when the output tiles cannot fill the GPU: partial sums go to the context's
+// workspace and k_splitk_reduce adds them. During stream capture the workspace cannot grow,
+// so a capture that finds it too small runs without splitting.
 template <int BITS, bool HAS_ZP, bool SPLIT>
-void launch_gemm_lds(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   const int mblocks = static_cast<int>((a.M + kGemmBM - 1) / kGemmBM);
-  const int64_t nblocks = (w->ntiles * 16 + kGemmBN - 1) / kGemmBN;
-  const dim3 grid(static_cast<unsigned>(nblocks * mblocks));
+  const int nblocks = static_cast<int>((w->ntiles * 16 + kGemmBN - 1) / kGemmBN);
+  const int64_t tiles = static_cast<int64_t>(mblocks) * nblocks;
+  int splits = 1;
+  int cps = static_cast<int>(w->nchunks);
+  const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  if (tiles < cus && w->nchunks >= 4) {
+    splits = static_cast<int>(std::min<int64_t>({8, (cus + tiles - 1) / tiles, w->nchunks / 2}));
+    cps = static_cast<int>((w->nchunks + splits - 1) / splits);
+    splits = static_cast<int>((w->nchunks + cps - 1) / cps);
+  }
+  float* ws = nullptr;
+  if (splits > 1) {
+    ws = static_cast<float*>(workspace(ctx, static_cast<size_t>(splits) * a.M * w->N * sizeof(float), s));
+    if (!ws) {
+      splits = 1;
+      cps = static_cast<int>(w->nchunks);
+    }
+  }
+  const dim3 grid(static_cast<unsigned>(tiles * splits));
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
       static_cast<int>(gemm_lds_bytes<BITS>()));
@@ -752,11 +833,17 @@ void launch_gemm_lds(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   k_gemm_lds<BITS, HAS_ZP, SPLIT><<<grid, 256, gemm_lds_bytes<BITS>(), s>>>(
       reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
       static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
-      a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks);
+      a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
+      nblocks, cps, ws);
+  if (ws) {
+    const int64_t total = a.M * w->N;
+    k_splitk_reduce<<<static_cast<unsigned>((total + 255) / 256), 256, 0, s>>>(
+        ws, splits, a.M, w->N, a.bias, a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy);
+  }
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
-void launch_fast_variant(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+void launch_fast_variant(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   if (a.M <= 16) {
     launch_gemv<BITS, 1, HAS_ZP, SPLIT>(w, a, s);
   } else if (a.M <= 32) {
@@ -767,20 +854,20 @@ void launch_fast_variant(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
     const bool fits = a.M * a.lda * 2 < (int64_t(1) << 31) &&
                       w->ntiles * w->nchunks * 1024 + 8 * w->nchunks * 1024 < (int64_t(1) << 31);
     if (a.a_vec && fits)
-      launch_gemm_lds<BITS, HAS_ZP, SPLIT>(w, a, s);
+      launch_gemm_lds<BITS, HAS_ZP, SPLIT>(ctx, w, a, s);
     else
       launch_gemm<BITS, HAS_ZP, SPLIT>(w, a, s);
   }
 }
 
 template <int BITS>
-void launch_fast_bits(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+void launch_fast_bits(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   const bool zp = w->zp_kind == TMH_ZP_PACKED;
   const bool split = split_params(w);
-  if (zp && split) launch_fast_variant<BITS, true, true>(w, a, s);
-  else if (zp) launch_fast_variant<BITS, true, false>(w, a, s);
-  else if (split) launch_fast_variant<BITS, false, true>(w, a, s);
-  else launch_fast_variant<BITS, false, false>(w, a, s);
+  if (zp && split) launch_fast_variant<BITS, true, true>(ctx, w, a, s);
+  else if (zp) launch_fast_variant<BITS, true, false>(ctx, w, a, s);
+  else if (split) launch_fast_variant<BITS, false, true>(ctx, w, a, s);
+  else launch_fast_variant<BITS, false, false>(ctx, w, a, s);
 }
 
 template <int BITS, int WDT>
@@ -1178,9 +1265,9 @@ int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_d
   const bool fast = a_dtype == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT;
   if (fast) {
     switch (w->bits) {
-      case 2: launch_fast_bits<2>(w, a, s); break;
-      case 4: launch_fast_bits<4>(w, a, s); break;
-      default: launch_fast_bits<8>(w, a, s);
+      case 2: launch_fast_bits<2>(ctx, w, a, s); break;
+      case 4: launch_fast_bits<4>(ctx, w, a, s); break;
+      default: launch_fast_bits<8>(ctx, w, a, s);
     }
     return check_launch(ctx, "k_gemv_f16/k_gemm_f16");
   }

@@ -55,6 +55,34 @@ int check_launch(tmh_ctx* ctx, const char* kernel) {
   return check_hip(ctx, hipGetLastError(), kernel);
 }
 
+void* workspace(tmh_ctx* ctx, size_t bytes, hipStream_t stream) {
+  if (ctx->ws_bytes >= bytes) return ctx->ws;
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &status) != hipSuccess || status != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  // The old workspace may still be read by queued work: wait for the device before freeing it.
+  if (ctx->ws) {
+    if (hipDeviceSynchronize() != hipSuccess || hipFree(ctx->ws) != hipSuccess) {
+      (void)hipGetLastError();
+      ctx->ws = nullptr;
+      ctx->ws_bytes = 0;
+      return nullptr;
+    }
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+  }
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  ctx->ws = p;
+  ctx->ws_bytes = bytes;
+  return p;
+}
+
 float f16_to_f32(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 
 uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
@@ -138,6 +166,7 @@ void tmh_ctx_destroy(tmh_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipStreamDestroy(ctx->stream);
   }
+  if (ctx->ws) (void)hipFree(ctx->ws);
   delete ctx;
 }
 
