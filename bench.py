@@ -214,6 +214,8 @@ def prefill(ctx, reps, ms_list):
         for (name, k, n), w in zip(SMOLLM3_3B, ws):
             a = ctx.put(rng.standard_normal((m, k), dtype=np.float32).astype(np.float16))
             y = ctx.empty((m, n), "f16")
+            matmul_call(ctx, w, a, y, m)  # eager first: sizes the split-K workspace before capture
+            ctx.synchronize()
             g = Graph(ctx, lambda w=w, a=a, y=y: matmul_call(ctx, w, a, y, m))
             ms_total = time_graphs(ctx, [g], reps, 3)
             g.destroy()
@@ -305,6 +307,66 @@ def cpu_baseline(seconds=10.0):
             "ms_per_decode_step_28_layers": elapsed / done * 1e3 * 28 / layers}
 
 
+# ---------------------------------------------------------------- profiling runs
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_gemv_traffic.json")
+COPY_BYTES = 256 << 20
+
+
+def profile_run(ctx, kind, steps):
+    """A short, graph-free run for rocprofv3: `decode` runs the M=1 projection sweep over one
+    weight copy plus one 256 MiB device copy (the calibration of the memory counters);
+    `prefill` runs the SmolLM3-3B projections at M=2048."""
+    global USE_GRAPHS
+    USE_GRAPHS = False
+    if kind == "decode":
+        decode_sweep(ctx, steps, 2, 1, [1])
+        src, dst = ctx.empty((COPY_BYTES,), "u8"), ctx.empty((COPY_BYTES,), "u8")
+        from transmuter_amd._lib import lib
+
+        for _ in range(3):
+            ctx.check(lib().tmh_copy_2d(ctx.handle, dst.ptr, COPY_BYTES, src.ptr, COPY_BYTES, COPY_BYTES, 1, None))
+        ctx.synchronize()
+    else:
+        prefill(ctx, steps, [2048])
+
+
+def summarize(kernel_csv, pmc_dirs):
+    """A markdown summary of rocprofv3 output: per-kernel durations (kernel_stats.csv) and,
+    for --pmc runs (counter_collection.csv), FETCH_SIZE / WRITE_SIZE per dispatch."""
+    import csv
+    import glob
+
+    out = []
+    if kernel_csv:
+        rows = list(csv.DictReader(open(kernel_csv)))
+        out.append("| kernel | calls | avg us | min us | max us | total % |")
+        out.append("|---|---|---|---|---|---|")
+        for r in rows[:12]:
+            out.append(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                       f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f} |")
+    for d in pmc_dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            agg = {}
+            for r in csv.DictReader(open(f)):
+                key = (r["Kernel_Name"][:70], r["Counter_Name"], r["Grid_Size"])
+                agg.setdefault(key, []).append(float(r["Counter_Value"]))
+            out.append("")
+            out.append("| kernel | counter | grid | dispatches | avg KiB per dispatch |")
+            out.append("|---|---|---|---|---|")
+            for (k, c, grid), v in sorted(agg.items()):
+                out.append(f"| `{k}` | {c} | {grid} | {len(v)} | {sum(v) / len(v):.1f} |")
+    return "\n".join(out)
+
+
+def traffic_per_launch():
+    """HBM bytes per decode GEMV launch from the committed counter summary, or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    t = json.load(open(TRAFFIC_FILE))
+    return t.get("hbm_bytes_per_launch")
+
+
 # ---------------------------------------------------------------- main
 
 
@@ -318,17 +380,29 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-graph", action="store_true", help="launch each call on the stream, no HIP graphs")
+    p.add_argument("--profile", choices=["decode", "prefill"], help="a short graph-free run for rocprofv3")
+    p.add_argument("--summarize", nargs="*", metavar="PATH",
+                   help="print a markdown summary of rocprofv3 output: a kernel_stats.csv, then --pmc directories")
     args = p.parse_args()
+    if args.summarize is not None:
+        paths = args.summarize
+        kernel_csv = paths[0] if paths and paths[0].endswith(".csv") else None
+        print(summarize(kernel_csv, paths[1:] if kernel_csv else paths))
+        return
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path runs on one GPU, "
-              "and its multi-GPU sharding is a design in DESIGN.md, not a measured run)", file=sys.stderr)
+              "and its multi-GPU sharding is a design, not a measured run)", file=sys.stderr)
         sys.exit(2)
 
     from transmuter_amd import Context
 
     ctx = Context(0)
+    if args.profile:
+        profile_run(ctx, args.profile, args.steps)
+        ctx.close()
+        return
     ms = [1] if args.quick else [1, 4, 8, 16]
     dec = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms)
     dec_merged = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms, merged=True)
@@ -340,7 +414,7 @@ def main():
     roofline = {
         "bound": "hbm", "kernel": "k_gemv_f16<4,1,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
         "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "traffic": None,
+        "traffic": traffic_per_launch(),
     }
     roofline["frac"] = roofline["achieved"] / HBM_PEAK_GBS
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)

@@ -627,18 +627,35 @@ __global__ __launch_bounds__(256) void k_gemm_lds(
 }
 
 // Split-K epilogue: Y = sum over the splits of ws[split][M][N] (in split order), rounded to the
-// dot type, plus the bias, in Y's type.
+// dot type, plus the bias, in Y's type. Four consecutive outputs per thread.
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits, int64_t M, int64_t N,
                                                        const void* __restrict__ bias, int bias_dt, void* __restrict__ Y,
                                                        int y_dt, int dot_dt, int64_t ldy) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= M * N) return;
-  const int64_t m = i / N, n = i - m * N;
-  float v = ws[i];
-  for (int sp = 1; sp < splits; ++sp) v += ws[sp * M * N + i];
-  if (dot_dt == DT_F16) v = round_to<DT_F16>(v);
-  if (bias) v += load_float_rt(bias, bias_dt, n);
-  store_float_rt(Y, y_dt, m * ldy + n, v);
+  const int64_t i4 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  const int64_t total = M * N;
+  if (i4 >= total) return;
+  const bool vec = (N % 4) == 0;
+  if (vec) {
+    float4_t v = *reinterpret_cast<const float4_t*>(ws + i4);
+    for (int sp = 1; sp < splits; ++sp) v += *reinterpret_cast<const float4_t*>(ws + sp * total + i4);
+    const int64_t m = i4 / N, n = i4 - m * N;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = v[e];
+      if (dot_dt == DT_F16) x = round_to<DT_F16>(x);
+      if (bias) x += load_float_rt(bias, bias_dt, n + e);
+      store_float_rt(Y, y_dt, m * ldy + n + e, x);
+    }
+    return;
+  }
+  for (int64_t i = i4; i < i4 + 4 && i < total; ++i) {
+    float x = ws[i];
+    for (int sp = 1; sp < splits; ++sp) x += ws[sp * total + i];
+    const int64_t m = i / N, n = i - m * N;
+    if (dot_dt == DT_F16) x = round_to<DT_F16>(x);
+    if (bias) x += load_float_rt(bias, bias_dt, n);
+    store_float_rt(Y, y_dt, m * ldy + n, x);
+  }
 }
 
 // Any float types: the weights dequantize bit-exactly in WDT, then f32 FMA with A.
@@ -836,8 +853,8 @@ void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStr
       a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
       nblocks, cps, ws);
   if (ws) {
-    const int64_t total = a.M * w->N;
-    k_splitk_reduce<<<static_cast<unsigned>((total + 255) / 256), 256, 0, s>>>(
+    const int64_t quads = (a.M * w->N + 3) / 4;
+    k_splitk_reduce<<<static_cast<unsigned>((quads + 255) / 256), 256, 0, s>>>(
         ws, splits, a.M, w->N, a.bias, a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy);
   }
 }
