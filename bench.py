@@ -412,7 +412,7 @@ def main():
         extra["large_vocab"] = large_vocab(ctx, 50)
     head = dec[1]
     roofline = {
-        "bound": "hbm", "kernel": "k_gemv_f16<4,1,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
+        "bound": "hbm", "kernel": "k_gemv_lean<4,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
         "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "traffic": traffic_per_launch(),
     }

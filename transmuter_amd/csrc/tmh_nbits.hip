@@ -310,6 +310,91 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(
   gemv_epilogue<MT>(acc, red, nwaves, t, m0, M, N, bias, bias_dt, Y, y_dt, dot_dt, ldy);
 }
 
+// Raw buffer resource over `bytes` bytes: a load whose VGPR offset is at or beyond `bytes`
+// returns zeros, so tiles past N need no address clamps or selects. Every in-range access of
+// these kernels stays inside its buffer.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// Decode GEMV for the common case: M <= 16, f16 A (16-byte aligned rows, K a multiple of 8),
+// f16 weights, f16 Y, no bias. The same split of K over up to 16 wavefronts as k_gemv_f16, with
+// 32-bit buffer addressing (rows of A past M and tiles past N read zeros from the buffer range
+// check), the weights as the MFMA's first operand (a lane ends with 4 consecutive columns of
+// one row) and an LDS reduction read only by the lanes that own rows below M.
+template <int BITS, bool HAS_ZP, bool SPLIT, int U>
+__global__ __launch_bounds__(1024) void k_gemv_lean(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, int M, int K, int lda, _Float16* __restrict__ Y, int ldy, int N, int nchunks,
+    int ntiles, int nbc, int bsc_shift) {
+  constexpr int CW = 512 / BITS;
+  constexpr int GW = CW / 4;
+  constexpr int STEPS = GW / 8;
+  constexpr int NJ = SPLIT ? STEPS : 1;
+  __shared__ float4_t red[16 * 64];
+  const int nwaves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t t = blockIdx.x;
+  const uint32_t nch = static_cast<uint32_t>(nchunks);
+  const uint32_t n_params = static_cast<uint32_t>(ntiles) * nch * nbc * 16;
+  const auto q_rsrc = buffer_rsrc(qt, static_cast<uint32_t>(ntiles) * nch * 1024);
+  const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+  const auto a_rsrc = buffer_rsrc(A, static_cast<uint32_t>(M) * lda * 2);
+  const uint32_t a_row = r < M ? static_cast<uint32_t>(r) * lda * 2 : 0x80000000u;  // outside the range
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (uint32_t base = wave * U; base < nch; base += nwaves * U) {
+    uint4_t w[U];
+    uint32_t sv[U][NJ], zv[U][NJ];
+    half8_t af[U][STEPS];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t c = base + u < nch ? base + u : nch - 1;
+      w[u] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, (t * nch * 64 + lane) * 16, c * 1024, 0);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const uint32_t e = ((t * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
+        sv[u][j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, 0, 0);
+        if constexpr (HAS_ZP) zv[u][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < STEPS; ++i) {
+        const uint32_t k = (base + u) * CW + g * GW + 8 * i;
+        const uint32_t off = (base + u < nch && k < static_cast<uint32_t>(K)) ? a_row + k * 2 : 0x80000000u;
+        af[u][i] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (base + u >= nch) break;
+#pragma unroll
+      for (int i = 0; i < STEPS; ++i) {
+        const int j = SPLIT ? i : 0;
+        const uint32_t zq = HAS_ZP ? 0x6400u + zv[u][j] : 0x6400u + (1u << (BITS - 1));
+        const half8_t b = unpack_step<BITS>(w[u], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
+                                            __builtin_bit_cast(half2_t, sv[u][j] | (sv[u][j] << 16)));
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[u][i], acc, 0, 0, 0);
+      }
+    }
+  }
+  red[wave * 64 + lane] = acc;
+  __syncthreads();
+  if (wave != 0 || r >= M) return;
+  float4_t sum = red[lane];
+  for (int w2 = 1; w2 < nwaves; ++w2) sum += red[w2 * 64 + lane];
+  const int n = static_cast<int>(t) * 16 + 4 * g;
+  _Float16* dst = Y + static_cast<int64_t>(r) * ldy + n;
+  if (n + 4 <= N && (ldy % 4) == 0) {
+    const half2_t lo = {static_cast<_Float16>(sum[0]), static_cast<_Float16>(sum[1])};
+    const half2_t hi = {static_cast<_Float16>(sum[2]), static_cast<_Float16>(sum[3])};
+    *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+  } else {
+    for (int e = 0; e < 4 && n + e < N; ++e) dst[e] = static_cast<_Float16>(sum[e]);
+  }
+}
+
 // 128 x 128 output tile per workgroup: wave (wm, wn) computes rows 64*wm.. and columns
 // 64*wn.. (four 16-row tiles by four 16-column tiles) over all of K.
 template <int BITS, bool HAS_ZP, bool SPLIT>
@@ -383,14 +468,6 @@ __global__ __launch_bounds__(256) void k_gemm_f16(
       }
     }
   }
-}
-
-// Raw buffer resource over `bytes` bytes: a load whose VGPR offset is at or beyond `bytes`
-// returns zeros, so tiles past N need no address clamps or selects. Every in-range access of
-// these kernels stays inside its buffer.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
-                                           0x00020000);
 }
 
 // Prefill GEMM: 256 x 128 output tile per workgroup of four wavefronts, k-blocks of one
@@ -794,11 +871,37 @@ void launch_gemv_u(const tmh_weight* w, const MatArgs& a, hipStream_t s, int wav
       bsc_shift_of(w));
 }
 
+template <int BITS, bool HAS_ZP, bool SPLIT, int U>
+void launch_gemv_lean_u(const tmh_weight* w, const MatArgs& a, hipStream_t s, int waves) {
+  k_gemv_lean<BITS, HAS_ZP, SPLIT, U><<<static_cast<unsigned>(w->ntiles), 64 * waves, 0, s>>>(
+      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+      static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), static_cast<int>(a.M),
+      static_cast<int>(w->K), static_cast<int>(a.lda), static_cast<_Float16*>(a.y), static_cast<int>(a.ldy),
+      static_cast<int>(w->N), static_cast<int>(w->nchunks), static_cast<int>(w->ntiles), w->nbc, bsc_shift_of(w));
+}
+
+// The lean decode GEMV applies: M <= 16, aligned f16 A with K % 8 == 0, f16 Y, no bias, and
+// every buffer addressable with 32-bit byte offsets.
+bool lean_gemv_ok(const tmh_weight* w, const MatArgs& a) {
+  return a.M <= 16 && a.a_vec && a.y_dt == TMH_F16 && a.dot_dt == TMH_F16 && !a.bias &&
+         a.M * a.lda * 2 < (int64_t(1) << 31) && w->ntiles * w->nchunks * 1024 < (int64_t(1) << 31) &&
+         a.ldy < (int64_t(1) << 30) && (reinterpret_cast<uintptr_t>(a.y) & 7) == 0;
+}
+
 // Chunks per wavefront round (U) and wavefronts per block: up to 16 wavefronts, each with
 // 1, 2 or 4 chunk loads in flight, so that K of up to 64 chunks needs one round.
 template <int BITS, int MT, bool HAS_ZP, bool SPLIT>
 void launch_gemv(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   const int64_t c = w->nchunks;
+  if (MT == 1 && lean_gemv_ok(w, a)) {
+    if (c <= 16)
+      launch_gemv_lean_u<BITS, HAS_ZP, SPLIT, 1>(w, a, s, static_cast<int>(c));
+    else if (c <= 32)
+      launch_gemv_lean_u<BITS, HAS_ZP, SPLIT, 2>(w, a, s, static_cast<int>((c + 1) / 2));
+    else
+      launch_gemv_lean_u<BITS, HAS_ZP, SPLIT, 4>(w, a, s, static_cast<int>(std::min<int64_t>(16, (c + 3) / 4)));
+    return;
+  }
   if (c <= 16) {
     launch_gemv_u<BITS, MT, HAS_ZP, SPLIT, 1>(w, a, s, static_cast<int>(c));
   } else if (c <= 32) {
