@@ -88,6 +88,12 @@ MATMUL_CASES = [
     (4, 128, "packed", 11008, 64, [1, 20, 70], "f16", "f16", None),
     (8, 32, "packed", 8192, 24, [1, 33], "f16", "f16", "f16"),
     (2, 32, "packed", 4096, 40, [1, 9], "f16", "f16", None),
+    # more tiles than the GPU holds wavefronts at once: 2 and 4 tiles per workgroup, last group partial
+    (4, 32, "packed", 1024, 16400, [1, 16], "f16", "f16", None),
+    (4, 32, "packed", 1024, 30008, [1, 7, 16], "f16", "f16", None),
+    (8, 128, "none", 256, 50008, [1, 16], "f16", "f16", None),
+    (4, 32, "packed", 4096, 12000, [1, 9], "f16", "f16", None),
+    (4, 16, "packed", 512, 40000, [1, 5], "f16", "f16", None),
 ]
 
 
