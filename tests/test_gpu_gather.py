@@ -1,0 +1,76 @@
+"""GatherBlockQuantized on the GPU against the oracle, bit-exactly, over the kernel's variants:
+4-byte and 1-byte row units, one or several quantization blocks per thread, vector or scalar
+stores; u8 and s8 data; no, packed (u8 / s8) and float zero points; f32, f16 and bf16 scales;
+negative ids (counted from the end). Seeds and shapes are printed before each case."""
+
+import zlib
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from transmuter_amd import quantized
+from transmuter_amd.onnx_wire import ATTR_INT, AttributeProto, NodeProto
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # bits, rows, row_bytes, blocks, data type, zero points, scale type, ids shape
+    (4, 300, 512, 32, "u8", "u8", "f16", (8, 64)),     # bs 32: one block per thread, 16-byte stores
+    (4, 50, 12, 6, "u8", None, "f32", (37,)),          # bs 4: two blocks per thread
+    (4, 40, 10, 5, "u8", "u8", "bf16", (3, 5)),        # odd row bytes: 1-byte units
+    (4, 64, 64, 8, "s8", None, "f16", (20,)),          # signed nibbles, zero point 0
+    (4, 64, 64, 8, "s8", "s8", "bf16", (20,)),         # signed packed zero points
+    (8, 100, 256, 8, "s8", "float", "f32", (2, 33)),   # float zero points, 16-byte f32 stores
+    (8, 30, 12, 3, "u8", "u8", "f16", (11,)),          # rows of 24 bytes out: scalar stores
+    (2, 64, 64, 16, "u8", "u8", "f16", (9, 7)),        # q2, bs 16: 32-byte stores
+    (2, 16, 4, 1, "u8", None, "f32", (5,)),
+]
+
+
+def _scales(rng, shape, dtype):
+    s = (np.abs(rng.standard_normal(shape)) * 0.05 + 1e-3).astype(np.float32)
+    return o.bf16_round(s) if dtype == "bf16" else s.astype(np.float16 if dtype == "f16" else np.float32)
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "b{}_r{}_B{}_blk{}_{}_{}_{}".format(*c[:7]))
+def test_gather_matches_oracle(ctx, case):
+    bits, rows, row_bytes, blocks, dtype, zp, sdt, ids_shape = case
+    print(f"gather {case}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    data = rng.integers(0, 256, (rows, row_bytes), dtype=np.uint8)
+    if dtype == "s8":
+        data = data.view(np.int8)
+    scales = _scales(rng, (rows, blocks), sdt)
+    zrow = -(-blocks * bits // 8)
+    if zp is None:
+        zero = None
+    elif zp == "float":
+        zero = rng.integers(-3, 4, (rows, blocks)).astype(np.float32)
+    else:
+        zero = rng.integers(0, 256, (rows, zrow), dtype=np.uint8)
+        zero = zero.view(np.int8) if zp == "s8" else zero
+    ids = rng.integers(-rows, rows, ids_shape, dtype=np.int64)
+    node = NodeProto(op_type="GatherBlockQuantized", input=["data", "ids", "scales"] + (["zp"] if zp else []),
+                     output=["out"], attribute=[AttributeProto(name="bits", type=ATTR_INT, i=bits)])
+    sc_in = ctx.put(scales, sdt) if sdt == "bf16" else ctx.put(scales)
+    args = [ctx.put(data), ctx.put(ids), sc_in] + ([ctx.put(zero)] if zp else [])
+    got = quantized.apply(node, args)[0].numpy()
+    ref = o.gather_block_quantized(data, ids, scales, zero, bits=bits)  # bf16 as uint16 bits
+    assert got.shape == ids_shape + (row_bytes * 8 // bits,)
+    assert np.array_equal(np.ascontiguousarray(got).view(np.uint8), np.ascontiguousarray(ref).view(np.uint8))
+
+
+def test_gather_vocab_table(ctx):
+    """The tied-embedding lookup of a 151936 x 1024 q4 table, block 32, f16 scales: ids over the
+    whole table, including its first and last rows."""
+    rng = np.random.default_rng(5)
+    rows, d, bs = 151936, 1024, 32
+    data = rng.integers(0, 256, (rows, d // 2), dtype=np.uint8)
+    scales = _scales(rng, (rows, d // bs), "f16")
+    ids = np.concatenate([[0, rows - 1, -1], rng.integers(0, rows, 509)]).astype(np.int64).reshape(2, 256)
+    node = NodeProto(op_type="GatherBlockQuantized", input=["data", "ids", "scales"], output=["out"],
+                     attribute=[AttributeProto(name="bits", type=ATTR_INT, i=4)])
+    got = quantized.apply(node, [ctx.put(data), ctx.put(ids), ctx.put(scales)])[0].numpy()
+    ref = o.gather_block_quantized(data, ids, scales, bits=4)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))

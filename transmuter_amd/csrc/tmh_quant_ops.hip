@@ -18,17 +18,20 @@ namespace {
 
 // Bytes [u*UB, u*UB + UB) of a gathered row, each value dequantized in DT:
 // (q - zero) * scale, q and zero exact small integers, one rounding (packed.ex:28-36).
-template <int DT, int BITS, int UB>
+// ONE_BLOCK: the thread's values share one quantization block (one scale and zero point).
+// VEC_OUT: the values leave as 8- or 16-byte stores.
+template <int DT, int BITS, int UB, bool ONE_BLOCK, bool VEC_OUT>
 __global__ __launch_bounds__(256) void k_gather_bq(
     const uint8_t* __restrict__ data, bool data_signed, int64_t rows, int64_t row_bytes,
-    const void* __restrict__ ids, bool ids64, int64_t n_ids, const void* __restrict__ scales,
+    const void* __restrict__ ids, bool ids64, uint32_t n_ids, const void* __restrict__ scales,
     int64_t blocks, int64_t bs, const void* __restrict__ zp, int zp_dt, int64_t zrow,
-    void* __restrict__ out, int64_t units) {
+    void* __restrict__ out, uint32_t units) {
   constexpr int PER = 8 / BITS;
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  constexpr int V = UB * PER;
+  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
   if (idx >= n_ids * units) return;
-  const int64_t i = idx / units;
-  const int64_t u = idx - i * units;
+  const uint32_t i = idx / units;
+  const uint32_t u = idx - i * units;
   int64_t id = ids64 ? static_cast<const int64_t*>(ids)[i] : static_cast<const int32_t*>(ids)[i];
   if (id < 0) id += rows;  // ONNX: a negative index counts from the end
   id = id < 0 ? 0 : (id >= rows ? rows - 1 : id);
@@ -42,11 +45,34 @@ __global__ __launch_bounds__(256) void k_gather_bq(
     bytes[0] = data[id * row_bytes + u];
   }
   const float zdefault = data_signed ? 0.0f : static_cast<float>(1 << (BITS - 1));
+  auto zero_of = [&](int64_t blk) -> float {
+    if (!zp) return zdefault;
+    if (zp_dt == TMH_U8 || zp_dt == TMH_S8) {
+      const int64_t bit = blk * BITS;
+      const uint8_t zb = static_cast<const uint8_t*>(zp)[id * zrow + bit / 8];
+      int zq;
+      if constexpr (BITS == 8) {
+        zq = zp_dt == TMH_S8 ? static_cast<int>(static_cast<int8_t>(zb)) : static_cast<int>(zb);
+      } else {
+        zq = (zb >> (bit % 8)) & ((1 << BITS) - 1);
+        if (zp_dt == TMH_S8 && zq >= (1 << (BITS - 1))) zq -= (1 << BITS);
+      }
+      return static_cast<float>(zq);
+    }
+    return round_to<DT>(load_float_rt(zp, zp_dt, id * blocks + blk));
+  };
+  const int64_t col0 = static_cast<int64_t>(u) * V;
+  float s = 0.f, z = 0.f;
+  if constexpr (ONE_BLOCK) {
+    const int64_t blk = col0 / bs;
+    s = load_as_f32<DT>(scales, id * blocks + blk);
+    z = zero_of(blk);
+  }
+  float vals[V];
 #pragma unroll
   for (int b = 0; b < UB; ++b) {
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
-      const int64_t col = (u * UB + b) * PER + v;
       int q;
       if constexpr (BITS == 8) {
         q = data_signed ? static_cast<int>(static_cast<int8_t>(bytes[b])) : static_cast<int>(bytes[b]);
@@ -54,42 +80,82 @@ __global__ __launch_bounds__(256) void k_gather_bq(
         q = (bytes[b] >> (v * BITS)) & ((1 << BITS) - 1);
         if (data_signed && q >= (1 << (BITS - 1))) q -= (1 << BITS);
       }
-      const int64_t blk = col / bs;
-      const float s = load_as_f32<DT>(scales, id * blocks + blk);
-      float z = zdefault;
-      if (zp) {
-        if (zp_dt == TMH_U8 || zp_dt == TMH_S8) {
-          const int64_t bit = blk * BITS;
-          const uint8_t zb = static_cast<const uint8_t*>(zp)[id * zrow + bit / 8];
-          int zq;
-          if constexpr (BITS == 8) {
-            zq = zp_dt == TMH_S8 ? static_cast<int>(static_cast<int8_t>(zb)) : static_cast<int>(zb);
-          } else {
-            zq = (zb >> (bit % 8)) & ((1 << BITS) - 1);
-            if (zp_dt == TMH_S8 && zq >= (1 << (BITS - 1))) zq -= (1 << BITS);
-          }
-          z = static_cast<float>(zq);
-        } else {
-          z = round_to<DT>(load_float_rt(zp, zp_dt, id * blocks + blk));
-        }
+      if constexpr (!ONE_BLOCK) {
+        const int64_t blk = (col0 + b * PER + v) / bs;
+        s = load_as_f32<DT>(scales, id * blocks + blk);
+        z = zero_of(blk);
       }
-      store_as<DT>(out, i * D + col, dequant_value<DT>(static_cast<float>(q), z, s));
+      vals[b * PER + v] = dequant_value<DT>(static_cast<float>(q), z, s);
     }
   }
+  const int64_t o = static_cast<int64_t>(i) * D + col0;
+  if constexpr (VEC_OUT) {
+    constexpr int ES = DT == DT_F32 ? 4 : 2;
+    uint32_t words[V * ES / 4];
+#pragma unroll
+    for (int k = 0; k < V * ES / 4; ++k) {
+      if constexpr (DT == DT_F32) {
+        words[k] = __builtin_bit_cast(uint32_t, vals[k]);
+      } else if constexpr (DT == DT_F16) {
+        words[k] = f32_to_f16_bits(vals[2 * k]) | (static_cast<uint32_t>(f32_to_f16_bits(vals[2 * k + 1])) << 16);
+      } else {
+        words[k] = f32_to_bf16_bits(vals[2 * k]) | (static_cast<uint32_t>(f32_to_bf16_bits(vals[2 * k + 1])) << 16);
+      }
+    }
+    auto* dst = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(out) + o * ES);
+    if constexpr (V * ES == 8) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(words[0], words[1]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < V * ES / 16; ++k)
+        reinterpret_cast<uint4*>(dst)[k] = make_uint4(words[4 * k], words[4 * k + 1], words[4 * k + 2], words[4 * k + 3]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < V; ++k) store_as<DT>(out, o + k, vals[k]);
+  }
+}
+
+template <int DT, int BITS, int UB, bool ONE_BLOCK>
+void launch_gather_ub(const uint8_t* data, bool sgn, int64_t rows, int64_t row_bytes, const void* ids,
+                      bool ids64, int64_t n_ids, const void* scales, int64_t blocks, int64_t bs,
+                      const void* zp, int zp_dt, int64_t zrow, void* out, int64_t units, bool vec_out, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((n_ids * units + 255) / 256));
+  const auto n = static_cast<uint32_t>(n_ids);
+  const auto un = static_cast<uint32_t>(units);
+  if constexpr (UB == 4) {
+    if (vec_out) {
+      k_gather_bq<DT, BITS, UB, ONE_BLOCK, true><<<grid, 256, 0, s>>>(data, sgn, rows, row_bytes, ids, ids64, n, scales,
+                                                                      blocks, bs, zp, zp_dt, zrow, out, un);
+      return;
+    }
+  }
+  k_gather_bq<DT, BITS, UB, ONE_BLOCK, false><<<grid, 256, 0, s>>>(data, sgn, rows, row_bytes, ids, ids64, n, scales,
+                                                                   blocks, bs, zp, zp_dt, zrow, out, un);
 }
 
 template <int DT, int BITS>
 void launch_gather(const uint8_t* data, bool sgn, int64_t rows, int64_t row_bytes, const void* ids,
                    bool ids64, int64_t n_ids, const void* scales, int64_t blocks, int64_t bs,
                    const void* zp, int zp_dt, int64_t zrow, void* out, hipStream_t s) {
+  constexpr int PER = 8 / BITS;
+  constexpr int ES = DT == DT_F32 ? 4 : 2;
   const bool vec = row_bytes % 4 == 0 && reinterpret_cast<uintptr_t>(data) % 4 == 0;
   const int64_t units = vec ? row_bytes / 4 : row_bytes;
-  const int64_t total = n_ids * units;
-  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
-  if (vec)
-    k_gather_bq<DT, BITS, 4><<<grid, 256, 0, s>>>(data, sgn, rows, row_bytes, ids, ids64, n_ids, scales, blocks, bs, zp, zp_dt, zrow, out, units);
-  else
-    k_gather_bq<DT, BITS, 1><<<grid, 256, 0, s>>>(data, sgn, rows, row_bytes, ids, ids64, n_ids, scales, blocks, bs, zp, zp_dt, zrow, out, units);
+  const int64_t D = row_bytes * PER;
+  if (vec) {
+    const bool one = bs % (4 * PER) == 0;
+    const bool vec_out = reinterpret_cast<uintptr_t>(out) % 16 == 0 && (D * ES) % 16 == 0;
+    if (one)
+      launch_gather_ub<DT, BITS, 4, true>(data, sgn, rows, row_bytes, ids, ids64, n_ids, scales, blocks, bs, zp, zp_dt,
+                                          zrow, out, units, vec_out, s);
+    else
+      launch_gather_ub<DT, BITS, 4, false>(data, sgn, rows, row_bytes, ids, ids64, n_ids, scales, blocks, bs, zp, zp_dt,
+                                           zrow, out, units, vec_out, s);
+  } else {
+    launch_gather_ub<DT, BITS, 1, false>(data, sgn, rows, row_bytes, ids, ids64, n_ids, scales, blocks, bs, zp, zp_dt,
+                                         zrow, out, units, false, s);
+  }
 }
 
 template <int DT>
@@ -228,6 +294,9 @@ int tmh_gather_block_quantized(tmh_ctx* ctx, const void* d_data, int data_dtype,
     return fail(ctx, TMH_ERR_INVALID, "GatherBlockQuantized zero points must be u8, s8 or float, got %s", dtype_name(zp_dtype));
   if (n_ids == 0) return TMH_OK;
   if (!d_data || !d_ids || !d_scales || !d_out) return fail(ctx, TMH_ERR_INVALID, "GatherBlockQuantized: NULL pointer");
+  if (n_ids * row_bytes >= (int64_t(1) << 32) - 256)
+    return fail(ctx, TMH_ERR_UNSUPPORTED, "GatherBlockQuantized: %lld ids of %lld bytes exceed 2^32 packed bytes per call",
+                (long long)n_ids, (long long)row_bytes);
   hipStream_t s = pick_stream(ctx, stream);
   const int64_t bs = D / blocks;
   const int64_t zrow = (blocks * bits + 7) / 8;
