@@ -494,8 +494,8 @@ __global__ __launch_bounds__(256) void k_gemm_f16(
   }
 }
 
-// Prefill GEMM: 256 x 128 output tile per workgroup of four wavefronts, k-blocks of one
-// chunk (CW weights).
+// Prefill GEMM: 256 x 64*WN output tile per workgroup of 2*WN wavefronts (WN = 2: 256 x 128,
+// one wavefront per SIMD; WN = 4: 256 x 256, two per SIMD), k-blocks of one chunk (CW weights).
 //  - A: the k-block's 256 rows x CW f16 go global -> LDS by buffer_load ... lds (no VGPRs),
 //    double buffered, rows of CW*2 bytes whose 16-byte pieces are XOR-swizzled by row so the
 //    MFMA fragment reads of 16 rows hit distinct banks. Rows past M read row M-1 (their outputs
@@ -504,7 +504,6 @@ __global__ __launch_bounds__(256) void k_gemm_f16(
 //    weight tiles and their scales and zero points are loaded one k-block ahead and dequantized
 //    in registers (exact f16), each fragment feeding eight v_mfma_f32_16x16x32_f16.
 constexpr int kGemmBM = 256;
-constexpr int kGemmBN = 128;
 
 template <int BITS>
 constexpr size_t gemm_lds_bytes() {
@@ -528,8 +527,8 @@ __device__ __forceinline__ int a_slot(int row, int piece) {
   return BITS == 8 ? (piece ^ ((row >> 1) & 7)) : (piece ^ (row & 15));
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT>
-__global__ __launch_bounds__(256) void k_gemm_lds(
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN>
+__global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
     int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
@@ -541,13 +540,14 @@ __global__ __launch_bounds__(256) void k_gemm_lds(
   constexpr int ROWB = CW * 2;           // bytes per LDS row
   constexpr int PPR = CW / 8;            // 16-byte pieces per row
   constexpr int RPI = 64 / PPR;          // rows per wavefront load instruction
-  constexpr int LOADS = 64 / RPI;        // load instructions per wavefront per k-block (64 rows)
+  constexpr int RW = kGemmBM / (2 * WN); // A rows each wavefront brings into LDS
+  constexpr int LOADS = RW / RPI;        // load instructions per wavefront per k-block
   constexpr int NJ = SPLIT ? STEPS : 1;  // parameter entries per tile per k-block
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   // Consecutive workgroups take the m-blocks of one n-block, so each XCD keeps one m-block's
   // A rows in its L2 while the weights stream past.
   // With split K (ws != nullptr), workgroup blocks of mblocks*nblocks take consecutive ranges of
@@ -558,7 +558,7 @@ __global__ __launch_bounds__(256) void k_gemm_lds(
   const int mb = static_cast<int>(tile % static_cast<unsigned>(mblocks));
   const int nb = static_cast<int>(tile / static_cast<unsigned>(mblocks));
   const int m0 = mb * kGemmBM;
-  const int t0 = nb * (kGemmBN / 16) + wn * 4;
+  const int t0 = (nb * WN + wn) * 4;
   const uint32_t nch = static_cast<uint32_t>(nchunks);
   const uint32_t kb0 = static_cast<uint32_t>(split) * static_cast<uint32_t>(chunks_per_split);
   const uint32_t kb1 = kb0 + chunks_per_split < nch ? kb0 + chunks_per_split : nch;
@@ -569,43 +569,39 @@ __global__ __launch_bounds__(256) void k_gemm_lds(
   const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
   const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
 
-  // A loads of this wavefront: rows wave*64 + s*RPI + lane/PPR, LDS slot lane%PPR.
+  // A loads of this wavefront: rows wave*RW + s*RPI + lane/PPR, LDS slot lane%PPR. Offsets are
+  // formed per load (few live registers); rows at or past M lie outside the buffer range and
+  // read zeros (their outputs are never stored).
   const int a_lrow = lane / PPR, a_lslot = lane % PPR;
-  uint32_t a_off[LOADS];
-#pragma unroll
-  for (int s2 = 0; s2 < LOADS; ++s2) {
-    const int row = wave * 64 + s2 * RPI + a_lrow;
-    const int piece = a_slot<BITS>(row, a_lslot);  // the swizzle is its own inverse
-    const int64_t grow = m0 + row < M ? m0 + row : M - 1;
-    a_off[s2] = (static_cast<uint32_t>(grow) * static_cast<uint32_t>(lda) + piece * 8) * 2;
-  }
+  const uint32_t a_row0 = static_cast<uint32_t>(m0 + wave * RW + a_lrow) * static_cast<uint32_t>(lda) * 2;
+  const uint32_t a_rstep = static_cast<uint32_t>(RPI) * static_cast<uint32_t>(lda) * 2;
+  auto a_off = [&](int s2) -> uint32_t {
+    const int piece = a_slot<BITS>(wave * RW + s2 * RPI + a_lrow, a_lslot);  // the swizzle is its own inverse
+    return a_row0 + static_cast<uint32_t>(s2) * a_rstep + piece * 16;
+  };
   auto load_a = [&](uint32_t kb, int buf) {
-    uint8_t* base = lds + buf * (kGemmBM * ROWB) + wave * 64 * ROWB;
+    uint8_t* base = lds + buf * (kGemmBM * ROWB) + wave * RW * ROWB;
     if (static_cast<int64_t>(kb + 1) * CW <= K) {
 #pragma unroll
       for (int s2 = 0; s2 < LOADS; ++s2)
-        lds_dma16(a_rsrc, base + s2 * RPI * ROWB, a_off[s2], kb * (CW * 2));
+        lds_dma16(a_rsrc, base + s2 * RPI * ROWB, a_off(s2), kb * (CW * 2));
     } else {
       // A k-block that reaches past K: through registers, zero past K. The whole offset is in
       // the VGPR operand so the buffer range check covers it.
 #pragma unroll
       for (int s2 = 0; s2 < LOADS; ++s2) {
-        const int row = wave * 64 + s2 * RPI + a_lrow;
+        const int row = wave * RW + s2 * RPI + a_lrow;
         const int piece = a_slot<BITS>(row, a_lslot);
-        uint4_t v = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off[s2] + kb * (CW * 2), 0, 0);
+        uint4_t v = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off(s2) + kb * (CW * 2), 0, 0);
         if (static_cast<int64_t>(kb) * CW + piece * 8 >= K) v = uint4_t{0u, 0u, 0u, 0u};
         *reinterpret_cast<uint4_t*>(base + (s2 * RPI + a_lrow) * ROWB + a_lslot * 16) = v;
       }
     }
   };
   // This wavefront's four weight tiles and their parameters; tiles past N read zeros.
-  uint32_t b_off[4], p_off[4];
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const uint32_t t = static_cast<uint32_t>(t0 + nt);
-    b_off[nt] = (t * nch * 64 + lane) * 16;
-    p_off[nt] = (t * nch * nbc + ((g * GW) >> bsc_shift)) * 16 + r;
-  }
+  const uint32_t b_base = (static_cast<uint32_t>(t0) * nch * 64 + lane) * 16, b_tstep = nch * 1024;
+  const uint32_t p_base = (static_cast<uint32_t>(t0) * nch * nbc + ((g * GW) >> bsc_shift)) * 16 + r;
+  const uint32_t p_tstep = nch * static_cast<uint32_t>(nbc) * 16;
   struct BStage {
     uint4_t w[4];
     uint32_t s[NJ][4];
@@ -615,10 +611,10 @@ __global__ __launch_bounds__(256) void k_gemm_lds(
     const uint32_t kofs = kb * static_cast<uint32_t>(nbc) * 16;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      st.w[nt] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, b_off[nt], kb * 1024, 0);
+      st.w[nt] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, b_base + nt * b_tstep, kb * 1024, 0);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        uint32_t e = p_off[nt];
+        uint32_t e = p_base + nt * p_tstep;
         if constexpr (SPLIT) e += static_cast<uint32_t>(((g * GW + 8 * j) >> bsc_shift) - ((g * GW) >> bsc_shift)) * 16;
         st.s[j][nt] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, kofs * 2, 0);
         if constexpr (HAS_ZP) st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, kofs, 0);
@@ -642,25 +638,48 @@ __global__ __launch_bounds__(256) void k_gemm_lds(
                                  __builtin_bit_cast(half2_t, sv | (sv << 16)));
     }
   };
-  // Step i+1's weights dequantize while step i's MFMAs run.
+  // Software pipeline over the k-block's steps: once fragment mt of step i has fed its four
+  // MFMAs, the same registers take fragment mt of step i+1 from LDS; step i+1's weights are
+  // dequantized (into the other of two register sets) while step i's MFMAs run.
   auto compute = [&](int buf, const BStage& st) {
     const uint8_t* abase = lds + buf * (kGemmBM * ROWB) + (wm * 128 + r) * ROWB;
-    half8_t bf[4], bn[4];
-    dequant(st, 0, bf);
+    if constexpr (WN == 4) {
+      // Two wavefronts per SIMD: each keeps few registers live and relies on the other to fill
+      // its waits; one set of weight fragments per step, A fragments read as they are used.
+#pragma unroll
+      for (int i = 0; i < STEPS; ++i) {
+        half8_t bc[4];
+        dequant(st, i, bc);
+        const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+          const half8_t a = *reinterpret_cast<const half8_t*>(abase + mt * 16 * ROWB + slot);
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[nt], a, acc[mt][nt], 0, 0, 0);
+        }
+      }
+      return;
+    }
+    half8_t af[8], b0[4], b1[4];
+    {
+      const int slot = a_slot<BITS>(r, g * (GW / 8)) * 16;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) af[mt] = *reinterpret_cast<const half8_t*>(abase + mt * 16 * ROWB + slot);
+    }
+    dequant(st, 0, b0);
 #pragma unroll
     for (int i = 0; i < STEPS; ++i) {
+      half8_t(&bc)[4] = (i & 1) ? b1 : b0;
+      half8_t(&bn)[4] = (i & 1) ? b0 : b1;
       if (i + 1 < STEPS) dequant(st, i + 1, bn);
-      const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
+      const int slot = a_slot<BITS>(r, g * (GW / 8) + i + 1) * 16;
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) {
-        const half8_t a = *reinterpret_cast<const half8_t*>(abase + mt * 16 * ROWB + slot);
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt)  // weights as the first operand: lane holds 4 columns of one row
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[nt], a, acc[mt][nt], 0, 0, 0);
-      }
-      if (i + 1 < STEPS) {
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) bf[nt] = bn[nt];
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[nt], af[mt], acc[mt][nt], 0, 0, 0);
+        if (i + 1 < STEPS) af[mt] = *reinterpret_cast<const half8_t*>(abase + mt * 16 * ROWB + slot);
       }
     }
   };
@@ -970,19 +989,44 @@ void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
 // Split K when the output tiles cannot fill the GPU: partial sums go to the context's
 // workspace and k_splitk_reduce adds them. During stream capture the workspace cannot grow,
 // so a capture that finds it too small runs without splitting.
-template <int BITS, bool HAS_ZP, bool SPLIT>
-void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
-  const int mblocks = static_cast<int>((a.M + kGemmBM - 1) / kGemmBM);
-  const int nblocks = static_cast<int>((w->ntiles * 16 + kGemmBN - 1) / kGemmBN);
-  const int64_t tiles = static_cast<int64_t>(mblocks) * nblocks;
-  int splits = 1;
-  int cps = static_cast<int>(w->nchunks);
-  const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-  if (tiles < cus && w->nchunks >= 4) {
-    splits = static_cast<int>(std::min<int64_t>({8, (cus + tiles - 1) / tiles, w->nchunks / 2}));
-    cps = static_cast<int>((w->nchunks + splits - 1) / splits);
-    splits = static_cast<int>((w->nchunks + cps - 1) / cps);
+// Tile shape and K split of one prefill GEMM. Each candidate (256 x 128 or 256 x 256 tiles,
+// 1-8 splits of K) is priced as rounds of workgroups over the CUs times the work of one, at the
+// per-CU rates the two tile shapes sustain on MI355X (2.71 and 3.27 dense f16 TFLOP/s per CU
+// at K = 4096), plus the f32 partial sums a split writes and the reduction reads back.
+struct GemmPlan {
+  int wn, splits, cps;
+};
+
+GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bits, int cus) {
+  const double cw = 512.0 / bits;
+  const int64_t mblocks = (M + kGemmBM - 1) / kGemmBM;
+  GemmPlan best{2, 1, static_cast<int>(nchunks)};
+  double best_t = 1e30;
+  for (int wn : {2, 4}) {
+    const int64_t tiles = mblocks * ((ntiles + 4 * wn - 1) / (4 * wn));
+    const double chunk_s = 2.0 * kGemmBM * 64.0 * wn * cw / (wn == 4 ? 3.27e12 : 2.71e12);
+    for (int64_t splits = 1; splits <= 8; ++splits) {
+      if (splits > 1 && 2 * splits > nchunks) break;
+      const int64_t cps = (nchunks + splits - 1) / splits;
+      const int64_t used = (nchunks + cps - 1) / cps;
+      if (used != splits) continue;
+      const int64_t rounds = (tiles * splits + cus - 1) / cus;
+      double t = static_cast<double>(rounds) * cps * chunk_s;
+      if (splits > 1) t += 2.0 * splits * M * N * 4 / 5e12;
+      if (t < best_t) {
+        best_t = t;
+        best = GemmPlan{wn, static_cast<int>(splits), static_cast<int>(cps)};
+      }
+    }
   }
+  return best;
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN>
+void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s, int splits, int cps) {
+  const int mblocks = static_cast<int>((a.M + kGemmBM - 1) / kGemmBM);
+  const int nblocks = static_cast<int>((w->ntiles + 4 * WN - 1) / (4 * WN));
+  const int64_t tiles = static_cast<int64_t>(mblocks) * nblocks;
   float* ws = nullptr;
   if (splits > 1) {
     ws = static_cast<float*>(workspace(ctx, static_cast<size_t>(splits) * a.M * w->N * sizeof(float), s));
@@ -993,10 +1037,10 @@ void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStr
   }
   const dim3 grid(static_cast<unsigned>(tiles * splits));
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN>), hipFuncAttributeMaxDynamicSharedMemorySize,
       static_cast<int>(gemm_lds_bytes<BITS>()));
   (void)attr;
-  k_gemm_lds<BITS, HAS_ZP, SPLIT><<<grid, 256, gemm_lds_bytes<BITS>(), s>>>(
+  k_gemm_lds<BITS, HAS_ZP, SPLIT, WN><<<grid, 128 * WN, gemm_lds_bytes<BITS>(), s>>>(
       reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
       static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
       a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
@@ -1009,6 +1053,15 @@ void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStr
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
+void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, ctx->num_cus > 0 ? ctx->num_cus : 256);
+  if (p.wn == 4)
+    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4>(ctx, w, a, s, p.splits, p.cps);
+  else
+    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2>(ctx, w, a, s, p.splits, p.cps);
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_fast_variant(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   if (a.M <= 16) {
     launch_gemv<BITS, 1, HAS_ZP, SPLIT>(w, a, s, ctx->num_cus);
@@ -1017,8 +1070,8 @@ void launch_fast_variant(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hi
   } else if (a.M <= 64 || BITS == 2) {
     launch_gemv<BITS, 4, HAS_ZP, SPLIT>(w, a, s, ctx->num_cus);
   } else if constexpr (BITS != 2) {
-    const bool fits = a.M * a.lda * 2 < (int64_t(1) << 31) &&
-                      w->ntiles * w->nchunks * 1024 + 8 * w->nchunks * 1024 < (int64_t(1) << 31);
+    const bool fits = (a.M + kGemmBM) * a.lda * 2 < (int64_t(1) << 31) &&
+                      w->ntiles * w->nchunks * 1024 + 16 * w->nchunks * 1024 < (int64_t(1) << 31);
     if (a.a_vec && fits)
       launch_gemm_lds<BITS, HAS_ZP, SPLIT>(ctx, w, a, s);
     else
