@@ -237,6 +237,18 @@ int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d
                        int64_t b_zero_count, int64_t batch, int64_t M, int64_t K, int64_t N,
                        int b_batched, void* d_y, void* stream);
 
+/* ------------------------------------------------------------------ DynamicQuantizeLinear */
+
+/*
+ * DynamicQuantizeLinear (quantized.ex:94-103), the u8 activations MatMulInteger takes:
+ * low = min(min(x), 0), high = max(max(x), 0), scale = (high - low) / 255 (1 when 0),
+ * zero = saturate(round(-low / scale)), y = saturate(round(x / scale) + zero), in f32 with
+ * rounding half to even. The scale and zero point are written on the device.
+ *  d_x [n] F32; d_y [n] U8; d_scale one F32; d_zero one U8
+ */
+int tmh_dynamic_quantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t n, void* d_y,
+                                void* d_scale, void* d_zero, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,8 +12,9 @@ from transmuter_amd import quantized
 pytestmark = pytest.mark.gpu
 
 SINGLE_NODE = (names("MatMulNBits") + names("GatherBlockQuantized") + names("DequantizeLinear")
-               + ["MatMulInteger", "MatMulInteger_k4096_extremes", "MatMulInteger_k4096_signed"])
-BIT_EXACT = ("GatherBlockQuantized", "DequantizeLinear", "MatMulInteger")
+               + ["MatMulInteger", "MatMulInteger_k4096_extremes", "MatMulInteger_k4096_signed"]
+               + names("DynamicQuantizeLinear"))
+BIT_EXACT = ("GatherBlockQuantized", "DequantizeLinear", "MatMulInteger", "DynamicQuantizeLinear")
 
 
 def run_fixture(ctx, f: Fixture):

@@ -1,0 +1,123 @@
+"""The u8/s8 activation path on the GPU: DynamicQuantizeLinear and MatMulInteger (int8 MFMA with
+row/column-sum corrections) against the oracle, bit-exactly, and the reference's
+MatMulInteger_dynamic_quant graph (DynamicQuantizeLinear -> MatMulInteger on the device, Cast
+and Mul on the host as they stay on the Nx backend) against its ONNX Runtime output."""
+
+import zlib
+
+import numpy as np
+import pytest
+
+from fixtures import Fixture, tolerance
+from oracle import oracle as o
+from transmuter_amd import quantized
+from transmuter_amd.onnx_wire import NodeProto
+
+pytestmark = pytest.mark.gpu
+
+MI_CASES = [
+    # batch, M, K, N, a type, b type, a_zero (None / "scalar" / "row"), b_zero, b batched
+    (1, 1, 64, 16, "u8", "s8", "scalar", None, False),
+    (1, 130, 200, 70, "u8", "u8", "row", "col", False),    # ragged tiles and k
+    (1, 128, 256, 128, "s8", "s8", None, None, False),
+    (1, 33, 4096, 257, "u8", "s8", "scalar", "scalar", False),
+    (3, 40, 96, 48, "s8", "u8", "row", "col", True),
+    (2, 17, 75, 9, "u8", "u8", "scalar", "col", False),      # K and N off every vector width
+    (1, 300, 512, 520, "u8", "s8", "scalar", None, False),
+]
+
+
+def _ints(rng, shape, dtype):
+    return rng.integers(-128, 128, shape, dtype=np.int8) if dtype == "s8" else rng.integers(0, 256, shape, dtype=np.uint8)
+
+
+@pytest.mark.parametrize("case", MI_CASES, ids=lambda c: "b{}_M{}_K{}_N{}_{}{}".format(*c[:6]))
+def test_matmul_integer_matches_oracle(ctx, case):
+    batch, m, k, n, adt, bdt, az, bz, bb = case
+    print(f"matmul_integer {case}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    a = _ints(rng, (batch, m, k) if batch > 1 else (m, k), adt)
+    b = _ints(rng, (batch, k, n) if bb else (k, n), bdt)
+    a_zero = None if az is None else _ints(rng, (1,) if az == "scalar" else (m,), adt)
+    b_zero = None if bz is None else _ints(rng, (1,) if bz == "scalar" else (n,), bdt)
+    inputs = [ctx.put(a), ctx.put(b), ctx.put(a_zero) if a_zero is not None else None,
+              ctx.put(b_zero) if b_zero is not None else None]
+    node = NodeProto(op_type="MatMulInteger", input=["a", "b", "az" if az else "", "bz" if bz else ""], output=["y"])
+    got = quantized.apply(node, inputs)[0].numpy()
+    ref = o.matmul_integer(a, b, a_zero.reshape(-1) if a_zero is not None else None,
+                           b_zero.reshape(-1) if b_zero is not None else None)
+    assert got.dtype == np.int32 and got.shape == ref.shape
+    assert np.array_equal(got, ref)
+
+
+def test_matmul_integer_extremes_past_two_to_the_24(ctx):
+    """Every product at its largest: 4096 * 255 * 255 is beyond 2^24 (f32-exact) but within s32."""
+    k = 4096
+    a = np.full((3, k), 255, np.uint8)
+    b = np.full((k, 5), 255, np.uint8)
+    node = NodeProto(op_type="MatMulInteger", input=["a", "b"], output=["y"])
+    got = quantized.apply(node, [ctx.put(a), ctx.put(b)])[0].numpy()
+    assert np.all(got == 4096 * 255 * 255)
+
+
+DQL_CASES = [
+    ("normal", 1000), ("normal", 5), ("normal", 300_000), ("positive", 4097), ("negative", 77), ("constant", 64),
+    ("zeros", 10), ("ties", 256), ("empty", 0),
+]
+
+
+def _dql_input(rng, kind, n):
+    if kind == "normal":
+        return rng.standard_normal(n).astype(np.float32) * 3
+    if kind == "positive":
+        return rng.random(n).astype(np.float32) * 7 + 0.5
+    if kind == "negative":
+        return -rng.random(n).astype(np.float32) * 2 - 0.25
+    if kind == "constant":
+        return np.full(n, 2.5, np.float32)
+    if kind == "zeros":
+        return np.zeros(n, np.float32)
+    if kind == "ties":  # x / scale lands on halves: scale is exactly 1 here
+        return np.arange(n, dtype=np.float32) - np.float32(127.5)
+    return np.zeros(0, np.float32)
+
+
+@pytest.mark.parametrize("case", DQL_CASES, ids=lambda c: f"{c[0]}_{c[1]}")
+def test_dynamic_quantize_linear_matches_oracle(ctx, case):
+    kind, n = case
+    print(f"dynamic_quantize_linear {case}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    x = _dql_input(rng, kind, n)
+    node = NodeProto(op_type="DynamicQuantizeLinear", input=["x"], output=["y", "s", "z"])
+    y, s, z = (t.numpy() for t in quantized.apply(node, [ctx.put(x)]))
+    if n == 0:  # no range: the scale of a constant (1) and zero point 0
+        assert y.shape == (0,) and s == np.float32(1) and z == 0
+        return
+    ry, rs, rz = o.dynamic_quantize_linear(x)
+    assert y.dtype == np.uint8 and y.shape == x.shape
+    assert np.array_equal(y, ry)
+    assert np.float32(s).view(np.uint32) == np.float32(rs).view(np.uint32)
+    assert np.uint8(z) == rz
+
+
+def test_dynamic_quant_matmul_fixture(ctx):
+    """MatMulInteger_dynamic_quant: x -> DynamicQuantizeLinear -> MatMulInteger with the s8
+    weights and the activation zero point -> Cast -> Mul by (x scale * w scale)."""
+    f = Fixture("MatMulInteger_dynamic_quant")
+    values = {name: ctx.put(v) for name, v in f.inputs.items()}
+    values.update(f.initializers)
+    for node in f.nodes:
+        args = [values[name] if name else None for name in node.input]
+        if node.op_type in quantized.op_types():
+            outs = quantized.apply(node, args)
+        elif node.op_type == "Cast":
+            outs = [np.asarray(args[0].numpy(), np.float32)]
+        else:  # Mul
+            host = [a.numpy() if hasattr(a, "numpy") else np.asarray(a) for a in args]
+            outs = [(np.asarray(host[0], np.float32) * np.asarray(host[1], np.float32)).astype(np.float32)]
+        for name, v in zip(node.output, outs):
+            values[name] = v
+    got = np.asarray(values["y"])
+    expected = f.outputs["y"]
+    assert got.shape == expected.shape
+    assert np.abs(got - expected).max() <= tolerance(expected)

@@ -65,6 +65,7 @@ SIGNATURES = {
     "tmh_dequantize_linear": (_i, [_vp, _vp, _i, _i64, _i64, _i64, _vp, _i, _vp, _i, _i, _i64, _vp, _vp]),
     "tmh_matmul_integer": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i, _vp,
                                 _vp]),
+    "tmh_dynamic_quantize_linear": (_i, [_vp, _vp, _i, _i64, _vp, _vp, _vp, _vp]),
 }
 
 _lock = threading.Lock()

@@ -5,6 +5,9 @@
 //   lib/transmuter/ops/quantized.ex:70-84    DequantizeLinear, expand_quant_param/3 at :328-353
 //   lib/transmuter/ops/quantized.ex:105-110  MatMulInteger, per_axis/3 at :288-291
 //   lib/transmuter/ops/nn.ex:537-555         integer_product/5: exact s32 sums
+//   lib/transmuter/ops/quantized.ex:94-103   DynamicQuantizeLinear
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 
 #include "tmh_device.h"
@@ -267,6 +270,224 @@ __global__ __launch_bounds__(256) void k_matmul_integer(
   if (m < M && n < N) y[(bt * M + m) * N + n] = static_cast<int32_t>(acc);
 }
 
+
+// ------------------------------------------------------------------ MatMulInteger on int8 MFMA
+
+// With a = sa + oa (sa the s8 form of a: the byte itself for s8 data, a ^ 0x80 = a - 128 for
+// u8 data, so oa is 0 or 128) and likewise b:
+//   sum_k (a - az_m)(b - bz_n) = sum_k sa sb + cb_n * rs_m + ca_m * cs_n + K * ca_m * cb_n
+// with ca_m = oa - az_m, cb_n = ob - bz_n, rs_m = sum_k sa[m][k], cs_n = sum_k sb[k][n], all
+// modulo 2^32 (the s32 wrap of the exact sum). The sa sb sums run on v_mfma_i32_16x16x64_i8.
+
+// rs for every row of every A batch, cs for every column of every B batch.
+__global__ __launch_bounds__(256) void k_int8_sums(const uint8_t* __restrict__ a, bool a_signed,
+                                                    const uint8_t* __restrict__ b, bool b_signed, int64_t a_rows,
+                                                    int64_t K, int64_t N, int64_t b_batches, int32_t* __restrict__ rs,
+                                                    int32_t* __restrict__ cs) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < a_rows) {
+    const uint8_t* row = a + i * K;
+    uint32_t sum = 0;
+    for (int64_t k = 0; k < K; ++k) sum += static_cast<uint32_t>(static_cast<int8_t>(a_signed ? row[k] : row[k] ^ 0x80));
+    rs[i] = static_cast<int32_t>(sum);
+  }
+  const int64_t j = i - a_rows;
+  if (j >= 0 && j < b_batches * N) {
+    const int64_t bt = j / N, n = j - bt * N;
+    const uint8_t* col = b + bt * K * N + n;
+    uint32_t sum = 0;
+    for (int64_t k = 0; k < K; ++k)
+      sum += static_cast<uint32_t>(static_cast<int8_t>(b_signed ? col[k * N] : col[k * N] ^ 0x80));
+    cs[j] = static_cast<int32_t>(sum);
+  }
+}
+
+constexpr int kI8Tile = 128;  // output rows and columns per workgroup
+constexpr int kI8K = 64;      // k per step (one MFMA deep)
+constexpr int kI8Row = 80;    // LDS bytes per row of 64: 16-byte pieces of 8 consecutive rows on distinct banks
+
+// 128 x 128 outputs per workgroup of four wavefronts (64 x 64 each, 4 x 4 MFMA tiles). Per
+// k-step A's rows and B's columns go to LDS as s8 bytes, B transposed through 4 x 4 byte
+// blocks, zeros outside the matrices.
+__global__ __launch_bounds__(256) void k_matmul_integer_mfma(
+    const uint8_t* __restrict__ a, bool a_signed, const uint8_t* __restrict__ b, bool b_signed,
+    const void* __restrict__ a_zero, int64_t a_zero_count, const void* __restrict__ b_zero,
+    int64_t b_zero_count, int64_t M, int64_t K, int64_t N, bool b_batched, const int32_t* __restrict__ rs,
+    const int32_t* __restrict__ cs, int32_t* __restrict__ y) {
+  __shared__ __align__(16) uint8_t sA[kI8Tile * kI8Row];
+  __shared__ __align__(16) uint8_t sB[kI8Tile * kI8Row];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t bt = blockIdx.z;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kI8Tile, n0 = static_cast<int64_t>(blockIdx.x) * kI8Tile;
+  const uint8_t* a8 = a + bt * M * K;
+  const uint8_t* b8 = b + (b_batched ? bt * K * N : 0);
+  const uint32_t aflip = a_signed ? 0u : 0x80808080u, bflip = b_signed ? 0u : 0x80808080u;
+  const bool a_vec = (K % 16) == 0 && (reinterpret_cast<uintptr_t>(a) % 16) == 0;
+  const bool b_vec = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(b) % 4) == 0;
+  int4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = int4_t{0, 0, 0, 0};
+  for (int64_t k0 = 0; k0 < K; k0 += kI8K) {
+    // A: 128 rows x 64 bytes, 16 bytes per thread and load.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + 256 * h;
+      const int row = c >> 2, kc = (c & 3) * 16;
+      const int64_t gm = m0 + row, gk = k0 + kc;
+      uint4_t v = {0u, 0u, 0u, 0u};
+      if (gm < M) {
+        if (a_vec && gk + 16 <= K) {
+          v = *reinterpret_cast<const uint4_t*>(a8 + gm * K + gk) ^ aflip;
+        } else {
+          for (int e = 0; e < 16; ++e)
+            if (gk + e < K) v[e >> 2] |= static_cast<uint32_t>(a8[gm * K + gk + e] ^ (aflip & 0xFFu)) << (8 * (e & 3));
+        }
+      }
+      *reinterpret_cast<uint4_t*>(sA + row * kI8Row + kc) = v;
+    }
+    // B: 64 k x 128 columns as 4 x 4 byte blocks, stored column-major (sB[n][k]).
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int u = tid + 256 * h;
+      const int kq = u >> 5, nq = u & 31;
+      const int64_t gk = k0 + 4 * kq, gn = n0 + 4 * nq;
+      uint32_t rw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        rw[i] = 0;
+        if (gk + i < K) {
+          if (b_vec && gn + 4 <= N) {
+            rw[i] = *reinterpret_cast<const uint32_t*>(b8 + (gk + i) * N + gn) ^ bflip;
+          } else {
+            for (int e = 0; e < 4; ++e)
+              if (gn + e < N) rw[i] |= static_cast<uint32_t>(b8[(gk + i) * N + gn + e] ^ (bflip & 0xFFu)) << (8 * e);
+          }
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t col = ((rw[0] >> (8 * e)) & 0xFFu) | (((rw[1] >> (8 * e)) & 0xFFu) << 8) |
+                             (((rw[2] >> (8 * e)) & 0xFFu) << 16) | (((rw[3] >> (8 * e)) & 0xFFu) << 24);
+        *reinterpret_cast<uint32_t*>(sB + (4 * nq + e) * kI8Row + 4 * kq) = col;
+      }
+    }
+    __syncthreads();
+    int4_t af[4], bf[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      af[mt] = *reinterpret_cast<const int4_t*>(sA + (wm * 64 + mt * 16 + r) * kI8Row + g * 16);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      bf[nt] = *reinterpret_cast<const int4_t*>(sB + (wn * 64 + nt * 16 + r) * kI8Row + g * 16);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)  // B first: a lane ends with 4 consecutive columns of one row
+        acc[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[nt], af[mt], acc[mt][nt], 0, 0, 0);
+    __syncthreads();
+  }
+  const uint32_t oa = a_signed ? 0u : 128u, ob = b_signed ? 0u : 128u;
+  auto zero_of = [](const void* z, int64_t count, int64_t i, bool sgn) -> uint32_t {
+    if (!z) return 0u;
+    const uint8_t raw = static_cast<const uint8_t*>(z)[count == 1 ? 0 : i];
+    return sgn ? static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(raw))) : raw;
+  };
+  const uint32_t kk = static_cast<uint32_t>(K);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int64_t m = m0 + wm * 64 + mt * 16 + r;
+    if (m >= M) continue;
+    const uint32_t ca = oa - zero_of(a_zero, a_zero_count, m, a_signed);
+    const uint32_t rsm = static_cast<uint32_t>(rs[bt * M + m]);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int64_t n = n0 + wn * 64 + nt * 16 + 4 * g;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (n + e >= N) break;
+        const uint32_t cb = ob - zero_of(b_zero, b_zero_count, n + e, b_signed);
+        const uint32_t csn = static_cast<uint32_t>(cs[(b_batched ? bt * N : 0) + n + e]);
+        const uint32_t v = static_cast<uint32_t>(acc[mt][nt][e]) + cb * rsm + ca * csn + kk * ca * cb;
+        y[(bt * M + m) * N + n + e] = static_cast<int32_t>(v);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ DynamicQuantizeLinear
+
+// scale = (max(x, 0) - min(x, 0)) / 255 (1 when that is 0), zero = saturate(round(-low / scale)),
+// in f32 with round-half-even, as quantized.ex:94-103.
+__device__ __forceinline__ void dql_params(float low, float high, float* scale, uint8_t* zero) {
+  low = fminf(low, 0.f);
+  high = fmaxf(high, 0.f);
+  float sc = (high - low) / 255.f;
+  if (sc == 0.f) sc = 1.f;
+  const float z = rintf(-low / sc);
+  *scale = sc;
+  *zero = static_cast<uint8_t>(fminf(fmaxf(z, 0.f), 255.f));
+}
+
+// Minimum and maximum of the block's share of x; with one block, the scale and zero point.
+__global__ __launch_bounds__(256) void k_dql_minmax(const float* __restrict__ x, int64_t n, float* __restrict__ part,
+                                                     float* __restrict__ scale, uint8_t* __restrict__ zero) {
+  __shared__ float lo_s[256], hi_s[256];
+  float lo = INFINITY, hi = -INFINITY;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    lo = fminf(lo, x[i]);
+    hi = fmaxf(hi, x[i]);
+  }
+  lo_s[threadIdx.x] = lo;
+  hi_s[threadIdx.x] = hi;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) {
+      lo_s[threadIdx.x] = fminf(lo_s[threadIdx.x], lo_s[threadIdx.x + w]);
+      hi_s[threadIdx.x] = fmaxf(hi_s[threadIdx.x], hi_s[threadIdx.x + w]);
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x != 0) return;
+  if (gridDim.x == 1) {
+    dql_params(lo_s[0], hi_s[0], scale, zero);
+  } else {
+    part[2 * blockIdx.x] = lo_s[0];
+    part[2 * blockIdx.x + 1] = hi_s[0];
+  }
+}
+
+__global__ __launch_bounds__(64) void k_dql_finalize(const float* __restrict__ part, int parts, float* __restrict__ scale,
+                                                      uint8_t* __restrict__ zero) {
+  if (threadIdx.x != 0) return;
+  float lo = INFINITY, hi = -INFINITY;
+  for (int i = 0; i < parts; ++i) {
+    lo = fminf(lo, part[2 * i]);
+    hi = fmaxf(hi, part[2 * i + 1]);
+  }
+  dql_params(lo, hi, scale, zero);
+}
+
+// y = saturate(round(x / scale) + zero), four values per thread.
+__global__ __launch_bounds__(256) void k_dql_quantize(const float* __restrict__ x, int64_t n,
+                                                       const float* __restrict__ scale, const uint8_t* __restrict__ zero,
+                                                       uint8_t* __restrict__ y) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (i >= n) return;
+  const float sc = *scale, z = static_cast<float>(*zero);
+  auto q = [&](float v) -> uint32_t { return static_cast<uint32_t>(fminf(fmaxf(rintf(v / sc) + z, 0.f), 255.f)); };
+  if (i + 4 <= n && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (reinterpret_cast<uintptr_t>(y) % 4) == 0) {
+    const float4_t v = *reinterpret_cast<const float4_t*>(x + i);
+    *reinterpret_cast<uint32_t*>(y + i) = q(v[0]) | (q(v[1]) << 8) | (q(v[2]) << 16) | (q(v[3]) << 24);
+  } else {
+    for (int e = 0; e < 4 && i + e < n; ++e) y[i + e] = static_cast<uint8_t>(q(x[i + e]));
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -362,11 +583,62 @@ int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d
   if (!d_a || !d_b || !d_y) return fail(ctx, TMH_ERR_INVALID, "MatMulInteger: NULL pointer");
   if (batch > 65535) return fail(ctx, TMH_ERR_INVALID, "MatMulInteger batch must be below 65536");
   hipStream_t s = pick_stream(ctx, stream);
-  const dim3 grid(static_cast<unsigned>((N + kMiTile - 1) / kMiTile), static_cast<unsigned>((M + kMiTile - 1) / kMiTile),
+  const bool a_sgn = a_dtype == TMH_S8, b_sgn = b_dtype == TMH_S8;
+  const int64_t b_batches = b_batched ? batch : 1;
+  const size_t sums_bytes = static_cast<size_t>(batch * M + b_batches * N) * sizeof(int32_t);
+  auto* sums = K > 0 ? static_cast<int32_t*>(workspace(ctx, sums_bytes, s)) : nullptr;
+  if (!sums) {
+    // K = 0, or no workspace inside a graph capture: the LDS-tiled kernel needs none.
+    const dim3 grid(static_cast<unsigned>((N + kMiTile - 1) / kMiTile), static_cast<unsigned>((M + kMiTile - 1) / kMiTile),
+                    static_cast<unsigned>(batch));
+    k_matmul_integer<<<grid, 256, 0, s>>>(d_a, a_sgn, d_b, b_sgn, d_a_zero, a_zero_count, d_b_zero, b_zero_count, M, K, N,
+                                          b_batched != 0, static_cast<int32_t*>(d_y));
+    return check_launch(ctx, "k_matmul_integer");
+  }
+  const auto* a8 = static_cast<const uint8_t*>(d_a);
+  const auto* b8 = static_cast<const uint8_t*>(d_b);
+  int32_t* rs = sums;
+  int32_t* cs = sums + batch * M;
+  const int64_t lines = batch * M + b_batches * N;
+  k_int8_sums<<<static_cast<unsigned>((lines + 255) / 256), 256, 0, s>>>(a8, a_sgn, b8, b_sgn, batch * M, K, N,
+                                                                        b_batches, rs, cs);
+  TMH_TRY(check_launch(ctx, "k_int8_sums"));
+  const dim3 grid(static_cast<unsigned>((N + kI8Tile - 1) / kI8Tile), static_cast<unsigned>((M + kI8Tile - 1) / kI8Tile),
                   static_cast<unsigned>(batch));
-  k_matmul_integer<<<grid, 256, 0, s>>>(d_a, a_dtype == TMH_S8, d_b, b_dtype == TMH_S8, d_a_zero, a_zero_count,
-                                        d_b_zero, b_zero_count, M, K, N, b_batched != 0, static_cast<int32_t*>(d_y));
-  return check_launch(ctx, "k_matmul_integer");
+  k_matmul_integer_mfma<<<grid, 256, 0, s>>>(a8, a_sgn, b8, b_sgn, d_a_zero, a_zero_count, d_b_zero, b_zero_count, M,
+                                             K, N, b_batched != 0, rs, cs, static_cast<int32_t*>(d_y));
+  return check_launch(ctx, "k_matmul_integer_mfma");
+}
+
+int tmh_dynamic_quantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t n, void* d_y, void* d_scale,
+                                void* d_zero, void* stream) {
+  TMH_TRY(use_device(ctx));
+  if (x_dtype != TMH_F32)
+    return fail(ctx, TMH_ERR_UNSUPPORTED, "DynamicQuantizeLinear takes f32 values, got %s", dtype_name(x_dtype));
+  if (n < 0) return fail(ctx, TMH_ERR_INVALID, "DynamicQuantizeLinear size must not be negative");
+  if (!d_scale || !d_zero || (n > 0 && (!d_x || !d_y)))
+    return fail(ctx, TMH_ERR_INVALID, "DynamicQuantizeLinear: NULL pointer");
+  hipStream_t s = pick_stream(ctx, stream);
+  const auto* x = static_cast<const float*>(d_x);
+  auto* scale = static_cast<float*>(d_scale);
+  auto* zero = static_cast<uint8_t*>(d_zero);
+  // One workgroup per 64 Ki values, at most 256; their partial ranges go through the workspace
+  // (one workgroup does it all when there is none, inside a graph capture).
+  int parts = static_cast<int>(std::min<int64_t>(256, (n + 65535) / 65536));
+  float* part = nullptr;
+  if (parts > 1) {
+    part = static_cast<float*>(workspace(ctx, static_cast<size_t>(parts) * 2 * sizeof(float), s));
+    if (!part) parts = 1;
+  }
+  k_dql_minmax<<<static_cast<unsigned>(std::max(parts, 1)), 256, 0, s>>>(x, n, part, scale, zero);
+  TMH_TRY(check_launch(ctx, "k_dql_minmax"));
+  if (parts > 1) {
+    k_dql_finalize<<<1, 64, 0, s>>>(part, parts, scale, zero);
+    TMH_TRY(check_launch(ctx, "k_dql_finalize"));
+  }
+  if (n == 0) return TMH_OK;
+  k_dql_quantize<<<static_cast<unsigned>((n + 1023) / 1024), 256, 0, s>>>(x, n, scale, zero, static_cast<uint8_t*>(d_y));
+  return check_launch(ctx, "k_dql_quantize");
 }
 
 }  // extern "C"

@@ -6,9 +6,10 @@ Inputs are `DeviceTensor`s on one context; quantization parameters may also be h
 (the reference keeps small initializers as static host values, lib/transmuter.ex:29-32).
 A missing optional input is None (lib/transmuter.ex:796).
 
-The four operators of the quantized-weight path run on the GPU: MatMulNBits (:30-46),
-GatherBlockQuantized (:49-66), DequantizeLinear (:70-84) and MatMulInteger (:105-110).
-The other handlers of the reference's op list (:19-21) stay on the Nx backend and raise here.
+The operators of the quantized-weight path run on the GPU: MatMulNBits (:30-46),
+GatherBlockQuantized (:49-66), DequantizeLinear (:70-84), MatMulInteger (:105-110) and the
+DynamicQuantizeLinear (:94-103) that feeds it u8 activations. The other handlers of the
+reference's op list (:19-21) stay on the Nx backend and raise here.
 """
 
 from __future__ import annotations
@@ -24,9 +25,9 @@ from .device import FLOAT_TYPES, NX_TO_TMH, Context, DeviceTensor, merge_types, 
 from .onnx_wire import ATTR_FLOAT, ATTR_FLOATS, ATTR_INT, ATTR_INTS, ATTR_STRING, ATTR_TENSOR
 from .packed import PackedWeight
 
-OP_TYPES = ["MatMulNBits", "GatherBlockQuantized", "DequantizeLinear", "MatMulInteger"]
+OP_TYPES = ["MatMulNBits", "GatherBlockQuantized", "DequantizeLinear", "MatMulInteger", "DynamicQuantizeLinear"]
 # The reference's other quantized handlers (quantized.ex:19-21), not on this path.
-NX_OP_TYPES = ["QuantizeLinear", "DynamicQuantizeLinear", "ConvInteger", "QLinearMatMul",
+NX_OP_TYPES = ["QuantizeLinear", "ConvInteger", "QLinearMatMul",
                "QLinearConv", "QLinearAdd", "QLinearMul"]
 
 
@@ -330,9 +331,34 @@ def _op_matmul_integer(node, inputs):
     return y
 
 
+# ---------------------------------------------------------------- DynamicQuantizeLinear
+
+
+def _op_dynamic_quantize_linear(node, inputs):
+    """[y, scale, zero] of quantized.ex:94-103: u8 y of x's shape, f32 scale and u8 zero point
+    as scalars, all on the device."""
+    (x,) = inputs[:1]
+    ctx = _ctx_of(x)
+    if _type_of(x) != "f32":
+        raise ArgumentError(f"DynamicQuantizeLinear takes f32 values, got {_type_of(x)}")
+    x_t, own = _device(ctx, x)
+    try:
+        y = ctx.empty(tuple(_shape_of(x)), "u8")
+        scale = ctx.empty((), "f32")
+        zero = ctx.empty((), "u8")
+        ctx.check(lib().tmh_dynamic_quantize_linear(ctx.handle, x_t.ptr, x_t.tmh_dtype, x_t.size, y.ptr, scale.ptr,
+                                                    zero.ptr, None))
+    finally:
+        if own:
+            ctx.synchronize()
+            x_t.free()
+    return [y, scale, zero]
+
+
 _HANDLERS = {
     "MatMulNBits": _op_matmul_nbits,
     "GatherBlockQuantized": _op_gather_block_quantized,
     "DequantizeLinear": _op_dequantize_linear,
     "MatMulInteger": _op_matmul_integer,
+    "DynamicQuantizeLinear": _op_dynamic_quantize_linear,
 }
