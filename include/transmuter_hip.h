@@ -249,6 +249,44 @@ int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d
 int tmh_dynamic_quantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t n, void* d_y,
                                 void* d_scale, void* d_zero, void* stream);
 
+/* ------------------------------------------------------------------ QMoE */
+
+/* activation_type of QMoE (moe.ex:176-196) */
+enum { TMH_ACT_RELU = 0, TMH_ACT_GELU = 1, TMH_ACT_SILU = 2, TMH_ACT_IDENTITY = 3, TMH_ACT_SWIGLU = 4 };
+
+/*
+ * The expert weights of one QMoE input (fc1, fc2 or fc3) as one packed weight of E*N rows,
+ * dequantized as MoE.dequant/6 does (moe.ex:216-253): (q - zero) * scale in weight_dtype (the
+ * QMoE input's type).
+ *  h_w [E, N, K*bits/8] U8, values low bits first
+ *  block_size > 0 with scales: scales [E, N, blocks] (blocks * block_size >= K), zero points
+ *    NULL or [E, N, ceil(blocks*bits/8)] packed along the blocks
+ *  block_size 0 (or no scales): scales NULL (no scaling) or [E, N] / [E, N, 1], zero points NULL
+ *    or [E, ceil(N*bits/8)] packed along N; absent zero points are 2^(bits-1)
+ * N must be a multiple of 16; bits 2, 4 or 8. Free with tmh_weight_free.
+ */
+int tmh_weight_upload_qmoe(tmh_ctx* ctx, const uint8_t* h_w, size_t w_bytes, const void* h_scales,
+                           int scales_dtype, size_t scales_count, const uint8_t* h_zero_points,
+                           size_t zp_bytes, int64_t E, int64_t N, int64_t K, int bits, int64_t block_size,
+                           int weight_dtype, tmh_weight** out);
+
+/*
+ * QMoE (com.microsoft; moe.ex:42-61 and experts/4 at :64-102): each token's k largest router
+ * values (lower expert index first among equals) and a softmax over them weight the outputs of
+ * its experts: fc2(act(fc1(x) + b1[, fc3(x) + b3]) ) + b2, summed over the token's slots.
+ *  d_x [T, H] of x_dtype; d_router [T, E] float; fc1 [E*N1, H]; fc2 [E*H, inter]; fc3 NULL or
+ *  as fc1 (swiglu with swiglu_fusion 0); biases NULL or [E, N1] / [E, H] of bias_dtype.
+ *  activation TMH_ACT_*; swiglu: fusion 0 with fc3 (gate fc1, linear fc3), 1 (or 0 without fc3)
+ *  interleaved pairs, 2 halves; g * sigmoid(alpha * g) * (l + beta), g and l limited by limit
+ *  when it is not 0.
+ *  d_y [T, H] of x_dtype. Uses the context's workspace, which grows outside graph capture only.
+ */
+int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, const void* d_router,
+             int router_dtype, int64_t E, int k, const tmh_weight* fc1, const void* d_fc1_bias,
+             const tmh_weight* fc2, const void* d_fc2_bias, const tmh_weight* fc3, const void* d_fc3_bias,
+             int bias_dtype, int activation, int swiglu_fusion, float alpha, float beta, float limit,
+             void* d_y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

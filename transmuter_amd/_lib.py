@@ -22,6 +22,8 @@ F32, U8, S8, U16, S16, S32, S64, F16, BF16 = 1, 2, 3, 4, 5, 6, 7, 10, 16
 ZP_NONE, ZP_PACKED, ZP_FLOAT = 0, 1, 2
 # tmh_qparam_mode
 QPARAM_TENSOR, QPARAM_AXIS, QPARAM_BLOCKED = 0, 1, 2
+# QMoE activation_type
+ACTIVATIONS = {"relu": 0, "gelu": 1, "silu": 2, "identity": 3, "swiglu": 4}
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -66,6 +68,10 @@ SIGNATURES = {
     "tmh_matmul_integer": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i, _vp,
                                 _vp]),
     "tmh_dynamic_quantize_linear": (_i, [_vp, _vp, _i, _i64, _vp, _vp, _vp, _vp]),
+    "tmh_weight_upload_qmoe": (_i, [_vp, _vp, _sz, _vp, _i, _sz, _vp, _sz, _i64, _i64, _i64, _i, _i64, _i,
+                                    ctypes.POINTER(_vp)]),
+    "tmh_qmoe": (_i, [_vp, _vp, _i, _i64, _i64, _vp, _i, _i64, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,
+                      ctypes.c_float, ctypes.c_float, ctypes.c_float, _vp, _vp]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,682 @@
+// QMoE (com.microsoft) on gfx950: routing, grouping by expert, grouped expert GEMMs over
+// packed weights, activation and the weighted sum over each token's experts.
+//
+// Reference (georgeguimaraes/transmuter):
+//   lib/transmuter/ops/moe.ex:42-61    QMoE: top-k router values, a softmax over those k values,
+//                                      experts dequantized as (q - zero) * scale
+//   lib/transmuter/ops/moe.ex:64-102   experts/4: fc1 (and fc3), activation, fc2, bias of the
+//                                      row's expert, weighted sum over the slots (weight 0 adds 0)
+//   lib/transmuter/ops/moe.ex:108-138  route/3: the routed rows; the dense variant (every expert
+//                                      on every token, weight 0 for the unselected) sums the same
+//   lib/transmuter/ops/moe.ex:158-165  topk/2: a stable descending sort (lower index first)
+//   lib/transmuter/ops/moe.ex:176-206  activate/2 and swiglu_gate/3
+//   lib/transmuter/ops/moe.ex:216-253  dequant/6: block-wise or per-row scales and zero points
+//
+// Layout on the device: the experts of one weight are one tmh_weight of E*N rows (expert e owns
+// rows e*N.. and 16-row tiles e*N/16..). A call sorts its T*k (token, slot) rows by expert, runs
+// each expert's rows against its tiles in work items of up to 32 rows, and keeps every
+// intermediate in expert order; the final sum reads them back per token, slot by slot.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <vector>
+
+#include "tmh_device.h"
+#include "tmh_internal.h"
+
+using namespace tmh;
+
+namespace {
+
+constexpr int kMoeRows = 32;  // rows per work item: two 16-row MFMA tiles
+
+// ------------------------------------------------------------------ routing and grouping
+
+__global__ __launch_bounds__(256) void k_moe_zero(int* __restrict__ counts, int E) {
+  for (int e = threadIdx.x; e < E; e += blockDim.x) counts[e] = 0;
+}
+
+// One wavefront per token: the k largest router values (lower index first among equals), a
+// softmax over them in f32, and the per-expert row counts. Lane l holds experts l, l+64, ...
+__global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ router, int router_dt, int T, int E, int k,
+                                                   int* __restrict__ topi, float* __restrict__ topw,
+                                                   int* __restrict__ counts) {
+  constexpr int kPerLane = 16;  // E <= 1024
+  constexpr int kNone = 0x7fffffff;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float v[kPerLane];
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? load_float_rt(router, router_dt, static_cast<int64_t>(t) * E + e) : 0.f;
+  }
+  uint32_t taken = 0;
+  float mx = -INFINITY;
+  for (int j = 0; j < k; ++j) {
+    float best = 0.f;
+    int bi = kNone;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && !(taken >> i & 1u) && (bi == kNone || v[i] > best)) {
+        best = v[i];
+        bi = e;
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ob = __shfl_xor(best, off);
+      const int oi = __shfl_xor(bi, off);
+      if (oi != kNone && (bi == kNone || ob > best || (ob == best && oi < bi))) {
+        best = ob;
+        bi = oi;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i)
+      if (lane + 64 * i == bi) taken |= 1u << i;
+    mx = fmaxf(mx, best);
+    if (lane == 0) {
+      topi[t * k + j] = bi;
+      topw[t * k + j] = best;
+    }
+  }
+  if (lane != 0) return;
+  float sum = 0.f;
+  for (int j = 0; j < k; ++j) sum += expf(topw[t * k + j] - mx);
+  for (int j = 0; j < k; ++j) {
+    topw[t * k + j] = expf(topw[t * k + j] - mx) / sum;
+    atomicAdd(&counts[topi[t * k + j]], 1);
+  }
+}
+
+// One workgroup: expert offsets (exclusive prefix of the counts), the list of work items
+// (expert << 16 | item of the expert), and the fill counters of the scatter.
+__global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ counts, int E, int* __restrict__ offsets,
+                                                   int* __restrict__ fill, int* __restrict__ items,
+                                                   int* __restrict__ n_items) {
+  __shared__ int rows_s[1024], items_s[1024];
+  const int e = threadIdx.x;
+  const int c = e < E ? counts[e] : 0;
+  rows_s[e] = c;
+  items_s[e] = (c + kMoeRows - 1) / kMoeRows;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {  // inclusive scans
+    const int r = e >= off ? rows_s[e - off] : 0;
+    const int it = e >= off ? items_s[e - off] : 0;
+    __syncthreads();
+    rows_s[e] += r;
+    items_s[e] += it;
+    __syncthreads();
+  }
+  if (e < E) {
+    offsets[e] = rows_s[e] - c;
+    fill[e] = 0;
+    const int nb = (c + kMoeRows - 1) / kMoeRows;
+    const int first = items_s[e] - nb;
+    for (int b = 0; b < nb; ++b) items[first + b] = (e << 16) | b;
+  }
+  if (e == 1023) *n_items = items_s[1023];
+}
+
+// Row position of every (token, slot) in expert order, and its inverse.
+__global__ __launch_bounds__(256) void k_moe_scatter(const int* __restrict__ topi, int Tk, const int* __restrict__ offsets,
+                                                     int* __restrict__ fill, int* __restrict__ perm,
+                                                     int* __restrict__ slot_pos) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= Tk) return;
+  const int e = topi[idx];
+  const int pos = offsets[e] + atomicAdd(&fill[e], 1);
+  perm[pos] = idx;
+  slot_pos[idx] = pos;
+}
+
+// ------------------------------------------------------------------ grouped expert GEMMs
+
+// The rows of a work item: expert, first sorted row, row count.
+struct MoeItem {
+  int e, row0, rows;
+};
+
+__device__ __forceinline__ MoeItem moe_item(const int* items, int item, const int* offsets, const int* counts) {
+  const int it = items[item];
+  const int e = it >> 16, b = it & 0xffff;
+  return MoeItem{e, offsets[e] + b * kMoeRows, min(kMoeRows, counts[e] - b * kMoeRows)};
+}
+
+// out[row][n] = sum_k A[src(row)][k] * W_e[n][k] for the up to 32 sorted rows of one work item
+// and TN 16-column tiles of its expert, f16 in and out with f32 sums (v_mfma_f32_16x16x32_f16).
+// src(row) = perm[row] / perm_div when perm is given (rows gathered from the tokens), else row.
+// The wavefronts split the chunks of K and add their sums through LDS.
+template <int BITS, bool HAS_ZP, bool SPLIT, int TN>
+__global__ __launch_bounds__(1024) void k_moe_gemm_f16(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp, int ntiles,
+    int nchunks, int nbc, int bsc_shift, int tiles_per_expert, const _Float16* __restrict__ A, int a_rows, int lda,
+    const int* __restrict__ perm, int perm_div, const int* __restrict__ items, const int* __restrict__ n_items,
+    const int* __restrict__ offsets, const int* __restrict__ counts, _Float16* __restrict__ out, int ldo) {
+  constexpr int CW = 512 / BITS;
+  constexpr int GW = CW / 4;
+  constexpr int STEPS = GW / 8;
+  constexpr int NJ = SPLIT ? STEPS : 1;
+  extern __shared__ float4_t red[];  // nwaves * 2 * TN * 64
+  if (static_cast<int>(blockIdx.y) >= *n_items) return;
+  const MoeItem it = moe_item(items, blockIdx.y, offsets, counts);
+  const int nwaves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t nch = static_cast<uint32_t>(nchunks);
+  const uint32_t n_params = static_cast<uint32_t>(ntiles) * nch * nbc * 16;
+  const auto q_rsrc = buffer_rsrc(qt, static_cast<uint32_t>(ntiles) * nch * 1024);
+  const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+  const auto a_rsrc = buffer_rsrc(A, static_cast<uint32_t>(a_rows) * lda * 2);
+  const int lt0 = blockIdx.x * TN;  // first tile within the expert
+  uint32_t tile[TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+    tile[tn] = lt0 + tn < tiles_per_expert ? static_cast<uint32_t>(it.e * tiles_per_expert + lt0 + tn)
+                                           : static_cast<uint32_t>(ntiles);  // past the end: zeros
+  uint32_t a_row[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int i = mt * 16 + r;
+    const int src = i < it.rows ? (perm ? perm[it.row0 + i] / perm_div : it.row0 + i) : -1;
+    a_row[mt] = src >= 0 ? static_cast<uint32_t>(src) * lda * 2 : 0x80000000u;
+  }
+  float4_t acc[2][TN];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[mt][tn] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (uint32_t c = wave; c < nch; c += nwaves) {
+    uint4_t w[TN];
+    uint32_t sv[TN][NJ], zv[TN][NJ];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      w[tn] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, (tile[tn] * nch * 64 + lane) * 16, c * 1024, 0);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const uint32_t e = ((tile[tn] * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
+        sv[tn][j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, 0, 0);
+        if constexpr (HAS_ZP) zv[tn][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0);
+      }
+    }
+    half8_t af[2][STEPS];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < STEPS; ++i) {
+        const uint32_t k = c * CW + g * GW + 8 * i;
+        const uint32_t off = k < static_cast<uint32_t>(lda) ? a_row[mt] + k * 2 : 0x80000000u;
+        af[mt][i] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
+      }
+#pragma unroll
+    for (int i = 0; i < STEPS; ++i) {
+      const int j = SPLIT ? i : 0;
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t zq = HAS_ZP ? 0x6400u + zv[tn][j] : 0x6400u + (1u << (BITS - 1));
+        const half8_t b = unpack_step<BITS>(w[tn], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
+                                            __builtin_bit_cast(half2_t, sv[tn][j] | (sv[tn][j] << 16)));
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          acc[mt][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[mt][i], acc[mt][tn], 0, 0, 0);
+      }
+    }
+  }
+  if (nwaves > 1) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) red[((wave * 2 + mt) * TN + tn) * 64 + lane] = acc[mt][tn];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int i = mt * 16 + r;
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      if (nwaves > 1) {
+        if ((mt * TN + tn) % nwaves != wave) continue;
+        acc[mt][tn] = red[(mt * TN + tn) * 64 + lane];
+        for (int w2 = 1; w2 < nwaves; ++w2) acc[mt][tn] += red[((w2 * 2 + mt) * TN + tn) * 64 + lane];
+      }
+      if (i >= it.rows || lt0 + tn >= tiles_per_expert) continue;
+      const float4_t v = acc[mt][tn];
+      const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
+      const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+      _Float16* dst = out + static_cast<int64_t>(it.row0 + i) * ldo + (lt0 + tn) * 16 + 4 * g;
+      *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+    }
+  }
+}
+
+// The same product for any float types (A in a_dt, weights dequantized in WDT, out in out_dt):
+// one 16-column tile per workgroup, the four wavefronts splitting the chunks of K.
+template <int BITS, int WDT, int ZK>
+__global__ __launch_bounds__(256) void k_moe_gemm_general(
+    const uint4_t* __restrict__ qt, const void* __restrict__ sc, const void* __restrict__ zp, int nchunks, int nbc,
+    int bsc_shift, int tiles_per_expert, int K, const void* __restrict__ A, int a_dt, int lda,
+    const int* __restrict__ perm, int perm_div, const int* __restrict__ items, const int* __restrict__ n_items,
+    const int* __restrict__ offsets, const int* __restrict__ counts, void* __restrict__ out, int out_dt, int ldo) {
+  constexpr int CW = 512 / BITS;
+  constexpr int GW = CW / 4;
+  constexpr int PER_WORD = 32 / BITS;
+  __shared__ float red[4][kMoeRows][16];
+  if (static_cast<int>(blockIdx.y) >= *n_items) return;
+  const MoeItem it = moe_item(items, blockIdx.y, offsets, counts);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t t = static_cast<int64_t>(it.e) * tiles_per_expert + blockIdx.x;
+  int64_t src[kMoeRows];
+#pragma unroll
+  for (int i = 0; i < kMoeRows; ++i)
+    src[i] = i < it.rows ? (perm ? perm[it.row0 + i] / perm_div : it.row0 + i) : 0;
+  float acc[kMoeRows];
+#pragma unroll
+  for (int i = 0; i < kMoeRows; ++i) acc[i] = 0.f;
+  for (int c = wave; c < nchunks; c += 4) {
+    const int64_t tc = t * nchunks + c;
+    const uint4_t w = qt[tc * 64 + lane];
+    for (int e = 0; e < GW; ++e) {
+      const int k = c * CW + g * GW + e;
+      if (k >= K) break;
+      const int64_t p = (tc * nbc + ((g * GW + e) >> bsc_shift)) * 16 + r;
+      const float s = load_as_f32<WDT>(sc, p);
+      float z;
+      if constexpr (ZK == TMH_ZP_PACKED) {
+        z = static_cast<float>(static_cast<const uint8_t*>(zp)[p]);
+      } else {
+        z = static_cast<float>(1 << (BITS - 1));
+      }
+      const float wv = dequant_value<WDT>(static_cast<float>(word_value<BITS>(w[e / PER_WORD], e % PER_WORD)), z, s);
+#pragma unroll
+      for (int i = 0; i < kMoeRows; ++i)
+        if (i < it.rows) acc[i] = fmaf(load_float_rt(A, a_dt, src[i] * lda + k), wv, acc[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kMoeRows; ++i) {
+    float v = acc[i];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (g == 0) red[wave][i][r] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x >> 4; i < it.rows; i += 16) {
+    const int col = threadIdx.x & 15;
+    const float v = red[0][i][col] + red[1][i][col] + red[2][i][col] + red[3][i][col];
+    store_float_rt(out, out_dt, static_cast<int64_t>(it.row0 + i) * ldo + blockIdx.x * 16 + col, v);
+  }
+}
+
+// ------------------------------------------------------------------ activation and sum
+
+enum : int { ACT_RELU = 0, ACT_GELU = 1, ACT_SILU = 2, ACT_IDENTITY = 3, ACT_SWIGLU = 4 };
+
+template <int DT>
+__device__ __forceinline__ float rt(float x) {
+  return round_to<DT>(x);
+}
+
+template <int DT>
+__device__ __forceinline__ float sigmoid_t(float x) {
+  return rt<DT>(1.f / (1.f + expf(-x)));
+}
+
+// swiglu_gate/3 (moe.ex:199-206): g * sigmoid(alpha * g) * (l + beta), g and l limited first
+// when limit is not 0; each operation rounds to the input type.
+template <int DT>
+__device__ __forceinline__ float swiglu(float g, float l, float alpha, float beta, float limit) {
+  if (limit != 0.f) {
+    g = fminf(g, limit);
+    l = fminf(fmaxf(l, -limit), limit);
+  }
+  const float sg = sigmoid_t<DT>(rt<DT>(alpha * g));
+  return rt<DT>(rt<DT>(g * sg) * rt<DT>(l + beta));
+}
+
+// Activated rows: hact[row][c] from h1 (and h3), with the biases of the row's expert.
+// fusion (for swiglu): 0 with h3 = gate h1, linear h3; 2 = halves of h1; otherwise interleaved.
+template <int DT>
+__global__ __launch_bounds__(256) void k_moe_activate(const void* __restrict__ h1, const void* __restrict__ h3, int n1,
+                                                      int inter, const void* __restrict__ b1,
+                                                      const void* __restrict__ b3, int bias_dt,
+                                                      const int* __restrict__ perm, const int* __restrict__ topi,
+                                                      int Tk, int act, int fusion, float alpha, float beta, float limit,
+                                                      void* __restrict__ hact) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int width = act == ACT_SWIGLU ? inter : n1;
+  if (idx >= static_cast<int64_t>(Tk) * width) return;
+  const int row = static_cast<int>(idx / width), c = static_cast<int>(idx - static_cast<int64_t>(row) * width);
+  const int e = topi[perm[row]];
+  auto h = [&](const void* src, const void* bias, int col) -> float {
+    float v = load_as_f32<DT>(src, static_cast<int64_t>(row) * n1 + col);
+    if (bias) v = rt<DT>(v + load_float_rt(bias, bias_dt, static_cast<int64_t>(e) * n1 + col));
+    return v;
+  };
+  float y;
+  if (act == ACT_SWIGLU) {
+    float g, l;
+    if (h3) {
+      g = h(h1, b1, c);
+      l = h(h3, b3, c);
+    } else if (fusion == 2) {
+      g = h(h1, b1, c);
+      l = h(h1, b1, inter + c);
+    } else {
+      g = h(h1, b1, 2 * c);
+      l = h(h1, b1, 2 * c + 1);
+    }
+    y = swiglu<DT>(g, l, alpha, beta, limit);
+  } else {
+    const float v = h(h1, b1, c);
+    if (act == ACT_RELU) {
+      y = fmaxf(v, 0.f);
+    } else if (act == ACT_SILU) {
+      y = rt<DT>(v * sigmoid_t<DT>(v));
+    } else if (act == ACT_GELU) {
+      y = rt<DT>(v * rt<DT>(0.5f * rt<DT>(1.f + rt<DT>(erff(rt<DT>(v * 0.70710678118654752f))))));
+    } else {
+      y = v;
+    }
+  }
+  store_as<DT>(hact, idx, y);
+}
+
+// y[t][h] = sum over the token's slots j of weight_j * (o[row of (t, j)][h] + fc2 bias), in slot
+// order; a slot of weight 0 adds 0.
+template <int DT>
+__global__ __launch_bounds__(256) void k_moe_combine(const void* __restrict__ o, int H, const void* __restrict__ b2,
+                                                     int bias_dt, const int* __restrict__ topi,
+                                                     const float* __restrict__ topw, const int* __restrict__ slot_pos,
+                                                     int T, int k, void* __restrict__ y) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(T) * H) return;
+  const int t = static_cast<int>(idx / H), hc = static_cast<int>(idx - static_cast<int64_t>(t) * H);
+  float sum = 0.f;
+  for (int j = 0; j < k; ++j) {
+    const float wgt = rt<DT>(topw[t * k + j]);
+    if (wgt == 0.f) continue;
+    float v = load_as_f32<DT>(o, static_cast<int64_t>(slot_pos[t * k + j]) * H + hc);
+    if (b2) v = rt<DT>(v + load_float_rt(b2, bias_dt, static_cast<int64_t>(topi[t * k + j]) * H + hc));
+    sum = rt<DT>(sum + rt<DT>(v * wgt));
+  }
+  store_as<DT>(y, idx, sum);
+}
+
+// ------------------------------------------------------------------ launchers
+
+int bsc_shift_moe(const tmh_weight* w) {
+  int cw = 512 / w->bits, bs = std::min(w->block_size, cw), s = 0;
+  while ((1 << s) < bs) ++s;
+  return s;
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT>
+void launch_moe_f16_v(const tmh_weight* w, int tpe, const void* A, int a_rows, int lda, const int* perm, int perm_div,
+                      const int* items, const int* n_items, int max_items, const int* offsets, const int* counts,
+                      void* out, int ldo, hipStream_t s) {
+  constexpr int TN = 2;
+  const int waves = static_cast<int>(std::min<int64_t>(8, w->nchunks));
+  const dim3 grid(static_cast<unsigned>((tpe + TN - 1) / TN), static_cast<unsigned>(max_items));
+  const size_t lds = waves > 1 ? static_cast<size_t>(waves) * 2 * TN * 64 * sizeof(float4_t) : 0;
+  k_moe_gemm_f16<BITS, HAS_ZP, SPLIT, TN><<<grid, 64 * waves, lds, s>>>(
+      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+      static_cast<const uint8_t*>(w->d_zero), static_cast<int>(w->ntiles), static_cast<int>(w->nchunks), w->nbc,
+      bsc_shift_moe(w), tpe, static_cast<const _Float16*>(A), a_rows, lda, perm, perm_div, items, n_items, offsets,
+      counts, static_cast<_Float16*>(out), ldo);
+}
+
+template <int BITS>
+void launch_moe_f16(const tmh_weight* w, int tpe, const void* A, int a_rows, int lda, const int* perm, int perm_div,
+                    const int* items, const int* n_items, int max_items, const int* offsets, const int* counts,
+                    void* out, int ldo, hipStream_t s) {
+  const bool zp = w->zp_kind == TMH_ZP_PACKED;
+  const bool split = w->block_size < (512 / BITS) / 4;
+#define TMH_MOE_F16(Z, S) \
+  launch_moe_f16_v<BITS, Z, S>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, s)
+  if (zp && split) TMH_MOE_F16(true, true);
+  else if (zp) TMH_MOE_F16(true, false);
+  else if (split) TMH_MOE_F16(false, true);
+  else TMH_MOE_F16(false, false);
+#undef TMH_MOE_F16
+}
+
+template <int BITS, int WDT>
+void launch_moe_general_w(const tmh_weight* w, int tpe, const void* A, int a_dt, int lda, const int* perm, int perm_div,
+                          const int* items, const int* n_items, int max_items, const int* offsets, const int* counts,
+                          void* out, int out_dt, int ldo, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(tpe), static_cast<unsigned>(max_items));
+  const auto* qt = reinterpret_cast<const uint4_t*>(w->d_q);
+  const int sh = bsc_shift_moe(w);
+  if (w->zp_kind == TMH_ZP_PACKED)
+    k_moe_gemm_general<BITS, WDT, TMH_ZP_PACKED><<<grid, 256, 0, s>>>(
+        qt, w->d_scale, w->d_zero, static_cast<int>(w->nchunks), w->nbc, sh, tpe, static_cast<int>(w->K), A, a_dt, lda,
+        perm, perm_div, items, n_items, offsets, counts, out, out_dt, ldo);
+  else
+    k_moe_gemm_general<BITS, WDT, TMH_ZP_NONE><<<grid, 256, 0, s>>>(
+        qt, w->d_scale, w->d_zero, static_cast<int>(w->nchunks), w->nbc, sh, tpe, static_cast<int>(w->K), A, a_dt, lda,
+        perm, perm_div, items, n_items, offsets, counts, out, out_dt, ldo);
+}
+
+template <int BITS>
+void launch_moe_general(const tmh_weight* w, int tpe, const void* A, int a_dt, int lda, const int* perm, int perm_div,
+                        const int* items, const int* n_items, int max_items, const int* offsets, const int* counts,
+                        void* out, int out_dt, int ldo, hipStream_t s) {
+  switch (w->wdtype) {
+    case TMH_F16:
+      launch_moe_general_w<BITS, DT_F16>(w, tpe, A, a_dt, lda, perm, perm_div, items, n_items, max_items, offsets,
+                                         counts, out, out_dt, ldo, s);
+      break;
+    case TMH_BF16:
+      launch_moe_general_w<BITS, DT_BF16>(w, tpe, A, a_dt, lda, perm, perm_div, items, n_items, max_items, offsets,
+                                          counts, out, out_dt, ldo, s);
+      break;
+    default:
+      launch_moe_general_w<BITS, DT_F32>(w, tpe, A, a_dt, lda, perm, perm_div, items, n_items, max_items, offsets,
+                                         counts, out, out_dt, ldo, s);
+  }
+}
+
+// One grouped product: rows (gathered through perm when given) times each row's expert.
+void moe_gemm(const tmh_weight* w, int experts, const void* A, int a_dt, int a_rows, int lda, const int* perm,
+              int perm_div, const int* items, const int* n_items, int max_items, const int* offsets,
+              const int* counts, void* out, int ldo, hipStream_t s) {
+  const int tpe = static_cast<int>(w->N / experts / 16);
+  const bool fast = a_dt == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT && lda % 8 == 0 &&
+                    reinterpret_cast<uintptr_t>(A) % 16 == 0 && static_cast<int64_t>(a_rows) * lda * 2 < (int64_t(1) << 31) &&
+                    (w->ntiles + 1) * w->nchunks * 1024 < (int64_t(1) << 31);
+  if (fast) {
+    switch (w->bits) {
+      case 2: launch_moe_f16<2>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, s); break;
+      case 4: launch_moe_f16<4>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, s); break;
+      default: launch_moe_f16<8>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, s);
+    }
+    return;
+  }
+  switch (w->bits) {
+    case 2: launch_moe_general<2>(w, tpe, A, a_dt, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, a_dt, ldo, s); break;
+    case 4: launch_moe_general<4>(w, tpe, A, a_dt, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, a_dt, ldo, s); break;
+    default: launch_moe_general<8>(w, tpe, A, a_dt, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, a_dt, ldo, s);
+  }
+}
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+}  // namespace
+
+extern "C" {
+
+int tmh_weight_upload_qmoe(tmh_ctx* ctx, const uint8_t* h_w, size_t w_bytes, const void* h_scales, int scales_dtype,
+                           size_t scales_count, const uint8_t* h_zero_points, size_t zp_bytes, int64_t E, int64_t N,
+                           int64_t K, int bits, int64_t block_size, int weight_dtype, tmh_weight** out) {
+  if (!ctx) return fail(nullptr, TMH_ERR_INVALID, "the context is NULL");
+  if (!out) return fail(ctx, TMH_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  if (bits != 2 && bits != 4 && bits != 8)
+    return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE expert_weight_bits must be 2, 4 or 8, got %d", bits);
+  if (E <= 0 || N <= 0 || K <= 0) return fail(ctx, TMH_ERR_INVALID, "QMoE weights must have positive sizes");
+  if (N % 16 != 0) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE expert rows (%lld) must be a multiple of 16", (long long)N);
+  if ((K * bits) % 8 != 0) return fail(ctx, TMH_ERR_INVALID, "QMoE rows of %lld %d-bit values are not whole bytes", (long long)K, bits);
+  const int64_t row_bytes = K * bits / 8;
+  if (!h_w || w_bytes != static_cast<size_t>(E * N * row_bytes))
+    return fail(ctx, TMH_ERR_INVALID, "QMoE weights hold %zu bytes; %lld expected", w_bytes, (long long)(E * N * row_bytes));
+  const int64_t rows = E * N;
+  const bool blockwise = block_size > 0 && h_scales;
+  int64_t bs, blocks;  // block size and blocks per row as given
+  if (blockwise) {
+    if (block_size < 16 || (block_size & (block_size - 1)))
+      return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE block_size must be a power of two of at least 16, got %lld", (long long)block_size);
+    if (scales_count % rows != 0) return fail(ctx, TMH_ERR_INVALID, "QMoE scales do not split into %lld rows", (long long)rows);
+    bs = block_size;
+    blocks = static_cast<int64_t>(scales_count) / rows;  // K pads to whole blocks (moe.ex:225-233)
+    if (blocks * bs < K) return fail(ctx, TMH_ERR_INVALID, "QMoE has %lld blocks of %lld for K=%lld", (long long)blocks, (long long)bs, (long long)K);
+  } else {
+    if (h_scales && scales_count != static_cast<size_t>(rows))
+      return fail(ctx, TMH_ERR_INVALID, "QMoE per-row scales hold %zu values; %lld expected", scales_count, (long long)rows);
+    bs = 512 / bits;  // one scale and zero point per chunk, copied from the row's
+    blocks = (K + bs - 1) / bs;
+  }
+  const int64_t kb = (K + bs - 1) / bs;  // blocks that hold values of the row
+  const int64_t bbytes = bs * bits / 8;
+  // B as MatMulNBits lays it out: [rows, kb, bs*bits/8], zero past K.
+  std::vector<uint8_t> b(static_cast<size_t>(rows * kb * bbytes), 0);
+  for (int64_t rr = 0; rr < rows; ++rr)
+    std::copy_n(h_w + rr * row_bytes, row_bytes, b.begin() + rr * kb * bbytes);
+  const int sdt = h_scales ? scales_dtype : TMH_F32;
+  if (!is_float_dtype(sdt)) return fail(ctx, TMH_ERR_INVALID, "QMoE scales must be float");
+  const size_t ses = static_cast<size_t>(dtype_size(sdt));
+  std::vector<uint8_t> scales(static_cast<size_t>(rows * kb) * ses);
+  const float one = 1.f;
+  for (int64_t rr = 0; rr < rows; ++rr)
+    for (int64_t bl = 0; bl < kb; ++bl) {
+      const uint8_t* src = !h_scales ? reinterpret_cast<const uint8_t*>(&one)
+                           : blockwise ? static_cast<const uint8_t*>(h_scales) + (rr * blocks + bl) * ses
+                                       : static_cast<const uint8_t*>(h_scales) + rr * ses;
+      std::copy_n(src, ses, scales.begin() + (rr * kb + bl) * ses);
+    }
+  // Zero points of every (row, block), then packed as MatMulNBits rows of ceil(kb*bits/8) bytes.
+  const int64_t per = 8 / bits, zrow = (kb * bits + 7) / 8;
+  auto value = [&](const uint8_t* packed, int64_t i) -> uint8_t {
+    return static_cast<uint8_t>((packed[i / per] >> ((i % per) * bits)) & ((1 << bits) - 1));
+  };
+  std::vector<uint8_t> zero;
+  if (h_zero_points) {
+    zero.assign(static_cast<size_t>(rows * zrow), 0);
+    const int64_t in_row = (blocks * bits + 7) / 8, zn = (N + per - 1) / per;
+    const size_t expect = static_cast<size_t>(blockwise ? rows * in_row : E * zn);
+    if (zp_bytes != expect)
+      return fail(ctx, TMH_ERR_INVALID, "QMoE zero points hold %zu bytes; %zu expected", zp_bytes, expect);
+    for (int64_t rr = 0; rr < rows; ++rr) {
+      // Block-wise: {E, N, ceil(blocks*bits/8)} packed along the blocks; per row: {E, N} packed
+      // along N (moe.ex:233-244).
+      const uint8_t z_row = blockwise ? 0 : value(h_zero_points + (rr / N) * zn, rr % N);
+      for (int64_t bl = 0; bl < kb; ++bl) {
+        const uint8_t z = blockwise ? value(h_zero_points + rr * in_row, bl) : z_row;
+        zero[rr * zrow + bl / per] |= static_cast<uint8_t>(z << ((bl % per) * bits));
+      }
+    }
+  }
+  return tmh_weight_upload_nbits(ctx, b.data(), b.size(), scales.data(), sdt, static_cast<size_t>(rows * kb),
+                                 h_zero_points ? zero.data() : nullptr, h_zero_points ? TMH_ZP_PACKED : TMH_ZP_NONE,
+                                 TMH_U8, zero.size(), K, rows, bits, static_cast<int>(bs), weight_dtype, out);
+}
+
+int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, const void* d_router, int router_dtype,
+             int64_t E, int k, const tmh_weight* fc1, const void* d_fc1_bias, const tmh_weight* fc2,
+             const void* d_fc2_bias, const tmh_weight* fc3, const void* d_fc3_bias, int bias_dtype, int activation,
+             int swiglu_fusion, float alpha, float beta, float limit, void* d_y, void* stream) {
+  TMH_TRY(use_device(ctx));
+  if (!is_float_dtype(x_dtype) || !is_float_dtype(router_dtype))
+    return fail(ctx, TMH_ERR_INVALID, "QMoE input and router must be float tensors");
+  if (!fc1 || !fc2) return fail(ctx, TMH_ERR_INVALID, "QMoE needs fc1 and fc2 weights");
+  if (E <= 0 || E > 1024) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE supports 1 to 1024 experts, got %lld", (long long)E);
+  if (k <= 0 || k > 32 || k > E) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE k must be in 1..min(32, experts), got %d", k);
+  if (activation < ACT_RELU || activation > ACT_SWIGLU) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE activation %d", activation);
+  if (T < 0 || H <= 0) return fail(ctx, TMH_ERR_INVALID, "QMoE sizes must be positive");
+  if (fc1->N % E || fc2->N % E) return fail(ctx, TMH_ERR_INVALID, "QMoE weights do not hold %lld experts", (long long)E);
+  const int64_t n1 = fc1->N / E;
+  if (fc1->K != H || fc2->N / E != H)
+    return fail(ctx, TMH_ERR_INVALID, "QMoE fc1 [%lld, %lld] and fc2 rows %lld do not fit hidden size %lld", (long long)n1,
+                (long long)fc1->K, (long long)(fc2->N / E), (long long)H);
+  const bool two = activation == ACT_SWIGLU && swiglu_fusion == 0 && fc3;
+  if (two && (fc3->N != fc1->N || fc3->K != fc1->K)) return fail(ctx, TMH_ERR_INVALID, "QMoE fc3 must match fc1");
+  const int64_t inter = activation == ACT_SWIGLU && !two ? n1 / 2 : n1;
+  if (activation == ACT_SWIGLU && !two && n1 % 2) return fail(ctx, TMH_ERR_INVALID, "QMoE swiglu needs an even fc1 width");
+  if (fc2->K != inter)
+    return fail(ctx, TMH_ERR_INVALID, "QMoE fc2 takes %lld inputs; the activation gives %lld", (long long)fc2->K, (long long)inter);
+  if (fc1->wdtype != x_dtype || fc2->wdtype != x_dtype || (two && fc3->wdtype != x_dtype))
+    return fail(ctx, TMH_ERR_INVALID, "QMoE weights must dequantize in the input's type (%s)", dtype_name(x_dtype));
+  if (T == 0) return TMH_OK;
+  if (!d_x || !d_router || !d_y) return fail(ctx, TMH_ERR_INVALID, "QMoE: NULL pointer");
+  const int64_t tk = T * k;
+  if (tk >= (int64_t(1) << 24)) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE supports fewer than 2^24 routed rows");
+  hipStream_t s = pick_stream(ctx, stream);
+  const size_t es = static_cast<size_t>(dtype_size(x_dtype));
+  const int max_items = static_cast<int>((tk + kMoeRows - 1) / kMoeRows + E);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align256(bytes);
+    return at;
+  };
+  const size_t o_counts = take(E * 4), o_offsets = take(E * 4), o_fill = take(E * 4), o_nitems = take(4);
+  const size_t o_items = take(static_cast<size_t>(max_items) * 4), o_topi = take(tk * 4), o_topw = take(tk * 4);
+  const size_t o_perm = take(tk * 4), o_slot = take(tk * 4);
+  const size_t o_h1 = take(tk * n1 * es), o_h3 = two ? take(tk * n1 * es) : 0;
+  const size_t o_act = take(tk * inter * es), o_o = take(tk * H * es);
+  auto* ws = static_cast<uint8_t*>(workspace(ctx, off, s));
+  if (!ws)
+    return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE needs a %zu-byte workspace; run it once outside graph capture first", off);
+  auto* counts = reinterpret_cast<int*>(ws + o_counts);
+  auto* offsets = reinterpret_cast<int*>(ws + o_offsets);
+  auto* fill = reinterpret_cast<int*>(ws + o_fill);
+  auto* n_items = reinterpret_cast<int*>(ws + o_nitems);
+  auto* items = reinterpret_cast<int*>(ws + o_items);
+  auto* topi = reinterpret_cast<int*>(ws + o_topi);
+  auto* topw = reinterpret_cast<float*>(ws + o_topw);
+  auto* perm = reinterpret_cast<int*>(ws + o_perm);
+  auto* slot_pos = reinterpret_cast<int*>(ws + o_slot);
+  void* h1 = ws + o_h1;
+  void* h3 = two ? ws + o_h3 : nullptr;
+  void* hact = ws + o_act;
+  void* o = ws + o_o;
+  const int ti = static_cast<int>(T), ki = k, ei = static_cast<int>(E), tki = static_cast<int>(tk);
+  k_moe_zero<<<1, 256, 0, s>>>(counts, ei);
+  k_moe_route<<<static_cast<unsigned>((T + 3) / 4), 256, 0, s>>>(d_router, router_dtype, ti, ei, ki, topi, topw, counts);
+  k_moe_plan<<<1, 1024, 0, s>>>(counts, ei, offsets, fill, items, n_items);
+  k_moe_scatter<<<static_cast<unsigned>((tk + 255) / 256), 256, 0, s>>>(topi, tki, offsets, fill, perm, slot_pos);
+  TMH_TRY(check_launch(ctx, "k_moe_scatter"));
+  const int hi = static_cast<int>(H), n1i = static_cast<int>(n1), inti = static_cast<int>(inter);
+  moe_gemm(fc1, ei, d_x, x_dtype, ti, hi, perm, ki, items, n_items, max_items, offsets, counts, h1, n1i, s);
+  if (two) moe_gemm(fc3, ei, d_x, x_dtype, ti, hi, perm, ki, items, n_items, max_items, offsets, counts, h3, n1i, s);
+  TMH_TRY(check_launch(ctx, "k_moe_gemm (fc1)"));
+  const int64_t act_n = tk * (activation == ACT_SWIGLU ? inter : n1);
+  const unsigned act_grid = static_cast<unsigned>((act_n + 255) / 256);
+#define TMH_MOE_ACT(DT)                                                                                                  \
+  k_moe_activate<DT><<<act_grid, 256, 0, s>>>(h1, h3, n1i, inti, d_fc1_bias, two ? d_fc3_bias : nullptr, bias_dtype,    \
+                                              perm, topi, tki, activation, swiglu_fusion, alpha, beta, limit, hact)
+  switch (x_dtype) {
+    case TMH_F16: TMH_MOE_ACT(DT_F16); break;
+    case TMH_BF16: TMH_MOE_ACT(DT_BF16); break;
+    default: TMH_MOE_ACT(DT_F32);
+  }
+#undef TMH_MOE_ACT
+  TMH_TRY(check_launch(ctx, "k_moe_activate"));
+  moe_gemm(fc2, ei, hact, x_dtype, tki, inti, nullptr, 1, items, n_items, max_items, offsets, counts, o, hi, s);
+  TMH_TRY(check_launch(ctx, "k_moe_gemm (fc2)"));
+  const unsigned out_grid = static_cast<unsigned>((T * H + 255) / 256);
+#define TMH_MOE_SUM(DT) \
+  k_moe_combine<DT><<<out_grid, 256, 0, s>>>(o, hi, d_fc2_bias, bias_dtype, topi, topw, slot_pos, ti, ki, d_y)
+  switch (x_dtype) {
+    case TMH_F16: TMH_MOE_SUM(DT_F16); break;
+    case TMH_BF16: TMH_MOE_SUM(DT_BF16); break;
+    default: TMH_MOE_SUM(DT_F32);
+  }
+#undef TMH_MOE_SUM
+  return check_launch(ctx, "k_moe_combine");
+}
+
+}  // extern "C"

@@ -123,48 +123,6 @@ __global__ __launch_bounds__(256) void k_dequant(const uint4_t* __restrict__ qt,
   }
 }
 
-// (x & mask) | orv in one v_and_or_b32: the mask comes from an SGPR and orv from a VGPR, which
-// the one-scalar-operand limit of VOP3 on this target allows (two literals would not).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t orv) {
-  uint32_t out;
-  asm volatile("v_and_or_b32 %0, %1, %2, %3" : "=v"(out) : "v"(x), "s"(mask), "v"(orv));
-  return out;
-}
-
-// Eight exact f16 weights (q - zero) * scale of MFMA step i of a lane, from its 16 bytes.
-// zz holds 1024 + zero (f16, both halves) and ss the scale (both halves); a 16-bit half
-// 0x6400 | q is the f16 number 1024 + q, so (0x6400 | q) - zz is q - zero exactly.
-template <int BITS>
-__device__ __forceinline__ half8_t unpack_step(const uint4_t& w, int i, half2_t zz, half2_t ss) {
-  uint32_t pr[4];
-  if constexpr (BITS == 4) {
-    const uint32_t x = w[i];
-    const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pr[j] = and_or(x >> (4 * j), 0x000F000Fu, magic);
-  } else if constexpr (BITS == 8) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t x = w[2 * i + h];
-      pr[2 * h] = (x & 0xFFu) | ((x << 8) & 0x00FF0000u) | 0x64006400u;
-      pr[2 * h + 1] = ((x >> 16) & 0xFFu) | ((x >> 8) & 0x00FF0000u) | 0x64006400u;
-    }
-  } else {  // 2 bits: step i uses half of word i/2
-    const uint32_t x = w[i >> 1] >> (8 * (i & 1));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pr[j] = ((x >> (2 * j)) & 0x00030003u) | 0x64006400u;
-  }
-  half8_t out;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const half2_t q = __builtin_bit_cast(half2_t, pr[j]);
-    const half2_t wv = (q - zz) * ss;
-    out[2 * j] = wv[0];
-    out[2 * j + 1] = wv[1];
-  }
-  return out;
-}
-
 // Eight f16 values of A row m at columns k..k+7 (zeros outside the matrix).
 __device__ __forceinline__ half8_t load_a8(const _Float16* __restrict__ A, int64_t m, int64_t M,
                                            int64_t k, int64_t K, int64_t lda, bool vec) {
@@ -310,13 +268,6 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(
   gemv_epilogue<MT>(acc, red, nwaves, t, m0, M, N, bias, bias_dt, Y, y_dt, dot_dt, ldy);
 }
 
-// Raw buffer resource over `bytes` bytes: a load whose VGPR offset is at or beyond `bytes`
-// returns zeros, so tiles past N need no address clamps or selects. Every in-range access of
-// these kernels stays inside its buffer.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
-                                           0x00020000);
-}
 
 // Decode GEMV for the common case: M <= 16, f16 A (16-byte aligned rows, K a multiple of 8),
 // f16 weights, f16 Y, no bias. A workgroup covers TN consecutive 16-column tiles; its wavefronts

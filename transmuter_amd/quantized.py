@@ -55,8 +55,8 @@ def attr(node, name: str, default=None):
             return a.f
         if a.type == ATTR_FLOATS:
             return list(a.floats)
-        if a.type == ATTR_STRING:
-            return a.s
+        if a.type == ATTR_STRING:  # an Elixir binary: text
+            return a.s.decode() if isinstance(a.s, bytes) else a.s
         if a.type == ATTR_TENSOR:
             return a.t
     return default
