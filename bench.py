@@ -282,6 +282,49 @@ def large_vocab(ctx, reps, per_graph=21):
             "gather_8x512": {"us": us_g, "gbs": g_bytes / (us_g * 1e-6) / 1e9}}
 
 
+# ---------------------------------------------------------------- quantized MoE
+
+
+def moe_ffn(ctx, reps, per_graph=4):
+    """QMoE at the Qwen3-30B-A3B expert shape: 128 experts, top-8 routing, hidden 2048,
+    intermediate 768, SwiGLU (gate fc1, linear fc3, down fc2), q4 block 32 with f16 scales (no
+    zero points), 512 tokens of f16 activations and N(0,1) router logits; routing, grouping, the
+    three grouped expert products, activation and the weighted sum in each call."""
+    from transmuter_amd._lib import F16, F32, lib
+    from transmuter_amd.moe import ExpertWeight
+
+    rng = np.random.default_rng(6)
+    experts, k, hidden, inter, tokens = 128, 8, 2048, 768, 512
+
+    def expert_weight(n, kk):
+        packed = rng.integers(0, 256, (experts, n, kk // 2), dtype=np.uint8)
+        scales = (np.abs(rng.standard_normal((experts, n, kk // 32), dtype=np.float32)) * 0.01 + 1e-4).astype(np.float16)
+        return ExpertWeight.upload(ctx, packed, scales, None, bits=4, block_size=32, dtype="f16")
+
+    fc1, fc3, fc2 = expert_weight(inter, hidden), expert_weight(inter, hidden), expert_weight(hidden, inter)
+    x = ctx.put(rng.standard_normal((tokens, hidden), dtype=np.float32).astype(np.float16))
+    router = ctx.put(rng.standard_normal((tokens, experts), dtype=np.float32))
+    y = ctx.empty((tokens, hidden), "f16")
+
+    def call():
+        ctx.check(lib().tmh_qmoe(ctx.handle, x.ptr, F16, tokens, hidden, router.ptr, F32, experts, k, fc1.handle, None,
+                                 fc2.handle, None, fc3.handle, None, F16, 4, 0, 1.0, 0.0, 0.0, y.ptr, None))
+
+    call()  # eager first: sizes the workspace before capture
+    ctx.synchronize()
+    g = Graph(ctx, lambda: [call() for _ in range(per_graph)])
+    us = time_graphs(ctx, [g], reps, 2) * 1e3 / (reps * per_graph)
+    g.destroy()
+    for w in (fc1, fc2, fc3):
+        w.free()
+    flops = tokens * k * 2 * 3 * hidden * inter
+    weight_bytes = experts * 3 * hidden * inter * (0.5 + 2 / 32)
+    log(f"moe 128x top-8 2048/768 T={tokens}: {us:.1f} us, {flops / us / 1e6:.1f} TFLOP/s, "
+        f"{tokens / us * 1e6:.0f} tokens/s, {weight_bytes / us / 1e3:.0f} GB/s of expert weights")
+    return {"us": us, "tflops": flops / (us * 1e-6) / 1e12, "tokens_per_s": tokens / (us * 1e-6),
+            "weight_gbs": weight_bytes / (us * 1e-6) / 1e9}
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 
@@ -330,7 +373,7 @@ COPY_BYTES = 256 << 20
 def profile_run(ctx, kind, steps):
     """A short, graph-free run for rocprofv3: `decode` runs the M=1 projection sweep over one
     weight copy plus one 256 MiB device copy (the calibration of the memory counters);
-    `prefill` runs the SmolLM3-3B projections at M=2048."""
+    `prefill` runs the SmolLM3-3B projections at M=2048; `moe` the quantized MoE layer."""
     global USE_GRAPHS
     USE_GRAPHS = False
     if kind == "decode":
@@ -341,6 +384,8 @@ def profile_run(ctx, kind, steps):
         for _ in range(3):
             ctx.check(lib().tmh_copy_2d(ctx.handle, dst.ptr, COPY_BYTES, src.ptr, COPY_BYTES, COPY_BYTES, 1, None))
         ctx.synchronize()
+    elif kind == "moe":
+        moe_ffn(ctx, steps, per_graph=1)
     else:
         prefill(ctx, steps, [2048])
 
@@ -394,7 +439,7 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-graph", action="store_true", help="launch each call on the stream, no HIP graphs")
-    p.add_argument("--profile", choices=["decode", "prefill"], help="a short graph-free run for rocprofv3")
+    p.add_argument("--profile", choices=["decode", "prefill", "moe"], help="a short graph-free run for rocprofv3")
     p.add_argument("--summarize", nargs="*", metavar="PATH",
                    help="print a markdown summary of rocprofv3 output: a kernel_stats.csv, then --pmc directories")
     args = p.parse_args()
@@ -424,6 +469,7 @@ def main():
     if not args.quick:
         extra["prefill"] = prefill(ctx, 20, [256, 2048])
         extra["large_vocab"] = large_vocab(ctx, 50)
+        extra["moe"] = moe_ffn(ctx, 20)
     head = dec[1]
     roofline = {
         "bound": "hbm", "kernel": "k_gemv_lean<4,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
@@ -454,6 +500,7 @@ def main():
         line["prefill_tflops_M2048"] = extra["prefill"][2048]["tflops"]
         line["prefill_frac_M2048"] = extra["prefill"][2048]["tflops"] / MFMA_F16_PEAK_TFLOPS
         line["large_vocab"] = extra["large_vocab"]
+        line["moe"] = extra["moe"]
     ctx.close()
     print(json.dumps(line), flush=True)
 

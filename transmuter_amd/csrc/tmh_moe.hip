@@ -28,108 +28,137 @@ using namespace tmh;
 
 namespace {
 
-constexpr int kMoeRows = 32;  // rows per work item: two 16-row MFMA tiles
+constexpr int kMoeRows = 32;  // rows per work item of the general product
 
 // ------------------------------------------------------------------ routing and grouping
 
-__global__ __launch_bounds__(256) void k_moe_zero(int* __restrict__ counts, int E) {
-  for (int e = threadIdx.x; e < E; e += blockDim.x) counts[e] = 0;
-}
-
 // One wavefront per token: the k largest router values (lower index first among equals), a
-// softmax over them in f32, and the per-expert row counts. Lane l holds experts l, l+64, ...
-__global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ router, int router_dt, int T, int E, int k,
-                                                   int* __restrict__ topi, float* __restrict__ topw,
-                                                   int* __restrict__ counts) {
-  constexpr int kPerLane = 16;  // E <= 1024
-  constexpr int kNone = 0x7fffffff;
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= T) return;
-  float v[kPerLane];
+// softmax over them in f32. The router row goes to LDS; each
+// lane ranks its experts against all of them (rank = how many come first in the stable
+// descending order) and the experts ranked below k are the selection, in rank order.
+template <int RDT>
+__global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ router, int T, int E, int k,
+                                                   int* __restrict__ topi, float* __restrict__ topw) {
+  __shared__ __align__(16) float vals[4][1024];
+  __shared__ float sel_v[4][32];
+  __shared__ int sel_i[4][32];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + w;
+  const bool live = t < T;
+  const int E4 = (E + 3) & ~3;  // padded with -inf, which never comes first
+  if (live)
+    for (int e = lane; e < E4; e += 64) {
+      const float x = e < E ? load_as_f32<RDT>(router, static_cast<int64_t>(t) * E + e) : -INFINITY;
+      vals[w][e] = x != x ? -INFINITY : x;  // NaN ranks as -inf, so the order stays total
+    }
+  __syncthreads();
+  if (live)
+    for (int e = lane; e < E; e += 64) {
+      const float x = vals[w][e];
+      int rank = 0;
+      for (int e2 = 0; e2 < E4; e2 += 4) {
+        const float4_t y = *reinterpret_cast<const float4_t*>(&vals[w][e2]);
 #pragma unroll
-  for (int i = 0; i < kPerLane; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = e < E ? load_float_rt(router, router_dt, static_cast<int64_t>(t) * E + e) : 0.f;
-  }
-  uint32_t taken = 0;
-  float mx = -INFINITY;
-  for (int j = 0; j < k; ++j) {
-    float best = 0.f;
-    int bi = kNone;
-#pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && !(taken >> i & 1u) && (bi == kNone || v[i] > best)) {
-        best = v[i];
-        bi = e;
+        for (int q = 0; q < 4; ++q) rank += (y[q] > x || (y[q] == x && e2 + q < e)) ? 1 : 0;
+      }
+      if (rank < k) {
+        sel_v[w][rank] = x;
+        sel_i[w][rank] = e;
       }
     }
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ob = __shfl_xor(best, off);
-      const int oi = __shfl_xor(bi, off);
-      if (oi != kNone && (bi == kNone || ob > best || (ob == best && oi < bi))) {
-        best = ob;
-        bi = oi;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kPerLane; ++i)
-      if (lane + 64 * i == bi) taken |= 1u << i;
-    mx = fmaxf(mx, best);
-    if (lane == 0) {
-      topi[t * k + j] = bi;
-      topw[t * k + j] = best;
-    }
-  }
-  if (lane != 0) return;
-  float sum = 0.f;
-  for (int j = 0; j < k; ++j) sum += expf(topw[t * k + j] - mx);
-  for (int j = 0; j < k; ++j) {
-    topw[t * k + j] = expf(topw[t * k + j] - mx) / sum;
-    atomicAdd(&counts[topi[t * k + j]], 1);
+  __syncthreads();
+  if (!live) return;
+  const float mx = sel_v[w][0];
+  const float ex = lane < k ? expf(sel_v[w][lane] - mx) : 0.f;
+  float sum = ex;
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if (lane < k) {
+    topi[t * k + lane] = sel_i[w][lane];
+    topw[t * k + lane] = ex / sum;
   }
 }
 
-// One workgroup: expert offsets (exclusive prefix of the counts), the list of work items
-// (expert << 16 | item of the expert), and the fill counters of the scatter.
-__global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ counts, int E, int* __restrict__ offsets,
-                                                   int* __restrict__ fill, int* __restrict__ items,
-                                                   int* __restrict__ n_items) {
-  __shared__ int rows_s[1024], items_s[1024];
+// One workgroup: rows per expert, expert offsets (exclusive prefix of the counts), the list of work items
+// (expert << 16 | item of the expert, `rows` rows each), and the position of every (token,
+// slot) row in expert order (perm) with its inverse (slot_pos).
+__global__ __launch_bounds__(1024) void k_moe_plan(int* __restrict__ counts, int E, int rows, const int* __restrict__ topi,
+                                                   int Tk, int* __restrict__ offsets, int* __restrict__ items,
+                                                   int* __restrict__ n_items, int* __restrict__ perm,
+                                                   int* __restrict__ slot_pos) {
+  __shared__ int rows_s[1024], items_s[1024], fill[1024];
   const int e = threadIdx.x;
-  const int c = e < E ? counts[e] : 0;
-  rows_s[e] = c;
-  items_s[e] = (c + kMoeRows - 1) / kMoeRows;
+  fill[e] = 0;
   __syncthreads();
+  for (int idx = threadIdx.x; idx < Tk; idx += blockDim.x) atomicAdd(&fill[topi[idx]], 1);
+  __syncthreads();
+  const int c = fill[e];
+  if (e < E) counts[e] = c;
+  rows_s[e] = c;
+  items_s[e] = (c + rows - 1) / rows;
+  __syncthreads();
+  fill[e] = 0;
   for (int off = 1; off < 1024; off <<= 1) {  // inclusive scans
-    const int r = e >= off ? rows_s[e - off] : 0;
+    const int rr = e >= off ? rows_s[e - off] : 0;
     const int it = e >= off ? items_s[e - off] : 0;
     __syncthreads();
-    rows_s[e] += r;
+    rows_s[e] += rr;
     items_s[e] += it;
     __syncthreads();
   }
+  const int first_row = rows_s[e] - c;
   if (e < E) {
-    offsets[e] = rows_s[e] - c;
-    fill[e] = 0;
-    const int nb = (c + kMoeRows - 1) / kMoeRows;
+    offsets[e] = first_row;
+    const int nb = (c + rows - 1) / rows;
     const int first = items_s[e] - nb;
     for (int b = 0; b < nb; ++b) items[first + b] = (e << 16) | b;
   }
   if (e == 1023) *n_items = items_s[1023];
+  rows_s[e] = first_row;  // exclusive offsets, read back below
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < Tk; idx += blockDim.x) {
+    const int ex = topi[idx];
+    const int pos = rows_s[ex] + atomicAdd(&fill[ex], 1);
+    perm[pos] = idx;
+    slot_pos[idx] = pos;
+  }
 }
 
-// Row position of every (token, slot) in expert order, and its inverse.
-__global__ __launch_bounds__(256) void k_moe_scatter(const int* __restrict__ topi, int Tk, const int* __restrict__ offsets,
-                                                     int* __restrict__ fill, int* __restrict__ perm,
-                                                     int* __restrict__ slot_pos) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= Tk) return;
-  const int e = topi[idx];
-  const int pos = offsets[e] + atomicAdd(&fill[e], 1);
-  perm[pos] = idx;
-  slot_pos[idx] = pos;
+// ------------------------------------------------------------------ activations
+
+enum : int { ACT_RELU = 0, ACT_GELU = 1, ACT_SILU = 2, ACT_IDENTITY = 3, ACT_SWIGLU = 4 };
+
+template <int DT>
+__device__ __forceinline__ float rt(float x) {
+  return round_to<DT>(x);
+}
+
+template <int DT>
+__device__ __forceinline__ float sigmoid_t(float x) {
+  return rt<DT>(1.f / (1.f + expf(-x)));
+}
+
+// swiglu_gate/3 (moe.ex:199-206): g * sigmoid(alpha * g) * (l + beta), g and l limited first
+// when limit is not 0; each operation rounds to the input type.
+template <int DT>
+__device__ __forceinline__ float swiglu(float g, float l, float alpha, float beta, float limit) {
+  if (limit != 0.f) {
+    g = fminf(g, limit);
+    l = fminf(fmaxf(l, -limit), limit);
+  }
+  const float sg = sigmoid_t<DT>(rt<DT>(alpha * g));
+  return rt<DT>(rt<DT>(g * sg) * rt<DT>(l + beta));
+}
+
+// The activation of one element: elementwise activations of h, or swiglu of (h, l).
+template <int DT>
+__device__ __forceinline__ float activate(int act, float h, float l, float alpha, float beta, float limit) {
+  switch (act) {
+    case ACT_RELU: return fmaxf(h, 0.f);
+    case ACT_SILU: return rt<DT>(h * sigmoid_t<DT>(h));
+    case ACT_GELU: return rt<DT>(h * rt<DT>(0.5f * rt<DT>(1.f + rt<DT>(erff(rt<DT>(h * 0.70710678118654752f))))));
+    case ACT_SWIGLU: return swiglu<DT>(h, l, alpha, beta, limit);
+    default: return h;
+  }
 }
 
 // ------------------------------------------------------------------ grouped expert GEMMs
@@ -139,116 +168,176 @@ struct MoeItem {
   int e, row0, rows;
 };
 
-__device__ __forceinline__ MoeItem moe_item(const int* items, int item, const int* offsets, const int* counts) {
+__device__ __forceinline__ MoeItem moe_item(const int* items, int item, const int* offsets, const int* counts,
+                                            int rows) {
   const int it = items[item];
   const int e = it >> 16, b = it & 0xffff;
-  return MoeItem{e, offsets[e] + b * kMoeRows, min(kMoeRows, counts[e] - b * kMoeRows)};
+  return MoeItem{e, offsets[e] + b * rows, min(rows, counts[e] - b * rows)};
 }
 
-// out[row][n] = sum_k A[src(row)][k] * W_e[n][k] for the up to 32 sorted rows of one work item
-// and TN 16-column tiles of its expert, f16 in and out with f32 sums (v_mfma_f32_16x16x32_f16).
-// src(row) = perm[row] / perm_div when perm is given (rows gathered from the tokens), else row.
-// The wavefronts split the chunks of K and add their sums through LDS.
-template <int BITS, bool HAS_ZP, bool SPLIT, int TN>
-__global__ __launch_bounds__(1024) void k_moe_gemm_f16(
-    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp, int ntiles,
-    int nchunks, int nbc, int bsc_shift, int tiles_per_expert, const _Float16* __restrict__ A, int a_rows, int lda,
-    const int* __restrict__ perm, int perm_div, const int* __restrict__ items, const int* __restrict__ n_items,
-    const int* __restrict__ offsets, const int* __restrict__ counts, _Float16* __restrict__ out, int ldo) {
+// LDS slot of 16-byte piece `piece` of A row `row`: an XOR swizzle that puts the fragment reads
+// of 16 consecutive rows on distinct banks (8-bit weights: 8 pieces per row).
+template <int BITS>
+__device__ __forceinline__ int a_slot_moe(int row, int piece) {
+  return BITS == 8 ? (piece ^ ((row >> 1) & 7)) : (piece ^ (row & 15));
+}
+
+// Epilogue of the fast grouped product: none (the f16 sums), an activation of the sums plus the
+// bias, or swiglu of two tiles (fc1 and fc3, or the two halves of fc1).
+enum : int { EPI_STORE = 0, EPI_ACT = 1, EPI_GLU = 2 };
+
+// out[row][n] = epilogue(sum_k A[src(row)][k] * W_e[n][k]) for the up to 16*MT sorted rows of
+// one work item, f16 in and out with f32 sums (v_mfma_f32_16x16x32_f16). src(row) = perm[row] /
+// perm_div when perm is given (rows gathered from the tokens), else row. Each of the eight
+// wavefronts owns one 16-column output tile (and, for EPI_GLU, the matching tile of the second
+// weight) over all of K; the item's A rows pass through LDS one chunk at a time, double
+// buffered, with the next chunk's weights in flight.
+template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT>
+__global__ __launch_bounds__(512) void k_moe_gemm_f16(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const uint4_t* __restrict__ qt2, const uint16_t* __restrict__ sc2, const uint8_t* __restrict__ zp2,
+    int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles,
+    const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
+    const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
+    const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
+    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo) {
   constexpr int CW = 512 / BITS;
   constexpr int GW = CW / 4;
   constexpr int STEPS = GW / 8;
   constexpr int NJ = SPLIT ? STEPS : 1;
-  extern __shared__ float4_t red[];  // nwaves * 2 * TN * 64
+  constexpr int ROWB = CW * 2;                   // LDS bytes per A row
+  constexpr int PPR = CW / 8;                    // 16-byte pieces per row
+  constexpr int ROWS = 16 * MT;                  // rows per work item
+  constexpr int PIECES = ROWS * PPR;             // per chunk
+  constexpr int LOADS = (PIECES + 511) / 512;    // per thread
+  constexpr int NW = EPI == EPI_GLU ? 2 : 1;
+  __shared__ __align__(16) uint8_t lds[2 * ROWS * ROWB];
   if (static_cast<int>(blockIdx.y) >= *n_items) return;
-  const MoeItem it = moe_item(items, blockIdx.y, offsets, counts);
-  const int nwaves = blockDim.x >> 6;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const MoeItem it = moe_item(items, blockIdx.y, offsets, counts, ROWS);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
+  const int lt = blockIdx.x * 8 + wave;  // this wavefront's output tile within the expert
+  const bool active = lt < out_tiles;
   const uint32_t nch = static_cast<uint32_t>(nchunks);
   const uint32_t n_params = static_cast<uint32_t>(ntiles) * nch * nbc * 16;
-  const auto q_rsrc = buffer_rsrc(qt, static_cast<uint32_t>(ntiles) * nch * 1024);
-  const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
-  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
   const auto a_rsrc = buffer_rsrc(A, static_cast<uint32_t>(a_rows) * lda * 2);
-  const int lt0 = blockIdx.x * TN;  // first tile within the expert
-  uint32_t tile[TN];
+  __amdgpu_buffer_rsrc_t q_rsrc[NW], s_rsrc[NW], z_rsrc[NW];
+  uint32_t tile[NW];
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn)
-    tile[tn] = lt0 + tn < tiles_per_expert ? static_cast<uint32_t>(it.e * tiles_per_expert + lt0 + tn)
-                                           : static_cast<uint32_t>(ntiles);  // past the end: zeros
-  uint32_t a_row[2];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int i = mt * 16 + r;
-    const int src = i < it.rows ? (perm ? perm[it.row0 + i] / perm_div : it.row0 + i) : -1;
-    a_row[mt] = src >= 0 ? static_cast<uint32_t>(src) * lda * 2 : 0x80000000u;
+  for (int v = 0; v < NW; ++v) {
+    q_rsrc[v] = buffer_rsrc(v ? qt2 : qt, static_cast<uint32_t>(ntiles) * nch * 1024);
+    s_rsrc[v] = buffer_rsrc(v ? sc2 : sc, n_params * 2);
+    z_rsrc[v] = buffer_rsrc(v ? zp2 : zp, HAS_ZP ? n_params : 0u);
+    tile[v] = static_cast<uint32_t>(it.e * tiles_per_expert + lt + (v ? tile_off2 : 0));
   }
-  float4_t acc[2][TN];
+  // A pieces this thread brings to LDS: row p / PPR, piece p % PPR (rows past the item, and k
+  // past K, read zeros).
+  uint32_t a_src[LOADS];
+  int a_dst[LOADS], a_k[LOADS];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int l = 0; l < LOADS; ++l) {
+    const int p = tid + 512 * l;
+    const int row = p / PPR, piece = p % PPR;
+    const int src = p < PIECES && row < it.rows ? (perm ? perm[it.row0 + row] / perm_div : it.row0 + row) : -1;
+    a_src[l] = src >= 0 ? static_cast<uint32_t>(src) * lda * 2 + piece * 16 : 0x80000000u;
+    a_dst[l] = p < PIECES ? row * ROWB + a_slot_moe<BITS>(row, piece) * 16 : -1;
+    a_k[l] = piece * 8;
+  }
+  auto load_a = [&](uint32_t c, uint4_t (&v)[LOADS]) {
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) acc[mt][tn] = float4_t{0.f, 0.f, 0.f, 0.f};
-  for (uint32_t c = wave; c < nch; c += nwaves) {
-    uint4_t w[TN];
-    uint32_t sv[TN][NJ], zv[TN][NJ];
+    for (int l = 0; l < LOADS; ++l) {
+      const bool in_k = static_cast<int>(c) * CW + a_k[l] < lda;  // lda = K, a multiple of 8
+      v[l] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, in_k ? a_src[l] + c * CW * 2 : 0x80000000u, 0, 0);
+    }
+  };
+  auto store_a = [&](int buf, const uint4_t (&v)[LOADS]) {
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
-      w[tn] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, (tile[tn] * nch * 64 + lane) * 16, c * 1024, 0);
+    for (int l = 0; l < LOADS; ++l)
+      if (a_dst[l] >= 0) *reinterpret_cast<uint4_t*>(lds + buf * ROWS * ROWB + a_dst[l]) = v[l];
+  };
+  struct WStage {
+    uint4_t w[NW];
+    uint32_t s[NW][NJ], z[NW][NJ];
+  };
+  auto load_w = [&](uint32_t c, WStage& st) {
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      st.w[v] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc[v], (tile[v] * nch * 64 + lane) * 16, c * 1024, 0);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const uint32_t e = ((tile[tn] * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
-        sv[tn][j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, 0, 0);
-        if constexpr (HAS_ZP) zv[tn][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0);
+        const uint32_t e = ((tile[v] * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
+        st.s[v][j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc[v], e * 2, 0, 0);
+        if constexpr (HAS_ZP) st.z[v][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc[v], e, 0, 0);
       }
     }
-    half8_t af[2][STEPS];
+  };
+  float4_t acc[NW][MT];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+  for (int v = 0; v < NW; ++v)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[v][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  uint4_t av[LOADS];
+  WStage cur, next;
+  load_a(0, av);
+  if (active) load_w(0, cur);
+  store_a(0, av);
+  __syncthreads();
+  for (uint32_t c = 0; c < nch; ++c) {
+    const bool more = c + 1 < nch;
+    if (more) {
+      load_a(c + 1, av);
+      if (active) load_w(c + 1, next);
+    }
+    if (active) {
+      const uint8_t* abase = lds + (c & 1) * ROWS * ROWB;
 #pragma unroll
       for (int i = 0; i < STEPS; ++i) {
-        const uint32_t k = c * CW + g * GW + 8 * i;
-        const uint32_t off = k < static_cast<uint32_t>(lda) ? a_row[mt] + k * 2 : 0x80000000u;
-        af[mt][i] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
-      }
+        const int piece = g * (GW / 8) + i;
+        half8_t af[MT];
 #pragma unroll
-    for (int i = 0; i < STEPS; ++i) {
-      const int j = SPLIT ? i : 0;
+        for (int mt = 0; mt < MT; ++mt)
+          af[mt] = *reinterpret_cast<const half8_t*>(abase + (mt * 16 + r) * ROWB + a_slot_moe<BITS>(mt * 16 + r, piece) * 16);
+        const int j = SPLIT ? i : 0;
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const uint32_t zq = HAS_ZP ? 0x6400u + zv[tn][j] : 0x6400u + (1u << (BITS - 1));
-        const half8_t b = unpack_step<BITS>(w[tn], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
-                                            __builtin_bit_cast(half2_t, sv[tn][j] | (sv[tn][j] << 16)));
+        for (int v = 0; v < NW; ++v) {
+          const uint32_t zq = HAS_ZP ? 0x6400u + cur.z[v][j] : 0x6400u + (1u << (BITS - 1));
+          const half8_t b = unpack_step<BITS>(cur.w[v], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
+                                              __builtin_bit_cast(half2_t, cur.s[v][j] | (cur.s[v][j] << 16)));
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-          acc[mt][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[mt][i], acc[mt][tn], 0, 0, 0);
+          for (int mt = 0; mt < MT; ++mt)
+            acc[v][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[mt], acc[v][mt], 0, 0, 0);
+        }
       }
     }
-  }
-  if (nwaves > 1) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) red[((wave * 2 + mt) * TN + tn) * 64 + lane] = acc[mt][tn];
+    if (more) store_a((c + 1) & 1, av);
     __syncthreads();
+    if (more) cur = next;
   }
+  if (!active) return;
+  // Lane (16g + r) holds rows mt*16 + r and columns lt*16 + 4g .. +3.
+  const int n = lt * 16 + 4 * g;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
     const int i = mt * 16 + r;
+    if (i >= it.rows) continue;
+    float y[4];
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
-      if (nwaves > 1) {
-        if ((mt * TN + tn) % nwaves != wave) continue;
-        acc[mt][tn] = red[(mt * TN + tn) * 64 + lane];
-        for (int w2 = 1; w2 < nwaves; ++w2) acc[mt][tn] += red[((w2 * 2 + mt) * TN + tn) * 64 + lane];
+    for (int e = 0; e < 4; ++e) {
+      float h = rt<DT_F16>(acc[0][mt][e]);
+      if (EPI != EPI_STORE && bias1)
+        h = rt<DT_F16>(h + load_float_rt(bias1, bias_dt, static_cast<int64_t>(it.e) * bias_ld + n + e));
+      float l = 0.f;
+      if constexpr (EPI == EPI_GLU) {
+        l = rt<DT_F16>(acc[NW - 1][mt][e]);
+        if (bias2)
+          l = rt<DT_F16>(l + load_float_rt(bias2, bias_dt, static_cast<int64_t>(it.e) * bias_ld + n + e + tile_off2 * 16));
       }
-      if (i >= it.rows || lt0 + tn >= tiles_per_expert) continue;
-      const float4_t v = acc[mt][tn];
-      const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
-      const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
-      _Float16* dst = out + static_cast<int64_t>(it.row0 + i) * ldo + (lt0 + tn) * 16 + 4 * g;
-      *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+      y[e] = EPI == EPI_STORE ? h : activate<DT_F16>(act, h, l, alpha, beta, limit);
     }
+    const half2_t lo = {static_cast<_Float16>(y[0]), static_cast<_Float16>(y[1])};
+    const half2_t hi = {static_cast<_Float16>(y[2]), static_cast<_Float16>(y[3])};
+    _Float16* dst = out + static_cast<int64_t>(it.row0 + i) * ldo + n;
+    *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
   }
 }
 
@@ -265,7 +354,7 @@ __global__ __launch_bounds__(256) void k_moe_gemm_general(
   constexpr int PER_WORD = 32 / BITS;
   __shared__ float red[4][kMoeRows][16];
   if (static_cast<int>(blockIdx.y) >= *n_items) return;
-  const MoeItem it = moe_item(items, blockIdx.y, offsets, counts);
+  const MoeItem it = moe_item(items, blockIdx.y, offsets, counts, kMoeRows);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int64_t t = static_cast<int64_t>(it.e) * tiles_per_expert + blockIdx.x;
@@ -313,30 +402,6 @@ __global__ __launch_bounds__(256) void k_moe_gemm_general(
 
 // ------------------------------------------------------------------ activation and sum
 
-enum : int { ACT_RELU = 0, ACT_GELU = 1, ACT_SILU = 2, ACT_IDENTITY = 3, ACT_SWIGLU = 4 };
-
-template <int DT>
-__device__ __forceinline__ float rt(float x) {
-  return round_to<DT>(x);
-}
-
-template <int DT>
-__device__ __forceinline__ float sigmoid_t(float x) {
-  return rt<DT>(1.f / (1.f + expf(-x)));
-}
-
-// swiglu_gate/3 (moe.ex:199-206): g * sigmoid(alpha * g) * (l + beta), g and l limited first
-// when limit is not 0; each operation rounds to the input type.
-template <int DT>
-__device__ __forceinline__ float swiglu(float g, float l, float alpha, float beta, float limit) {
-  if (limit != 0.f) {
-    g = fminf(g, limit);
-    l = fminf(fmaxf(l, -limit), limit);
-  }
-  const float sg = sigmoid_t<DT>(rt<DT>(alpha * g));
-  return rt<DT>(rt<DT>(g * sg) * rt<DT>(l + beta));
-}
-
 // Activated rows: hact[row][c] from h1 (and h3), with the biases of the row's expert.
 // fusion (for swiglu): 0 with h3 = gate h1, linear h3; 2 = halves of h1; otherwise interleaved.
 template <int DT>
@@ -356,54 +421,66 @@ __global__ __launch_bounds__(256) void k_moe_activate(const void* __restrict__ h
     if (bias) v = rt<DT>(v + load_float_rt(bias, bias_dt, static_cast<int64_t>(e) * n1 + col));
     return v;
   };
-  float y;
-  if (act == ACT_SWIGLU) {
-    float g, l;
-    if (h3) {
-      g = h(h1, b1, c);
-      l = h(h3, b3, c);
-    } else if (fusion == 2) {
-      g = h(h1, b1, c);
-      l = h(h1, b1, inter + c);
-    } else {
-      g = h(h1, b1, 2 * c);
-      l = h(h1, b1, 2 * c + 1);
-    }
-    y = swiglu<DT>(g, l, alpha, beta, limit);
+  float g, l = 0.f;
+  if (act != ACT_SWIGLU) {
+    g = h(h1, b1, c);
+  } else if (h3) {
+    g = h(h1, b1, c);
+    l = h(h3, b3, c);
+  } else if (fusion == 2) {
+    g = h(h1, b1, c);
+    l = h(h1, b1, inter + c);
   } else {
-    const float v = h(h1, b1, c);
-    if (act == ACT_RELU) {
-      y = fmaxf(v, 0.f);
-    } else if (act == ACT_SILU) {
-      y = rt<DT>(v * sigmoid_t<DT>(v));
-    } else if (act == ACT_GELU) {
-      y = rt<DT>(v * rt<DT>(0.5f * rt<DT>(1.f + rt<DT>(erff(rt<DT>(v * 0.70710678118654752f))))));
-    } else {
-      y = v;
-    }
+    g = h(h1, b1, 2 * c);
+    l = h(h1, b1, 2 * c + 1);
   }
+  const float y = activate<DT>(act, g, l, alpha, beta, limit);
   store_as<DT>(hact, idx, y);
 }
 
 // y[t][h] = sum over the token's slots j of weight_j * (o[row of (t, j)][h] + fc2 bias), in slot
-// order; a slot of weight 0 adds 0.
-template <int DT>
+// order; a slot of weight 0 adds 0. V consecutive columns per thread.
+template <int DT, int V>
 __global__ __launch_bounds__(256) void k_moe_combine(const void* __restrict__ o, int H, const void* __restrict__ b2,
                                                      int bias_dt, const int* __restrict__ topi,
                                                      const float* __restrict__ topw, const int* __restrict__ slot_pos,
-                                                     int T, int k, void* __restrict__ y) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+                                                     int T, int k, void* __restrict__ y, bool y_vec) {
+  const int64_t idx = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * V;
   if (idx >= static_cast<int64_t>(T) * H) return;
   const int t = static_cast<int>(idx / H), hc = static_cast<int>(idx - static_cast<int64_t>(t) * H);
-  float sum = 0.f;
+  float sum[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) sum[v] = 0.f;
   for (int j = 0; j < k; ++j) {
     const float wgt = rt<DT>(topw[t * k + j]);
     if (wgt == 0.f) continue;
-    float v = load_as_f32<DT>(o, static_cast<int64_t>(slot_pos[t * k + j]) * H + hc);
-    if (b2) v = rt<DT>(v + load_float_rt(b2, bias_dt, static_cast<int64_t>(topi[t * k + j]) * H + hc));
-    sum = rt<DT>(sum + rt<DT>(v * wgt));
+    const int64_t row = slot_pos[t * k + j];
+    const int e = topi[t * k + j];
+    float ov[V];
+    if constexpr (DT == DT_F16 && V == 8) {
+      const half8_t h8 = *reinterpret_cast<const half8_t*>(static_cast<const _Float16*>(o) + row * H + hc);
+#pragma unroll
+      for (int v = 0; v < V; ++v) ov[v] = static_cast<float>(h8[v]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; ++v) ov[v] = load_as_f32<DT>(o, row * H + hc + v);
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float x = ov[v];
+      if (b2) x = rt<DT>(x + load_float_rt(b2, bias_dt, static_cast<int64_t>(e) * H + hc + v));
+      sum[v] = rt<DT>(sum[v] + rt<DT>(x * wgt));
+    }
   }
-  store_as<DT>(y, idx, sum);
+  if (DT == DT_F16 && V == 8 && y_vec) {
+    half8_t h8;
+#pragma unroll
+    for (int v = 0; v < V; ++v) h8[v] = static_cast<_Float16>(sum[v]);
+    *reinterpret_cast<half8_t*>(static_cast<_Float16*>(y) + idx) = h8;
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) store_as<DT>(y, idx + v, sum[v]);
+  }
 }
 
 // ------------------------------------------------------------------ launchers
@@ -414,29 +491,59 @@ int bsc_shift_moe(const tmh_weight* w) {
   return s;
 }
 
+// The epilogue of a fast grouped product.
+struct MoeEpilogue {
+  int kind = EPI_STORE;
+  const tmh_weight* w2 = nullptr;  // EPI_GLU: the weight of the second tile (fc3, or fc1 itself)
+  int tile_off2 = 0;               // and that tile's offset within the expert
+  int out_tiles = 0;               // output tiles per expert
+  const void *bias1 = nullptr, *bias2 = nullptr;
+  int bias_dt = TMH_F32, bias_ld = 0, act = ACT_IDENTITY;
+  float alpha = 1.f, beta = 0.f, limit = 0.f;
+  int rows = 32;                   // rows per work item: 32 or 64
+};
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT>
+void launch_moe_f16_e(const tmh_weight* w, int tpe, const void* A, int a_rows, int lda, const int* perm, int perm_div,
+                      const int* items, const int* n_items, int max_items, const int* offsets, const int* counts,
+                      void* out, int ldo, const MoeEpilogue& ep, hipStream_t s) {
+  const tmh_weight* w2 = ep.w2 ? ep.w2 : w;
+  const dim3 grid(static_cast<unsigned>((ep.out_tiles + 7) / 8), static_cast<unsigned>(max_items));
+  k_moe_gemm_f16<BITS, HAS_ZP, SPLIT, EPI, MT><<<grid, 512, 0, s>>>(
+      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+      static_cast<const uint8_t*>(w->d_zero), reinterpret_cast<const uint4_t*>(w2->d_q),
+      static_cast<const uint16_t*>(w2->d_scale), static_cast<const uint8_t*>(w2->d_zero), ep.tile_off2,
+      static_cast<int>(w->ntiles), static_cast<int>(w->nchunks), w->nbc, bsc_shift_moe(w), tpe, ep.out_tiles,
+      static_cast<const _Float16*>(A), a_rows, lda, perm, perm_div, items, n_items, offsets, counts, ep.bias1, ep.bias2,
+      ep.bias_dt, ep.bias_ld, ep.act, ep.alpha, ep.beta, ep.limit, static_cast<_Float16*>(out), ldo);
+}
+
 template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_moe_f16_v(const tmh_weight* w, int tpe, const void* A, int a_rows, int lda, const int* perm, int perm_div,
                       const int* items, const int* n_items, int max_items, const int* offsets, const int* counts,
-                      void* out, int ldo, hipStream_t s) {
-  constexpr int TN = 2;
-  const int waves = static_cast<int>(std::min<int64_t>(8, w->nchunks));
-  const dim3 grid(static_cast<unsigned>((tpe + TN - 1) / TN), static_cast<unsigned>(max_items));
-  const size_t lds = waves > 1 ? static_cast<size_t>(waves) * 2 * TN * 64 * sizeof(float4_t) : 0;
-  k_moe_gemm_f16<BITS, HAS_ZP, SPLIT, TN><<<grid, 64 * waves, lds, s>>>(
-      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
-      static_cast<const uint8_t*>(w->d_zero), static_cast<int>(w->ntiles), static_cast<int>(w->nchunks), w->nbc,
-      bsc_shift_moe(w), tpe, static_cast<const _Float16*>(A), a_rows, lda, perm, perm_div, items, n_items, offsets,
-      counts, static_cast<_Float16*>(out), ldo);
+                      void* out, int ldo, const MoeEpilogue& ep, hipStream_t s) {
+#define TMH_MOE_EPI(E, MT) \
+  launch_moe_f16_e<BITS, HAS_ZP, SPLIT, E, MT>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, ep, s)
+  if (ep.rows == 64) {
+    if (ep.kind == EPI_GLU) TMH_MOE_EPI(EPI_GLU, 4);
+    else if (ep.kind == EPI_ACT) TMH_MOE_EPI(EPI_ACT, 4);
+    else TMH_MOE_EPI(EPI_STORE, 4);
+  } else {
+    if (ep.kind == EPI_GLU) TMH_MOE_EPI(EPI_GLU, 2);
+    else if (ep.kind == EPI_ACT) TMH_MOE_EPI(EPI_ACT, 2);
+    else TMH_MOE_EPI(EPI_STORE, 2);
+  }
+#undef TMH_MOE_EPI
 }
 
 template <int BITS>
 void launch_moe_f16(const tmh_weight* w, int tpe, const void* A, int a_rows, int lda, const int* perm, int perm_div,
                     const int* items, const int* n_items, int max_items, const int* offsets, const int* counts,
-                    void* out, int ldo, hipStream_t s) {
+                    void* out, int ldo, const MoeEpilogue& ep, hipStream_t s) {
   const bool zp = w->zp_kind == TMH_ZP_PACKED;
   const bool split = w->block_size < (512 / BITS) / 4;
 #define TMH_MOE_F16(Z, S) \
-  launch_moe_f16_v<BITS, Z, S>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, s)
+  launch_moe_f16_v<BITS, Z, S>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, ep, s)
   if (zp && split) TMH_MOE_F16(true, true);
   else if (zp) TMH_MOE_F16(true, false);
   else if (split) TMH_MOE_F16(false, true);
@@ -480,19 +587,26 @@ void launch_moe_general(const tmh_weight* w, int tpe, const void* A, int a_dt, i
   }
 }
 
-// One grouped product: rows (gathered through perm when given) times each row's expert.
+// The fast grouped product applies: f16 rows and weights, packed or no zero points, K a multiple
+// of 8, 32-bit buffer offsets.
+bool moe_fast(const tmh_weight* w, int a_dt, const void* A, int a_rows, int lda) {
+  return a_dt == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT && lda % 8 == 0 &&
+         reinterpret_cast<uintptr_t>(A) % 16 == 0 && static_cast<int64_t>(a_rows) * lda * 2 < (int64_t(1) << 31) &&
+         (w->ntiles + 1) * w->nchunks * 1024 < (int64_t(1) << 31);
+}
+
+// One grouped product: rows (gathered through perm when given) times each row's expert. The
+// fast path applies the epilogue; the general path stores the sums (EPI_STORE only).
 void moe_gemm(const tmh_weight* w, int experts, const void* A, int a_dt, int a_rows, int lda, const int* perm,
               int perm_div, const int* items, const int* n_items, int max_items, const int* offsets,
-              const int* counts, void* out, int ldo, hipStream_t s) {
+              const int* counts, void* out, int ldo, hipStream_t s, MoeEpilogue ep = MoeEpilogue()) {
   const int tpe = static_cast<int>(w->N / experts / 16);
-  const bool fast = a_dt == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT && lda % 8 == 0 &&
-                    reinterpret_cast<uintptr_t>(A) % 16 == 0 && static_cast<int64_t>(a_rows) * lda * 2 < (int64_t(1) << 31) &&
-                    (w->ntiles + 1) * w->nchunks * 1024 < (int64_t(1) << 31);
-  if (fast) {
+  if (moe_fast(w, a_dt, A, a_rows, lda)) {
+    if (ep.out_tiles == 0) ep.out_tiles = tpe;
     switch (w->bits) {
-      case 2: launch_moe_f16<2>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, s); break;
-      case 4: launch_moe_f16<4>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, s); break;
-      default: launch_moe_f16<8>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, s);
+      case 2: launch_moe_f16<2>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, ep, s); break;
+      case 4: launch_moe_f16<4>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, ep, s); break;
+      default: launch_moe_f16<8>(w, tpe, A, a_rows, lda, perm, perm_div, items, n_items, max_items, offsets, counts, out, ldo, ep, s);
     }
     return;
   }
@@ -615,14 +729,22 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
   if (tk >= (int64_t(1) << 24)) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE supports fewer than 2^24 routed rows");
   hipStream_t s = pick_stream(ctx, stream);
   const size_t es = static_cast<size_t>(dtype_size(x_dtype));
-  const int max_items = static_cast<int>((tk + kMoeRows - 1) / kMoeRows + E);
+  // Rows per work item: 64 when experts average more than 24 rows and every product takes the
+  // fast path (each expert's weights are then mostly read once), else 32.
+  const int64_t inter_i = inter;
+  const bool all_fast = moe_fast(fc1, x_dtype, d_x, static_cast<int>(T), static_cast<int>(H)) &&
+                        (!two || moe_fast(fc3, x_dtype, d_x, static_cast<int>(T), static_cast<int>(H))) &&
+                        fc2->wdtype == TMH_F16 && fc2->zp_kind != TMH_ZP_FLOAT && inter_i % 8 == 0 &&
+                        tk * inter_i * 2 < (int64_t(1) << 31) && (fc2->ntiles + 1) * fc2->nchunks * 1024 < (int64_t(1) << 31);
+  const int rows = all_fast && tk > 24 * E ? 64 : kMoeRows;
+  const int max_items = static_cast<int>((tk + rows - 1) / rows + E);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t at = off;
     off += align256(bytes);
     return at;
   };
-  const size_t o_counts = take(E * 4), o_offsets = take(E * 4), o_fill = take(E * 4), o_nitems = take(4);
+  const size_t o_counts = take(E * 4), o_offsets = take(E * 4), o_nitems = take(4);
   const size_t o_items = take(static_cast<size_t>(max_items) * 4), o_topi = take(tk * 4), o_topw = take(tk * 4);
   const size_t o_perm = take(tk * 4), o_slot = take(tk * 4);
   const size_t o_h1 = take(tk * n1 * es), o_h3 = two ? take(tk * n1 * es) : 0;
@@ -632,7 +754,6 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
     return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE needs a %zu-byte workspace; run it once outside graph capture first", off);
   auto* counts = reinterpret_cast<int*>(ws + o_counts);
   auto* offsets = reinterpret_cast<int*>(ws + o_offsets);
-  auto* fill = reinterpret_cast<int*>(ws + o_fill);
   auto* n_items = reinterpret_cast<int*>(ws + o_nitems);
   auto* items = reinterpret_cast<int*>(ws + o_items);
   auto* topi = reinterpret_cast<int*>(ws + o_topi);
@@ -644,32 +765,67 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
   void* hact = ws + o_act;
   void* o = ws + o_o;
   const int ti = static_cast<int>(T), ki = k, ei = static_cast<int>(E), tki = static_cast<int>(tk);
-  k_moe_zero<<<1, 256, 0, s>>>(counts, ei);
-  k_moe_route<<<static_cast<unsigned>((T + 3) / 4), 256, 0, s>>>(d_router, router_dtype, ti, ei, ki, topi, topw, counts);
-  k_moe_plan<<<1, 1024, 0, s>>>(counts, ei, offsets, fill, items, n_items);
-  k_moe_scatter<<<static_cast<unsigned>((tk + 255) / 256), 256, 0, s>>>(topi, tki, offsets, fill, perm, slot_pos);
-  TMH_TRY(check_launch(ctx, "k_moe_scatter"));
+  const unsigned route_grid = static_cast<unsigned>((T + 3) / 4);
+  switch (router_dtype) {
+    case TMH_F16: k_moe_route<DT_F16><<<route_grid, 256, 0, s>>>(d_router, ti, ei, ki, topi, topw); break;
+    case TMH_BF16: k_moe_route<DT_BF16><<<route_grid, 256, 0, s>>>(d_router, ti, ei, ki, topi, topw); break;
+    default: k_moe_route<DT_F32><<<route_grid, 256, 0, s>>>(d_router, ti, ei, ki, topi, topw);
+  }
+  k_moe_plan<<<1, 1024, 0, s>>>(counts, ei, rows, topi, tki, offsets, items, n_items, perm, slot_pos);
+  TMH_TRY(check_launch(ctx, "k_moe_plan"));
   const int hi = static_cast<int>(H), n1i = static_cast<int>(n1), inti = static_cast<int>(inter);
-  moe_gemm(fc1, ei, d_x, x_dtype, ti, hi, perm, ki, items, n_items, max_items, offsets, counts, h1, n1i, s);
-  if (two) moe_gemm(fc3, ei, d_x, x_dtype, ti, hi, perm, ki, items, n_items, max_items, offsets, counts, h3, n1i, s);
-  TMH_TRY(check_launch(ctx, "k_moe_gemm (fc1)"));
-  const int64_t act_n = tk * (activation == ACT_SWIGLU ? inter : n1);
-  const unsigned act_grid = static_cast<unsigned>((act_n + 255) / 256);
+  // fc1 (and fc3) with the activation in the product's epilogue where the fast path allows it:
+  // swiglu of fc1 and fc3 tiles, of the two halves of fc1, or an elementwise activation.
+  // Interleaved swiglu pairs and the general path store the sums and activate separately.
+  MoeEpilogue ep;
+  ep.rows = rows;
+  ep.bias1 = d_fc1_bias;
+  ep.bias_dt = bias_dtype;
+  ep.bias_ld = n1i;
+  ep.act = activation;
+  ep.alpha = alpha;
+  ep.beta = beta;
+  ep.limit = limit;
+  const bool fused = moe_fast(fc1, x_dtype, d_x, ti, hi) && (!two || moe_fast(fc3, x_dtype, d_x, ti, hi)) &&
+                     (activation != ACT_SWIGLU || two || (swiglu_fusion == 2 && inter % 16 == 0));
+  if (fused) {
+    if (activation == ACT_SWIGLU) {
+      ep.kind = EPI_GLU;
+      ep.w2 = two ? fc3 : fc1;
+      ep.bias2 = two ? d_fc3_bias : d_fc1_bias;
+      ep.tile_off2 = two ? 0 : inti / 16;
+      ep.out_tiles = inti / 16;
+    } else {
+      ep.kind = EPI_ACT;
+    }
+    moe_gemm(fc1, ei, d_x, x_dtype, ti, hi, perm, ki, items, n_items, max_items, offsets, counts, hact, inti, s, ep);
+    TMH_TRY(check_launch(ctx, "k_moe_gemm (fc1)"));
+  } else {
+    moe_gemm(fc1, ei, d_x, x_dtype, ti, hi, perm, ki, items, n_items, max_items, offsets, counts, h1, n1i, s);
+    if (two) moe_gemm(fc3, ei, d_x, x_dtype, ti, hi, perm, ki, items, n_items, max_items, offsets, counts, h3, n1i, s);
+    TMH_TRY(check_launch(ctx, "k_moe_gemm (fc1)"));
+    const int64_t act_n = tk * (activation == ACT_SWIGLU ? inter : n1);
+    const unsigned act_grid = static_cast<unsigned>((act_n + 255) / 256);
 #define TMH_MOE_ACT(DT)                                                                                                  \
   k_moe_activate<DT><<<act_grid, 256, 0, s>>>(h1, h3, n1i, inti, d_fc1_bias, two ? d_fc3_bias : nullptr, bias_dtype,    \
                                               perm, topi, tki, activation, swiglu_fusion, alpha, beta, limit, hact)
-  switch (x_dtype) {
-    case TMH_F16: TMH_MOE_ACT(DT_F16); break;
-    case TMH_BF16: TMH_MOE_ACT(DT_BF16); break;
-    default: TMH_MOE_ACT(DT_F32);
-  }
+    switch (x_dtype) {
+      case TMH_F16: TMH_MOE_ACT(DT_F16); break;
+      case TMH_BF16: TMH_MOE_ACT(DT_BF16); break;
+      default: TMH_MOE_ACT(DT_F32);
+    }
 #undef TMH_MOE_ACT
-  TMH_TRY(check_launch(ctx, "k_moe_activate"));
-  moe_gemm(fc2, ei, hact, x_dtype, tki, inti, nullptr, 1, items, n_items, max_items, offsets, counts, o, hi, s);
+    TMH_TRY(check_launch(ctx, "k_moe_activate"));
+  }
+  MoeEpilogue ep2;
+  ep2.rows = rows;
+  moe_gemm(fc2, ei, hact, x_dtype, tki, inti, nullptr, 1, items, n_items, max_items, offsets, counts, o, hi, s, ep2);
   TMH_TRY(check_launch(ctx, "k_moe_gemm (fc2)"));
-  const unsigned out_grid = static_cast<unsigned>((T * H + 255) / 256);
+  // H is a multiple of 16: eight columns per thread.
+  const unsigned out_grid = static_cast<unsigned>((T * H / 8 + 255) / 256);
 #define TMH_MOE_SUM(DT) \
-  k_moe_combine<DT><<<out_grid, 256, 0, s>>>(o, hi, d_fc2_bias, bias_dtype, topi, topw, slot_pos, ti, ki, d_y)
+  k_moe_combine<DT, 8><<<out_grid, 256, 0, s>>>(o, hi, d_fc2_bias, bias_dtype, topi, topw, slot_pos, ti, ki, d_y, \
+                                               reinterpret_cast<uintptr_t>(d_y) % 16 == 0)
   switch (x_dtype) {
     case TMH_F16: TMH_MOE_SUM(DT_F16); break;
     case TMH_BF16: TMH_MOE_SUM(DT_BF16); break;
