@@ -90,6 +90,15 @@ int tmh_free(tmh_ctx* ctx, void* d_ptr);
 int tmh_upload(tmh_ctx* ctx, void* d_dst, const void* h_src, size_t bytes);
 int tmh_download(tmh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes);
 
+/*
+ * Synchronous copy of bytes [offset, offset + bytes) of a file to device memory, through two
+ * pinned 16 MiB staging buffers: the device upload of an initializer kept in an ONNX external
+ * data file (Ops.read_external/2, lib/transmuter/ops.ex:674-697, read by
+ * DeferredTensor.value/1 at move time, lib/transmuter/deferred_tensor.ex), without a host copy
+ * of the whole tensor.
+ */
+int tmh_upload_file(tmh_ctx* ctx, void* d_dst, const char* path, int64_t offset, size_t bytes);
+
 /* Copies `rows` rows of width_bytes between device buffers with row pitches (bytes):
  * the Split that Fusion.matmuls/2 puts after a merged matmul (lib/transmuter/fusion.ex:
  * 495-507) takes column ranges of the merged output this way. Asynchronous. */

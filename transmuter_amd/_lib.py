@@ -68,6 +68,7 @@ SIGNATURES = {
     "tmh_matmul_integer": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i, _vp,
                                 _vp]),
     "tmh_dynamic_quantize_linear": (_i, [_vp, _vp, _i, _i64, _vp, _vp, _vp, _vp]),
+    "tmh_upload_file": (_i, [_vp, _vp, ctypes.c_char_p, _i64, _sz]),
     "tmh_weight_upload_qmoe": (_i, [_vp, _vp, _sz, _vp, _i, _sz, _vp, _sz, _i64, _i64, _i64, _i, _i64, _i,
                                     ctypes.POINTER(_vp)]),
     "tmh_qmoe": (_i, [_vp, _vp, _i, _i64, _i64, _vp, _i, _i64, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,

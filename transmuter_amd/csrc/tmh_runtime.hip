@@ -1,8 +1,14 @@
 // Context, memory, events, graphs and error reporting of the C ABI.
+#include <algorithm>
+#include <cerrno>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include "tmh_internal.h"
 
@@ -198,6 +204,55 @@ int tmh_upload(tmh_ctx* ctx, void* d_dst, const void* h_src, size_t bytes) {
   TMH_TRY(check_hip(ctx, hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, ctx->stream),
                     "hipMemcpyAsync H2D"));
   return check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+int tmh_upload_file(tmh_ctx* ctx, void* d_dst, const char* path, int64_t offset, size_t bytes) {
+  TMH_TRY(use_device(ctx));
+  if (!path) return fail(ctx, TMH_ERR_INVALID, "tmh_upload_file: NULL path");
+  if (offset < 0) return fail(ctx, TMH_ERR_INVALID, "tmh_upload_file: negative offset");
+  if (bytes == 0) return TMH_OK;
+  if (!d_dst) return fail(ctx, TMH_ERR_INVALID, "tmh_upload_file: NULL destination");
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0) return fail(ctx, TMH_ERR_INVALID, "tmh_upload_file: cannot open %s: %s", path, strerror(errno));
+  struct stat st;
+  if (fstat(fd, &st) != 0 || static_cast<uint64_t>(offset) + bytes > static_cast<uint64_t>(st.st_size)) {
+    close(fd);
+    return fail(ctx, TMH_ERR_INVALID, "tmh_upload_file: %s holds no %zu bytes at offset %lld", path, bytes,
+                (long long)offset);
+  }
+  // Two pinned 16 MiB staging buffers: the file is read into one while the other copies.
+  constexpr size_t kChunk = size_t(16) << 20;
+  void* stage[2] = {nullptr, nullptr};
+  hipEvent_t done[2] = {nullptr, nullptr};
+  int st_code = TMH_OK;
+  for (int i = 0; i < 2 && st_code == TMH_OK; ++i) {
+    st_code = check_hip(ctx, hipHostMalloc(&stage[i], kChunk, hipHostMallocDefault), "hipHostMalloc");
+    if (st_code == TMH_OK) st_code = check_hip(ctx, hipEventCreateWithFlags(&done[i], hipEventDisableTiming), "hipEventCreate");
+  }
+  auto* dst = static_cast<uint8_t*>(d_dst);
+  for (size_t pos = 0, i = 0; st_code == TMH_OK && pos < bytes; ++i) {
+    const int b = static_cast<int>(i & 1);
+    if (i >= 2) st_code = check_hip(ctx, hipEventSynchronize(done[b]), "hipEventSynchronize");
+    const size_t n = std::min(kChunk, bytes - pos);
+    for (size_t got = 0; st_code == TMH_OK && got < n;) {
+      const ssize_t r = pread(fd, static_cast<uint8_t*>(stage[b]) + got, n - got, offset + static_cast<int64_t>(pos + got));
+      if (r < 0 && errno == EINTR) continue;
+      if (r <= 0) st_code = fail(ctx, TMH_ERR_INVALID, "tmh_upload_file: reading %s failed", path);
+      else got += static_cast<size_t>(r);
+    }
+    if (st_code == TMH_OK)
+      st_code = check_hip(ctx, hipMemcpyAsync(dst + pos, stage[b], n, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync H2D");
+    if (st_code == TMH_OK) st_code = check_hip(ctx, hipEventRecord(done[b], ctx->stream), "hipEventRecord");
+    pos += n;
+  }
+  const int sync = check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (st_code == TMH_OK) st_code = sync;
+  for (int i = 0; i < 2; ++i) {
+    if (done[i]) (void)hipEventDestroy(done[i]);
+    if (stage[i]) (void)hipHostFree(stage[i]);
+  }
+  close(fd);
+  return st_code;
 }
 
 int tmh_download(tmh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes) {

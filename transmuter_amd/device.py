@@ -7,6 +7,7 @@ host arrays are uint16 bit patterns.
 from __future__ import annotations
 
 import ctypes
+import os
 import math
 
 import numpy as np
@@ -80,6 +81,14 @@ class Context:
         t = self.empty(host.shape, dtype)
         if t.nbytes:
             self.check(lib().tmh_upload(self.handle, t.ptr, host.ctypes.data_as(ctypes.c_void_p), t.nbytes))
+        return t
+
+    def put_file(self, path: str, offset: int, shape, dtype: str) -> "DeviceTensor":
+        """A tensor whose bytes lie in a file at `offset` (an ONNX external data file), copied
+        to the device without a host copy of the whole tensor (tmh_upload_file)."""
+        t = self.empty(shape, dtype)
+        if t.nbytes:
+            self.check(lib().tmh_upload_file(self.handle, t.ptr, os.fsencode(path), offset, t.nbytes))
         return t
 
     def synchronize(self) -> None:

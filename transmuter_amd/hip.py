@@ -37,6 +37,22 @@ class Model:
     outputs: list = field(default_factory=list)
     compute_type: str | None = None
     backend: object = None
+    inputs: list = field(default_factory=list)
+
+
+def _deferred(value) -> bool:
+    """A DeferredTensor of the loader: an initializer still in its external data file."""
+    return hasattr(value, "proto") and hasattr(value, "to_device")
+
+
+def _host_value(value):
+    """A host array of a value: a deferred tensor is read (memory-mapped), a device tensor
+    copied back."""
+    if _deferred(value):
+        return value.value()
+    if isinstance(value, DeviceTensor):
+        return value.numpy()
+    return value
 
 
 def upcast(value, compute_type: str | None):
@@ -73,9 +89,11 @@ def packable(node, model: Model) -> bool:
         return False
     if isinstance(value, PackedWeight):
         return False
-    arr = np.asarray(value) if not isinstance(value, DeviceTensor) else None
-    dtype = value.dtype if isinstance(value, DeviceTensor) else ("u8" if arr.dtype == np.uint8 else None)
-    size = value.size if isinstance(value, DeviceTensor) else arr.size
+    if isinstance(value, DeviceTensor):
+        dtype, size = value.dtype, value.size
+    else:
+        dtype = "u8" if np.dtype(value.dtype) == np.uint8 else None
+        size = int(np.prod(value.shape, dtype=np.int64))
     return dtype == "u8" and size * 8 == n * k * bits
 
 
@@ -83,9 +101,9 @@ def weight(node, b, scales, zero_points, model: Model, backend: Context) -> Pack
     """The packed weight of a MatMulNBits node: its dequantization type is the scales' type
     after :compute_type (dequantized_weight/6, lib/transmuter.ex:1230-1240)."""
     k, n, bits, block = nbits_sizes(node)
-    scales, stype = upcast(scales.numpy() if isinstance(scales, DeviceTensor) else scales, model.compute_type)
-    return PackedWeight.upload(backend, b, scales, zero_points, k=k, n=n, bits=bits, block_size=block,
-                               weight_dtype=stype)
+    scales, stype = upcast(_host_value(scales), model.compute_type)
+    return PackedWeight.upload(backend, _host_value(b), scales, _host_value(zero_points), k=k, n=n, bits=bits,
+                               block_size=block, weight_dtype=stype)
 
 
 def evaluate(t):
@@ -134,11 +152,24 @@ def move(model: Model, ctx: Context) -> Model:
         zp_name = node.input[3] if len(node.input) > 3 else ""
         zero_points = values.get(zp_name) if zp_name else None
         weights[_packed_name(b_name)] = evaluate(weight(node, values[b_name], scales, zero_points, model, ctx))
-    params = {name: value for name, value in model.params.items() if name not in freed}
+    params = {name: _to_device(value, ctx, model.compute_type) for name, value in model.params.items()
+              if name not in freed}
     params.update(weights)
     static = {name: value for name, value in model.static.items() if name not in freed}
     # move/2 ends with Fusion.matmuls/2 (lib/transmuter.ex:1181).
     return merge_matmuls(replace(model, nodes=nodes, params=params, static=static, backend=ctx))
+
+
+def _to_device(value, ctx: Context, compute_type: str | None):
+    """A param on the device (move/2 transfers every param to the backend, lib/transmuter.ex:
+    1104-1182): packed weights and device tensors stay; a deferred tensor is copied from its
+    file; a host array is uploaded, f16/bf16 taking the compute type first."""
+    if isinstance(value, (PackedWeight, DeviceTensor)):
+        return value
+    if _deferred(value) and not (compute_type and np.dtype(value.dtype) == np.float16):
+        return value.to_device(ctx)
+    arr, dtype = upcast(_host_value(value), compute_type)
+    return ctx.put(np.ascontiguousarray(arr))
 
 
 # ---------------------------------------------------------------- merged matmuls

@@ -60,6 +60,10 @@ def _varint(buf: bytes, pos: int) -> tuple[int, int]:
             raise ValueError("varint too long")
 
 
+def _text(v) -> str:
+    return (v.tobytes() if isinstance(v, memoryview) else v).decode()
+
+
 def _signed64(v: int) -> int:
     return v - (1 << 64) if v >= 1 << 63 else v
 
@@ -175,9 +179,10 @@ def decode_tensor(buf: bytes) -> TensorProto:
         elif number == 7:
             t.int64_data.extend(_signed64(v) for v in _packed_varints(value, wire))
         elif number == 8:
-            t.name = value.decode()
+            t.name = _text(value)
         elif number == 9:
-            t.raw_data = bytes(value)
+            # A view into the model's buffer when it is a memoryview (a mapped file): no copy.
+            t.raw_data = value if isinstance(value, memoryview) else bytes(value)
         elif number == 10:
             t.double_data.extend(_packed_fixed(value, wire, "d", 8))
         elif number == 11:
@@ -186,9 +191,9 @@ def decode_tensor(buf: bytes) -> TensorProto:
             key = val = ""
             for n2, _w2, v2 in fields(value):
                 if n2 == 1:
-                    key = v2.decode()
+                    key = _text(v2)
                 elif n2 == 2:
-                    val = v2.decode()
+                    val = _text(v2)
             t.external_data[key] = val
         elif number == 14:
             t.data_location = value
@@ -199,7 +204,7 @@ def decode_attribute(buf: bytes) -> AttributeProto:
     a = AttributeProto()
     for number, wire, value in fields(buf):
         if number == 1:
-            a.name = value.decode()
+            a.name = _text(value)
         elif number == 20:
             a.type = value
         elif number == 2:
@@ -223,24 +228,24 @@ def decode_node(buf: bytes) -> NodeProto:
     node = NodeProto()
     for number, _wire, value in fields(buf):
         if number == 1:
-            node.input.append(value.decode())
+            node.input.append(_text(value))
         elif number == 2:
-            node.output.append(value.decode())
+            node.output.append(_text(value))
         elif number == 3:
-            node.name = value.decode()
+            node.name = _text(value)
         elif number == 4:
-            node.op_type = value.decode()
+            node.op_type = _text(value)
         elif number == 5:
             node.attribute.append(decode_attribute(value))
         elif number == 7:
-            node.domain = value.decode()
+            node.domain = _text(value)
     return node
 
 
 def _value_info_name(buf: bytes) -> str:
     for number, _wire, value in fields(buf):
         if number == 1:
-            return value.decode()
+            return _text(value)
     return ""
 
 
@@ -250,7 +255,7 @@ def decode_graph(buf: bytes) -> GraphProto:
         if number == 1:
             g.node.append(decode_node(value))
         elif number == 2:
-            g.name = value.decode()
+            g.name = _text(value)
         elif number == 5:
             g.initializer.append(decode_tensor(value))
         elif number == 11:
@@ -271,7 +276,7 @@ def decode_model(buf: bytes) -> ModelProto:
             domain, version = "", 0
             for n2, _w2, v2 in fields(value):
                 if n2 == 1:
-                    domain = v2.decode()
+                    domain = _text(v2)
                 elif n2 == 2:
                     version = _signed64(v2)
             m.opset_import[domain] = version
@@ -280,7 +285,15 @@ def decode_model(buf: bytes) -> ModelProto:
     return m
 
 
-def load_model(path: str) -> ModelProto:
+def load_model(path: str, mapped: bool = False) -> ModelProto:
+    """Decodes an .onnx file. With mapped=True the file is memory-mapped and the raw data of the
+    initializers are views into the mapping (no copy of the weights)."""
+    if mapped:
+        import mmap
+
+        with open(path, "rb") as f:
+            mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+        return decode_model(memoryview(mm))
     with open(path, "rb") as f:
         return decode_model(f.read())
 
@@ -334,16 +347,54 @@ def tensor(t: TensorProto, directory: str | None = None) -> np.ndarray:
     return flat.reshape(dims).copy()
 
 
-def _read_external(t: TensorProto, directory: str | None) -> TensorProto:
-    """Reads external data as `Ops.read_external/2` does (lib/transmuter/ops.ex:674-697)."""
+def external_location(t: TensorProto, directory: str | None) -> tuple[str, int, int]:
+    """(path, offset, length) of a tensor kept in an external data file (ops.ex:674-697):
+    without a length, the data runs to the end of the file."""
     if directory is None:
         raise ValueError(f"tensor {t.name} keeps its data in a file, and no directory is known")
     path = os.path.join(directory, t.external_data["location"])
     offset = int(t.external_data.get("offset", "0"))
     length = t.external_data.get("length")
+    length = int(length) if length is not None else os.path.getsize(path) - offset
+    return path, offset, length
+
+
+def shape_type(t: TensorProto) -> tuple[tuple, np.dtype] | None:
+    """The shape and array type `tensor` gives for t, without its data
+    (`Ops.tensor_shape_type/1`, ops.ex:610-625); None for types not held here."""
+    dims = list(t.dims)
+    if t.data_type in (UINT4, INT4):
+        last = dims[-1] if dims else 1
+        return tuple(dims[:-1] + [(last + 1) // 2]), np.dtype(np.int8 if t.data_type == INT4 else np.uint8)
+    if t.data_type == BFLOAT16:
+        return tuple(dims), np.dtype(np.uint16)
+    if t.data_type in ONNX_DTYPES:
+        return tuple(dims), np.dtype(ONNX_DTYPES[t.data_type])
+    return None
+
+
+def tensor_view(t: TensorProto, directory: str | None = None) -> np.ndarray:
+    """`tensor` without copies where the data allows: raw data becomes a read-only view of the
+    model's buffer, and external data a read-only memory map of its file."""
+    st = shape_type(t)
+    if st is not None and t.data_location == 1:
+        path, offset, length = external_location(t, directory)
+        shape, dtype = st
+        if length != int(np.prod(shape, dtype=np.int64)) * dtype.itemsize:
+            raise ValueError(f"tensor {t.name}: {length} bytes in {path} do not hold {shape} {dtype}")
+        return np.memmap(path, dtype=dtype, mode="r", offset=offset, shape=shape)
+    if st is not None and len(t.raw_data):
+        shape, dtype = st
+        return np.frombuffer(t.raw_data, dtype=dtype).reshape(shape)
+    return tensor(t, directory)
+
+
+def _read_external(t: TensorProto, directory: str | None) -> TensorProto:
+    """Reads external data as `Ops.read_external/2` does (lib/transmuter/ops.ex:674-697)."""
+    path, offset, length = external_location(t, directory)
     with open(path, "rb") as f:
         f.seek(offset)
-        raw = f.read(int(length)) if length is not None else f.read()
+        raw = f.read(length)
     return TensorProto(name=t.name, dims=t.dims, data_type=t.data_type, raw_data=raw)
 
 
