@@ -32,37 +32,53 @@ constexpr int kMoeRows = 32;  // rows per work item of the general product
 
 // ------------------------------------------------------------------ routing and grouping
 
+// Order key of a router value: larger values give larger keys and equal values equal keys, with
+// -0 taken as +0 and NaN as -inf, as the float comparisons of the sort see them.
+__device__ __forceinline__ uint32_t order_key(float x) {
+  if (x != x) x = -INFINITY;
+  if (x == 0.f) x = 0.f;
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t key) {
+  return __builtin_bit_cast(float, (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
+typedef uint64_t u64x2_t __attribute__((ext_vector_type(2)));
+
 // One wavefront per token: the k largest router values (lower index first among equals), a
-// softmax over them in f32. The router row goes to LDS; each
-// lane ranks its experts against all of them (rank = how many come first in the stable
-// descending order) and the experts ranked below k are the selection, in rank order.
+// softmax over them in f32. Each expert's 64-bit key (value key, then the complement of its
+// index) goes to LDS, so all keys differ and "comes first in the stable descending order" is one
+// unsigned comparison; each lane ranks its experts against all keys and the experts ranked below
+// k are the selection, in rank order.
 template <int RDT>
 __global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ router, int T, int E, int k,
                                                    int* __restrict__ topi, float* __restrict__ topw) {
-  __shared__ __align__(16) float vals[4][1024];
+  __shared__ __align__(16) uint64_t keys[4][1024];
   __shared__ float sel_v[4][32];
   __shared__ int sel_i[4][32];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + w;
   const bool live = t < T;
-  const int E4 = (E + 3) & ~3;  // padded with -inf, which never comes first
+  const int E2 = (E + 1) & ~1;  // padded with key 0, below every expert's key
   if (live)
-    for (int e = lane; e < E4; e += 64) {
-      const float x = e < E ? load_as_f32<RDT>(router, static_cast<int64_t>(t) * E + e) : -INFINITY;
-      vals[w][e] = x != x ? -INFINITY : x;  // NaN ranks as -inf, so the order stays total
-    }
+    for (int e = lane; e < E2; e += 64)
+      keys[w][e] = e < E ? (static_cast<uint64_t>(order_key(load_as_f32<RDT>(router, static_cast<int64_t>(t) * E + e)))
+                            << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(e))
+                         : 0;
   __syncthreads();
   if (live)
     for (int e = lane; e < E; e += 64) {
-      const float x = vals[w][e];
+      const uint64_t kx = keys[w][e];
       int rank = 0;
-      for (int e2 = 0; e2 < E4; e2 += 4) {
-        const float4_t y = *reinterpret_cast<const float4_t*>(&vals[w][e2]);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) rank += (y[q] > x || (y[q] == x && e2 + q < e)) ? 1 : 0;
+#pragma unroll 8
+      for (int e2 = 0; e2 < E2; e2 += 2) {
+        const u64x2_t y = *reinterpret_cast<const u64x2_t*>(&keys[w][e2]);
+        rank += (y[0] > kx ? 1 : 0) + (y[1] > kx ? 1 : 0);
       }
       if (rank < k) {
-        sel_v[w][rank] = x;
+        sel_v[w][rank] = key_value(static_cast<uint32_t>(kx >> 32));
         sel_i[w][rank] = e;
       }
     }
@@ -78,48 +94,66 @@ __global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ rout
   }
 }
 
-// One workgroup: rows per expert, expert offsets (exclusive prefix of the counts), the list of work items
-// (expert << 16 | item of the expert, `rows` rows each), and the position of every (token,
-// slot) row in expert order (perm) with its inverse (slot_pos).
+// One workgroup of 1024 threads (thread e for expert e): rows per expert, expert offsets (exclusive
+// prefix of the counts), the list of work items (expert << 16 | item of the expert, `rows` rows
+// each), and the position of every (token, slot) row in expert order (perm) with its inverse
+// (slot_pos). The prefix sums run per wavefront with shuffles, then across the 16 wavefronts.
 __global__ __launch_bounds__(1024) void k_moe_plan(int* __restrict__ counts, int E, int rows, const int* __restrict__ topi,
                                                    int Tk, int* __restrict__ offsets, int* __restrict__ items,
                                                    int* __restrict__ n_items, int* __restrict__ perm,
                                                    int* __restrict__ slot_pos) {
-  __shared__ int rows_s[1024], items_s[1024], fill[1024];
-  const int e = threadIdx.x;
+  __shared__ int first_s[1024], fill[1024], wsum_r[16], wsum_i[16];
+  const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
   fill[e] = 0;
   __syncthreads();
-  for (int idx = threadIdx.x; idx < Tk; idx += blockDim.x) atomicAdd(&fill[topi[idx]], 1);
+  for (int idx = e; idx < Tk; idx += 1024) atomicAdd(&fill[topi[idx]], 1);
   __syncthreads();
   const int c = fill[e];
+  const int nb = (c + rows - 1) / rows;
   if (e < E) counts[e] = c;
-  rows_s[e] = c;
-  items_s[e] = (c + rows - 1) / rows;
-  __syncthreads();
-  fill[e] = 0;
-  for (int off = 1; off < 1024; off <<= 1) {  // inclusive scans
-    const int rr = e >= off ? rows_s[e - off] : 0;
-    const int it = e >= off ? items_s[e - off] : 0;
-    __syncthreads();
-    rows_s[e] += rr;
-    items_s[e] += it;
-    __syncthreads();
+  int sr = c, si = nb;  // inclusive prefix sums of rows and items
+  for (int off = 1; off < 64; off <<= 1) {
+    const int r2 = __shfl_up(sr, off), i2 = __shfl_up(si, off);
+    if (lane >= off) {
+      sr += r2;
+      si += i2;
+    }
   }
-  const int first_row = rows_s[e] - c;
+  if (lane == 63) {
+    wsum_r[wave] = sr;
+    wsum_i[wave] = si;
+  }
+  __syncthreads();
+  for (int w2 = 0; w2 < wave; ++w2) {
+    sr += wsum_r[w2];
+    si += wsum_i[w2];
+  }
+  const int first_row = sr - c;
   if (e < E) {
     offsets[e] = first_row;
-    const int nb = (c + rows - 1) / rows;
-    const int first = items_s[e] - nb;
+    const int first = si - nb;
     for (int b = 0; b < nb; ++b) items[first + b] = (e << 16) | b;
   }
-  if (e == 1023) *n_items = items_s[1023];
-  rows_s[e] = first_row;  // exclusive offsets, read back below
+  if (e == 1023) *n_items = si;
+  first_s[e] = first_row;
+  fill[e] = 0;
   __syncthreads();
-  for (int idx = threadIdx.x; idx < Tk; idx += blockDim.x) {
-    const int ex = topi[idx];
-    const int pos = rows_s[ex] + atomicAdd(&fill[ex], 1);
-    perm[pos] = idx;
-    slot_pos[idx] = pos;
+  // Four rows per thread and round, their expert ids loaded before the LDS atomics.
+  for (int base = 0; base < Tk; base += 4096) {
+    int ex[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = base + u * 1024 + e;
+      ex[u] = idx < Tk ? topi[idx] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (ex[u] < 0) continue;
+      const int idx = base + u * 1024 + e;
+      const int pos = first_s[ex[u]] + atomicAdd(&fill[ex[u]], 1);
+      perm[pos] = idx;
+      slot_pos[idx] = pos;
+    }
   }
 }
 
@@ -445,31 +479,43 @@ __global__ __launch_bounds__(256) void k_moe_combine(const void* __restrict__ o,
                                                      int bias_dt, const int* __restrict__ topi,
                                                      const float* __restrict__ topw, const int* __restrict__ slot_pos,
                                                      int T, int k, void* __restrict__ y, bool y_vec) {
+  constexpr int JU = 8;  // slots whose loads are in flight together
   const int64_t idx = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * V;
   if (idx >= static_cast<int64_t>(T) * H) return;
   const int t = static_cast<int>(idx / H), hc = static_cast<int>(idx - static_cast<int64_t>(t) * H);
   float sum[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) sum[v] = 0.f;
-  for (int j = 0; j < k; ++j) {
-    const float wgt = rt<DT>(topw[t * k + j]);
-    if (wgt == 0.f) continue;
-    const int64_t row = slot_pos[t * k + j];
-    const int e = topi[t * k + j];
-    float ov[V];
-    if constexpr (DT == DT_F16 && V == 8) {
-      const half8_t h8 = *reinterpret_cast<const half8_t*>(static_cast<const _Float16*>(o) + row * H + hc);
+  for (int j0 = 0; j0 < k; j0 += JU) {
+    // Slot data and rows of up to JU slots first (slots past k repeat slot k-1 and are not
+    // summed), then the sum in slot order.
+    float wgt[JU];
+    int ex[JU];
+    float ov[JU][V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) ov[v] = static_cast<float>(h8[v]);
-    } else {
+    for (int u = 0; u < JU; ++u) {
+      const int j = j0 + u < k ? j0 + u : k - 1;
+      wgt[u] = rt<DT>(topw[t * k + j]);
+      ex[u] = topi[t * k + j];
+      const int64_t row = slot_pos[t * k + j];
+      if constexpr (DT == DT_F16 && V == 8) {
+        const half8_t h8 = *reinterpret_cast<const half8_t*>(static_cast<const _Float16*>(o) + row * H + hc);
 #pragma unroll
-      for (int v = 0; v < V; ++v) ov[v] = load_as_f32<DT>(o, row * H + hc + v);
+        for (int v = 0; v < V; ++v) ov[u][v] = static_cast<float>(h8[v]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v) ov[u][v] = load_as_f32<DT>(o, row * H + hc + v);
+      }
     }
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-      float x = ov[v];
-      if (b2) x = rt<DT>(x + load_float_rt(b2, bias_dt, static_cast<int64_t>(e) * H + hc + v));
-      sum[v] = rt<DT>(sum[v] + rt<DT>(x * wgt));
+    for (int u = 0; u < JU; ++u) {
+      if (j0 + u >= k || wgt[u] == 0.f) continue;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        float x = ov[u][v];
+        if (b2) x = rt<DT>(x + load_float_rt(b2, bias_dt, static_cast<int64_t>(ex[u]) * H + hc + v));
+        sum[v] = rt<DT>(sum[v] + rt<DT>(x * wgt[u]));
+      }
     }
   }
   if (DT == DT_F16 && V == 8 && y_vec) {
