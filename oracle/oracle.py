@@ -419,27 +419,35 @@ def qmoe(x, router, fc1, fc1_scales, fc2, fc2_scales, *, k: int, bits: int = 4, 
     x2 = x.reshape(-1, h)
     top_vals, top_idx = topk_stable(np.asarray(router, dtype=np.float32), k)
     weights = _softmax_last(top_vals)
-    w1 = qmoe_dequant(fc1, fc1_scales, fc1_zp, bits, block_size)
-    w2 = qmoe_dequant(fc2, fc2_scales, fc2_zp, bits, block_size)
-    w3 = qmoe_dequant(fc3, fc3_scales, fc3_zp, bits, block_size) if fc3 is not None else None
+
+    def expert(fc, scales, zp, e):  # expert e's {N, K} weights: dequant/6 on its slice
+        def part(t):
+            return None if t is None else np.asarray(t)[e:e + 1]
+        return qmoe_dequant(part(fc), part(scales), part(zp), bits, block_size)[0]
+    # Each expert's routed rows at once (the same per-row f64 dot products), then the slots of
+    # every token added in slot order.
+    n_tok = x2.shape[0]
+    outs = np.zeros((n_tok, k, h), dtype=np.float64)
+    for e in np.unique(top_idx):
+        rows_t, rows_j = np.nonzero(top_idx == e)
+        xe = x2[rows_t].astype(np.float64)
+        h1 = (xe @ expert(fc1, fc1_scales, fc1_zp, e).astype(np.float64).T).astype(np.float32)
+        if fc1_bias is not None:
+            h1 = h1 + np.asarray(fc1_bias)[e]
+        if activation == "swiglu" and swiglu_fusion == 0 and fc3 is not None:
+            h3 = (xe @ expert(fc3, fc3_scales, fc3_zp, e).astype(np.float64).T).astype(np.float32)
+            if fc3_bias is not None:
+                h3 = h3 + np.asarray(fc3_bias)[e]
+            act = _swiglu_gate(h1, h3, alpha, beta, limit)
+        else:
+            act = _activate(h1, activation, swiglu_fusion, alpha, beta, limit)
+        o = act.astype(np.float64) @ expert(fc2, fc2_scales, fc2_zp, e).astype(np.float64).T
+        if fc2_bias is not None:
+            o = o + np.asarray(fc2_bias)[e]
+        outs[rows_t, rows_j] = o
     out = np.zeros_like(x2, dtype=np.float64)
-    for t in range(x2.shape[0]):
-        for j in range(k):
-            e = top_idx[t, j]
-            wt = weights[t, j]
-            h1 = (w1[e].astype(np.float64) @ x2[t].astype(np.float64)).astype(np.float32)
-            if fc1_bias is not None:
-                h1 = h1 + np.asarray(fc1_bias)[e]
-            if activation == "swiglu" and swiglu_fusion == 0 and w3 is not None:
-                h3 = (w3[e].astype(np.float64) @ x2[t].astype(np.float64)).astype(np.float32)
-                if fc3_bias is not None:
-                    h3 = h3 + np.asarray(fc3_bias)[e]
-                act = _swiglu_gate(h1[None], h3[None], alpha, beta, limit)[0]
-            else:
-                act = _activate(h1[None], activation, swiglu_fusion, alpha, beta, limit)[0]
-            o = w2[e].astype(np.float64) @ act.astype(np.float64)
-            if fc2_bias is not None:
-                o = o + np.asarray(fc2_bias)[e]
-            if wt != 0:
-                out[t] += wt * o
+    for j in range(k):
+        wt = weights[:, j]
+        live = wt != 0
+        out[live] += wt[live, None] * outs[live, j]
     return out.astype(np.float32).reshape(x.shape)
