@@ -530,17 +530,18 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     const int piece = a_slot<BITS>(wave * RW + s2 * RPI + a_lrow, a_lslot);  // the swizzle is its own inverse
     return a_row0 + static_cast<uint32_t>(s2) * a_rstep + piece * 16;
   };
-  auto load_a = [&](uint32_t kb, int buf) {
+  auto load_a = [&](uint32_t kb, int buf, int s_lo = 0, int s_hi = 1 << 30) {
     uint8_t* base = lds + buf * (kGemmBM * ROWB) + wave * RW * ROWB;
     if (static_cast<int64_t>(kb + 1) * CW <= K) {
 #pragma unroll
       for (int s2 = 0; s2 < LOADS; ++s2)
-        lds_dma16(a_rsrc, base + s2 * RPI * ROWB, a_off(s2), kb * (CW * 2));
+        if (s2 >= s_lo && s2 < s_hi) lds_dma16(a_rsrc, base + s2 * RPI * ROWB, a_off(s2), kb * (CW * 2));
     } else {
       // A k-block that reaches past K: through registers, zero past K. The whole offset is in
       // the VGPR operand so the buffer range check covers it.
 #pragma unroll
       for (int s2 = 0; s2 < LOADS; ++s2) {
+        if (s2 < s_lo || s2 >= s_hi) continue;
         const int row = wave * RW + s2 * RPI + a_lrow;
         const int piece = a_slot<BITS>(row, a_lslot);
         uint4_t v = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off(s2) + kb * (CW * 2), 0, 0);
@@ -558,10 +559,11 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     uint32_t s[NJ][4];
     uint32_t z[NJ][4];
   };
-  auto load_b = [&](uint32_t kb, BStage& st) {
+  auto load_b = [&](uint32_t kb, BStage& st, int t_lo = 0, int t_hi = 4) {
     const uint32_t kofs = kb * static_cast<uint32_t>(nbc) * 16;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
+      if (nt < t_lo || nt >= t_hi) continue;
       st.w[nt] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, b_base + nt * b_tstep, kb * 1024, 0);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
@@ -589,16 +591,29 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
                                  __builtin_bit_cast(half2_t, sv | (sv << 16)));
     }
   };
+  // The next k-block's loads, spread over the steps of this one so that the eight wavefronts
+  // do not queue all of them on the CU's memory path at once after each barrier: A in the first
+  // half of the steps, then the weights, so the A loads still precede the weight loads (WAIT_A).
+  constexpr int HA = STEPS > 1 ? STEPS / 2 : 1;
+  constexpr int HB = STEPS > 1 ? STEPS - HA : 1;
+  auto issue = [&](int i, uint32_t kb, int buf, BStage& st) {
+    if (i < HA) load_a(kb, buf, i * LOADS / HA, (i + 1) * LOADS / HA);
+    if (STEPS == 1 || i >= HA) {
+      const int ib = STEPS == 1 ? 0 : i - HA;
+      load_b(kb, st, ib * 4 / HB, (ib + 1) * 4 / HB);
+    }
+  };
   // Software pipeline over the k-block's steps: once fragment mt of step i has fed its four
   // MFMAs, the same registers take fragment mt of step i+1 from LDS; step i+1's weights are
   // dequantized (into the other of two register sets) while step i's MFMAs run.
-  auto compute = [&](int buf, const BStage& st) {
+  auto compute = [&](int buf, const BStage& st, bool more, uint32_t kbn, BStage& nst) {
     const uint8_t* abase = lds + buf * (kGemmBM * ROWB) + (wm * 128 + r) * ROWB;
     if constexpr (WN == 4) {
       // Two wavefronts per SIMD: each keeps few registers live and relies on the other to fill
       // its waits; one set of weight fragments per step, A fragments read as they are used.
 #pragma unroll
       for (int i = 0; i < STEPS; ++i) {
+        if (more) issue(i, kbn, buf ^ 1, nst);
         half8_t bc[4];
         dequant(st, i, bc);
         const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
@@ -621,6 +636,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     dequant(st, 0, b0);
 #pragma unroll
     for (int i = 0; i < STEPS; ++i) {
+      if (more) issue(i, kbn, buf ^ 1, nst);
       half8_t(&bc)[4] = (i & 1) ? b1 : b0;
       half8_t(&bn)[4] = (i & 1) ? b0 : b1;
       if (i + 1 < STEPS) dequant(st, i + 1, bn);
@@ -647,12 +663,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   for (uint32_t kb = kb0; kb < kb1; ++kb) {
     const int buf = static_cast<int>((kb - kb0) & 1);
     const bool more = kb + 1 < kb1;
-    if (more) {
-      load_a(kb + 1, buf ^ 1);
-      __builtin_amdgcn_sched_barrier(0);  // keep the A loads ahead of the B loads (WAIT_A)
-      load_b(kb + 1, next);
-    }
-    compute(buf, cur);
+    compute(buf, cur, more, kb + 1, next);
     if (more) {
       __builtin_amdgcn_s_waitcnt(WAIT_A);
     }
