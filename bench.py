@@ -373,7 +373,8 @@ COPY_BYTES = 256 << 20
 def profile_run(ctx, kind, steps):
     """A short, graph-free run for rocprofv3: `decode` runs the M=1 projection sweep over one
     weight copy plus one 256 MiB device copy (the calibration of the memory counters);
-    `prefill` runs the SmolLM3-3B projections at M=2048; `moe` the quantized MoE layer."""
+    `prefill` runs the SmolLM3-3B projections at M=2048; `moe` the quantized MoE layer; `vocab`
+    the lm_head MatMulNBits and the GatherBlockQuantized lookup at the 151936 x 1024 shape."""
     global USE_GRAPHS
     USE_GRAPHS = False
     if kind == "decode":
@@ -386,6 +387,8 @@ def profile_run(ctx, kind, steps):
         ctx.synchronize()
     elif kind == "moe":
         moe_ffn(ctx, steps, per_graph=1)
+    elif kind == "vocab":
+        large_vocab(ctx, steps, per_graph=3)
     else:
         prefill(ctx, steps, [2048])
 
@@ -439,7 +442,7 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-graph", action="store_true", help="launch each call on the stream, no HIP graphs")
-    p.add_argument("--profile", choices=["decode", "prefill", "moe"], help="a short graph-free run for rocprofv3")
+    p.add_argument("--profile", choices=["decode", "prefill", "moe", "vocab"], help="a short graph-free run for rocprofv3")
     p.add_argument("--summarize", nargs="*", metavar="PATH",
                    help="print a markdown summary of rocprofv3 output: a kernel_stats.csv, then --pmc directories")
     args = p.parse_args()
