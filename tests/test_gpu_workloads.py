@@ -1,5 +1,7 @@
-"""The benchmark workloads at their full sizes against the oracle: the Qwen3-0.6B decode
-projections (q4, block 32, packed zero points, M in {1, 4, 8, 16}), the SmolLM3-3B prefill
+"""The benchmark workloads at their full sizes against the oracle: the single op of the CPU
+path (f32 A [1, 1024], q4 block 32 B [3072, 32, 16], f32 scales, no zero points; f32 Y within
+1e-3), the Qwen3-0.6B decode projections (q4, block 32, packed zero points, M in {1, 4, 8,
+16}), the SmolLM3-3B prefill
 projections (q4, block 128, M in {256, 2048}), the 151936 x 1024 lm_head (M = 8) and the
 Qwen3-30B-A3B QMoE layer (128 experts, top-8, 2048/768, swiglu, 512 tokens). Outputs within
 max|Y - Y_ref| / max|Y_ref| <= 1e-2 (f16 activations); QMoE within 2e-2 * max|ref|; the
@@ -43,6 +45,23 @@ def check_matmul(ctx, name, k, n, bs, ms, scale_mul):
             assert err <= 1e-2, f"{name} M={m}: relative error {err}"
     finally:
         w.free()
+
+
+def test_single_op_f32(ctx):
+    k, n = 1024, 3072
+    print(f"single op f32 K={k} N={n} M=1", flush=True)
+    rng = np.random.default_rng(1)
+    b, s, z = nbits_weight(rng, k, n, 4, 32, zp="none", scale_dtype=np.float32)
+    w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=4, block_size=32, weight_dtype="f32")
+    try:
+        a = rng.standard_normal((1, k)).astype(np.float32)
+        y = matmul_nbits(ctx.put(a), w).numpy()
+    finally:
+        w.free()
+    ref = o.matmul_nbits(a, b, s, z, k=k, n=n, bits=4, block_size=32)
+    assert y.dtype == np.float32 and ref.dtype == np.float32 and y.shape == (1, n)
+    err = rel_err(y.astype(np.float64), ref.astype(np.float64))
+    assert err <= 1e-3, f"relative error {err}"
 
 
 @pytest.mark.parametrize("proj", QWEN3_0_6B, ids=lambda p: p[0])
