@@ -958,8 +958,9 @@ void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
 // so a capture that finds it too small runs without splitting.
 // Tile shape and K split of one prefill GEMM. Each candidate (256 x 128 or 256 x 256 tiles,
 // 1-8 splits of K) is priced as rounds of workgroups over the CUs times the work of one, at the
-// per-CU rates the two tile shapes sustain on MI355X (2.71 and 3.27 dense f16 TFLOP/s per CU
-// at K = 4096), plus the f32 partial sums a split writes and the reduction reads back.
+// per-CU rates the two tile shapes sustain on MI355X with every CU busy (2.8 and 3.5 dense f16
+// TFLOP/s per CU, measured on the SmolLM3-3B and 2048x4096x8192 shapes), plus the f32 partial
+// sums a split writes and the reduction reads back.
 struct GemmPlan {
   int wn, splits, cps;
 };
@@ -971,14 +972,17 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
   double best_t = 1e30;
   for (int wn : {2, 4}) {
     const int64_t tiles = mblocks * ((ntiles + 4 * wn - 1) / (4 * wn));
-    const double chunk_s = 2.0 * kGemmBM * 64.0 * wn * cw / (wn == 4 ? 3.27e12 : 2.71e12);
+    const double chunk_s = 2.0 * kGemmBM * 64.0 * wn * cw / (wn == 4 ? 3.5e12 : 2.8e12);
     for (int64_t splits = 1; splits <= 8; ++splits) {
       if (splits > 1 && 2 * splits > nchunks) break;
       const int64_t cps = (nchunks + splits - 1) / splits;
       const int64_t used = (nchunks + cps - 1) / cps;
       if (used != splits) continue;
-      const int64_t rounds = (tiles * splits + cus - 1) / cus;
-      double t = static_cast<double>(rounds) * cps * chunk_s;
+      // A last round that occupies a fraction f of the CUs runs each workgroup faster (less
+      // memory contention, a higher clock): priced at 0.6 + 0.4 f of a full round.
+      const int64_t wgs = tiles * splits, full = wgs / cus, rem = wgs % cus;
+      const double rounds = static_cast<double>(full) + (rem ? 0.6 + 0.4 * static_cast<double>(rem) / cus : 0.0);
+      double t = rounds * cps * chunk_s;
       if (splits > 1) t += 2.0 * splits * M * N * 4 / 5e12;
       if (t < best_t) {
         best_t = t;
