@@ -18,6 +18,7 @@
 // intermediate in expert order; the final sum reads them back per token, slot by slot.
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 #include <cstdio>
 #include <vector>
 
@@ -310,42 +311,56 @@ __global__ __launch_bounds__(512) void k_moe_gemm_f16(
   for (int v = 0; v < NW; ++v)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[v][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  uint4_t av[LOADS];
-  WStage cur, next;
-  load_a(0, av);
-  if (active) load_w(0, cur);
-  store_a(0, av);
-  __syncthreads();
-  for (uint32_t c = 0; c < nch; ++c) {
-    const bool more = c + 1 < nch;
-    if (more) {
-      load_a(c + 1, av);
-      if (active) load_w(c + 1, next);
-    }
-    if (active) {
-      const uint8_t* abase = lds + (c & 1) * ROWS * ROWB;
+  // The chunk loop, specialized for the m-tiles that hold rows of this item (MA of MT, uniform
+  // per workgroup): an item of 17-32 rows runs half the MFMAs and LDS reads of a full one.
+  auto run = [&](auto ma) {
+    constexpr int MA = decltype(ma)::value;
+    uint4_t av[LOADS];
+    WStage cur, next;
+    load_a(0, av);
+    if (active) load_w(0, cur);
+    store_a(0, av);
+    __syncthreads();
+    for (uint32_t c = 0; c < nch; ++c) {
+      const bool more = c + 1 < nch;
+      if (more) {
+        load_a(c + 1, av);
+        if (active) load_w(c + 1, next);
+      }
+      if (active) {
+        const uint8_t* abase = lds + (c & 1) * ROWS * ROWB;
 #pragma unroll
-      for (int i = 0; i < STEPS; ++i) {
-        const int piece = g * (GW / 8) + i;
-        half8_t af[MT];
+        for (int i = 0; i < STEPS; ++i) {
+          const int piece = g * (GW / 8) + i;
+          half8_t af[MA];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          af[mt] = *reinterpret_cast<const half8_t*>(abase + (mt * 16 + r) * ROWB + a_slot_moe<BITS>(mt * 16 + r, piece) * 16);
-        const int j = SPLIT ? i : 0;
+          for (int mt = 0; mt < MA; ++mt)
+            af[mt] = *reinterpret_cast<const half8_t*>(abase + (mt * 16 + r) * ROWB + a_slot_moe<BITS>(mt * 16 + r, piece) * 16);
+          const int j = SPLIT ? i : 0;
 #pragma unroll
-        for (int v = 0; v < NW; ++v) {
-          const uint32_t zq = HAS_ZP ? 0x6400u + cur.z[v][j] : 0x6400u + (1u << (BITS - 1));
-          const half8_t b = unpack_step<BITS>(cur.w[v], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
-                                              __builtin_bit_cast(half2_t, cur.s[v][j] | (cur.s[v][j] << 16)));
+          for (int v = 0; v < NW; ++v) {
+            const uint32_t zq = HAS_ZP ? 0x6400u + cur.z[v][j] : 0x6400u + (1u << (BITS - 1));
+            const half8_t b = unpack_step<BITS>(cur.w[v], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
+                                                __builtin_bit_cast(half2_t, cur.s[v][j] | (cur.s[v][j] << 16)));
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            acc[v][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[mt], acc[v][mt], 0, 0, 0);
+            for (int mt = 0; mt < MA; ++mt)
+              acc[v][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[mt], acc[v][mt], 0, 0, 0);
+          }
         }
       }
+      if (more) store_a((c + 1) & 1, av);
+      __syncthreads();
+      if (more) cur = next;
     }
-    if (more) store_a((c + 1) & 1, av);
-    __syncthreads();
-    if (more) cur = next;
+  };
+  const int used = (it.rows + 15) / 16;
+  if (MT >= 4 && used > 2) {
+    if (used > 3) run(std::integral_constant<int, MT>{});
+    else run(std::integral_constant<int, MT >= 4 ? 3 : MT>{});
+  } else if (MT >= 2 && used > 1) {
+    run(std::integral_constant<int, MT >= 2 ? 2 : MT>{});
+  } else {
+    run(std::integral_constant<int, 1>{});
   }
   if (!active) return;
   // Lane (16g + r) holds rows mt*16 + r and columns lt*16 + 4g .. +3.
