@@ -616,13 +616,20 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
         if (more) issue(i, kbn, buf ^ 1, nst);
         half8_t bc[4];
         dequant(st, i, bc);
+        // A fragment mt + 1 is read while fragment mt feeds its four MFMAs; the scheduling
+        // barriers keep the compiler from sinking each read next to its first use.
         const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
+        half8_t a = *reinterpret_cast<const half8_t*>(abase + slot);
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) {
-          const half8_t a = *reinterpret_cast<const half8_t*>(abase + mt * 16 * ROWB + slot);
+          half8_t an;
+          if (mt + 1 < 8) an = *reinterpret_cast<const half8_t*>(abase + (mt + 1) * 16 * ROWB + slot);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int nt = 0; nt < 4; ++nt)
             acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[nt], a, acc[mt][nt], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          if (mt + 1 < 8) a = an;
         }
       }
       return;
