@@ -610,7 +610,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     const uint8_t* abase = lds + buf * (kGemmBM * ROWB) + (wm * 128 + r) * ROWB;
     if constexpr (WN == 4) {
       // Two wavefronts per SIMD: each keeps few registers live and relies on the other to fill
-      // its waits; one set of weight fragments per step, A fragments read as they are used.
+      // its waits; one set of weight fragments per step, A fragments read one ahead of use.
 #pragma unroll
       for (int i = 0; i < STEPS; ++i) {
         if (more) issue(i, kbn, buf ^ 1, nst);
