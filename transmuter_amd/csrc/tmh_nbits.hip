@@ -449,11 +449,14 @@ __global__ __launch_bounds__(256) void k_gemm_f16(
 // one wavefront per SIMD; WN = 4: 256 x 256, two per SIMD), k-blocks of one chunk (CW weights).
 //  - A: the k-block's 256 rows x CW f16 go global -> LDS by buffer_load ... lds (no VGPRs),
 //    double buffered, rows of CW*2 bytes whose 16-byte pieces are XOR-swizzled by row so the
-//    MFMA fragment reads of 16 rows hit distinct banks. Rows past M read row M-1 (their outputs
-//    are never stored). A partial last k-block goes through registers and is zeroed past K.
-//  - B: wavefront (wm, wn) computes rows 128*wm.. and columns 64*wn..; its four 16-column
-//    weight tiles and their scales and zero points are loaded one k-block ahead and dequantized
-//    in registers (exact f16), each fragment feeding eight v_mfma_f32_16x16x32_f16.
+//    MFMA fragment reads of 16 rows hit distinct banks. Rows past M lie outside the buffer
+//    range and read zeros (their outputs are never stored). A partial last k-block goes through
+//    registers and is zeroed past K.
+//  - B: with WN = 2, wavefront (wm, wn) computes rows 128*wm.. and columns 64*wn.. (four
+//    16-column weight tiles, each dequantized fragment feeding eight MFMAs); with WN = 4, each
+//    wavefront computes all 256 rows of two tiles (each fragment feeding sixteen). The tiles'
+//    weights, scales and zero points are loaded one k-block ahead and dequantized in registers
+//    (exact f16) for v_mfma_f32_16x16x32_f16.
 constexpr int kGemmBM = 256;
 
 template <int BITS>
@@ -494,11 +497,17 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   constexpr int RW = kGemmBM / (2 * WN); // A rows each wavefront brings into LDS
   constexpr int LOADS = RW / RPI;        // load instructions per wavefront per k-block
   constexpr int NJ = SPLIT ? STEPS : 1;  // parameter entries per tile per k-block
+  // WN == 4 (eight wavefronts, two per SIMD): each wavefront takes all 256 rows and two weight
+  // tiles, so every dequantized fragment feeds 16 MFMAs. WN == 2 (four wavefronts): 128 rows and
+  // four tiles per wavefront.
+  constexpr bool TALL = WN == 4;
+  constexpr int MTW = TALL ? 16 : 8;
+  constexpr int NTW = TALL ? 2 : 4;
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int wm = wave / WN, wn = wave % WN;
+  const int wm = TALL ? 0 : wave / WN, wn = TALL ? wave : wave % WN;
   // Consecutive workgroups take the m-blocks of one n-block, so each XCD keeps one m-block's
   // A rows in its L2 while the weights stream past.
   // With split K (ws != nullptr), workgroup blocks of mblocks*nblocks take consecutive ranges of
@@ -509,7 +518,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   const int mb = static_cast<int>(tile % static_cast<unsigned>(mblocks));
   const int nb = static_cast<int>(tile / static_cast<unsigned>(mblocks));
   const int m0 = mb * kGemmBM;
-  const int t0 = (nb * WN + wn) * 4;
+  const int t0 = TALL ? nb * 4 * WN + wave * NTW : (nb * WN + wn) * 4;
   const uint32_t nch = static_cast<uint32_t>(nchunks);
   const uint32_t kb0 = static_cast<uint32_t>(split) * static_cast<uint32_t>(chunks_per_split);
   const uint32_t kb1 = kb0 + chunks_per_split < nch ? kb0 + chunks_per_split : nch;
@@ -555,14 +564,14 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   const uint32_t p_base = (static_cast<uint32_t>(t0) * nch * nbc + ((g * GW) >> bsc_shift)) * 16 + r;
   const uint32_t p_tstep = nch * static_cast<uint32_t>(nbc) * 16;
   struct BStage {
-    uint4_t w[4];
-    uint32_t s[NJ][4];
-    uint32_t z[NJ][4];
+    uint4_t w[NTW];
+    uint32_t s[NJ][NTW];
+    uint32_t z[NJ][NTW];
   };
-  auto load_b = [&](uint32_t kb, BStage& st, int t_lo = 0, int t_hi = 4) {
+  auto load_b = [&](uint32_t kb, BStage& st, int t_lo = 0, int t_hi = 1 << 30) {
     const uint32_t kofs = kb * static_cast<uint32_t>(nbc) * 16;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int nt = 0; nt < NTW; ++nt) {
       if (nt < t_lo || nt >= t_hi) continue;
       st.w[nt] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, b_base + nt * b_tstep, kb * 1024, 0);
 #pragma unroll
@@ -575,15 +584,15 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     }
   };
 
-  float4_t acc[8][4];
+  float4_t acc[MTW][NTW];
 #pragma unroll
-  for (int a = 0; a < 8; ++a)
+  for (int a = 0; a < MTW; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < NTW; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  auto dequant = [&](const BStage& st, int i, half8_t (&bf)[4]) {
+  auto dequant = [&](const BStage& st, int i, half8_t (&bf)[NTW]) {
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int nt = 0; nt < NTW; ++nt) {
       const int j = SPLIT ? i : 0;
       const uint32_t sv = st.s[j][nt];
       const uint32_t zv = HAS_ZP ? 0x6400u + st.z[j][nt] : 0x6400u + (1u << (BITS - 1));
@@ -600,7 +609,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     if (i < HA) load_a(kb, buf, i * LOADS / HA, (i + 1) * LOADS / HA);
     if (STEPS == 1 || i >= HA) {
       const int ib = STEPS == 1 ? 0 : i - HA;
-      load_b(kb, st, ib * 4 / HB, (ib + 1) * 4 / HB);
+      load_b(kb, st, ib * NTW / HB, (ib + 1) * NTW / HB);
     }
   };
   // Software pipeline over the k-block's steps: once fragment mt of step i has fed its four
@@ -614,27 +623,27 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
 #pragma unroll
       for (int i = 0; i < STEPS; ++i) {
         if (more) issue(i, kbn, buf ^ 1, nst);
-        half8_t bc[4];
+        half8_t bc[NTW];
         dequant(st, i, bc);
         // A fragment mt + 1 is read while fragment mt feeds its four MFMAs; the scheduling
         // barriers keep the compiler from sinking each read next to its first use.
         const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
         half8_t a = *reinterpret_cast<const half8_t*>(abase + slot);
 #pragma unroll
-        for (int mt = 0; mt < 8; ++mt) {
+        for (int mt = 0; mt < MTW; ++mt) {
           half8_t an;
-          if (mt + 1 < 8) an = *reinterpret_cast<const half8_t*>(abase + (mt + 1) * 16 * ROWB + slot);
+          if (mt + 1 < MTW) an = *reinterpret_cast<const half8_t*>(abase + (mt + 1) * 16 * ROWB + slot);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int nt = 0; nt < 4; ++nt)
+          for (int nt = 0; nt < NTW; ++nt)
             acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[nt], a, acc[mt][nt], 0, 0, 0);
           __builtin_amdgcn_sched_barrier(0);
-          if (mt + 1 < 8) a = an;
+          if (mt + 1 < MTW) a = an;
         }
       }
       return;
     }
-    half8_t af[8], b0[4], b1[4];
+    half8_t af[8], b0[NTW], b1[NTW];
     {
       const int slot = a_slot<BITS>(r, g * (GW / 8)) * 16;
 #pragma unroll
@@ -644,14 +653,14 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
 #pragma unroll
     for (int i = 0; i < STEPS; ++i) {
       if (more) issue(i, kbn, buf ^ 1, nst);
-      half8_t(&bc)[4] = (i & 1) ? b1 : b0;
-      half8_t(&bn)[4] = (i & 1) ? b0 : b1;
+      half8_t(&bc)[NTW] = (i & 1) ? b1 : b0;
+      half8_t(&bn)[NTW] = (i & 1) ? b0 : b1;
       if (i + 1 < STEPS) dequant(st, i + 1, bn);
       const int slot = a_slot<BITS>(r, g * (GW / 8) + i + 1) * 16;
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) {
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)  // weights as the first operand: lane holds 4 columns of one row
+        for (int nt = 0; nt < NTW; ++nt)  // weights as the first operand: lane holds 4 columns of one row
           acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[nt], af[mt], acc[mt][nt], 0, 0, 0);
         if (i + 1 < STEPS) af[mt] = *reinterpret_cast<const half8_t*>(abase + mt * 16 * ROWB + slot);
       }
@@ -659,7 +668,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   };
   // Loads issued after the A tile of a k-block: its weights, scales and zero points. Waiting
   // until only these are outstanding means the A tile has landed in LDS.
-  constexpr int B_LOADS = 4 + 4 * NJ + (HAS_ZP ? 4 * NJ : 0);
+  constexpr int B_LOADS = NTW + NTW * NJ + (HAS_ZP ? NTW * NJ : 0);
   constexpr int WAIT_A = (B_LOADS & 15) | (7 << 4) | (15 << 8) | ((B_LOADS >> 4) << 14);
 
   BStage cur, next;
@@ -681,11 +690,11 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   const bool f16_out = y_dt == DT_F16 && dot_dt == DT_F16 && !bias;
   const bool vec_out = (ldy % 4) == 0;
 #pragma unroll
-  for (int mt = 0; mt < 8; ++mt) {
+  for (int mt = 0; mt < MTW; ++mt) {
     const int64_t m = m0 + wm * 128 + mt * 16 + r;
     if (m >= M) continue;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int nt = 0; nt < NTW; ++nt) {
       const int64_t n = static_cast<int64_t>(t0 + nt) * 16 + 4 * g;
       if (n >= N) continue;
       const float4_t v = acc[mt][nt];
