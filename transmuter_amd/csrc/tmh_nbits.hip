@@ -625,7 +625,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
         if (more) issue(i, kbn, buf ^ 1, nst);
         half8_t bc[NTW];
         dequant(st, i, bc);
-        // A fragment mt + 1 is read while fragment mt feeds its four MFMAs; the scheduling
+        // A fragment mt + 1 is read while fragment mt feeds its MFMAs; the scheduling
         // barriers keep the compiler from sinking each read next to its first use.
         const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
         half8_t a = *reinterpret_cast<const half8_t*>(abase + slot);
@@ -974,7 +974,7 @@ void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
 // so a capture that finds it too small runs without splitting.
 // Tile shape and K split of one prefill GEMM. Each candidate (256 x 128 or 256 x 256 tiles,
 // 1-8 splits of K) is priced as rounds of workgroups over the CUs times the work of one, at the
-// per-CU rates the two tile shapes sustain on MI355X with every CU busy (2.8 and 3.5 dense f16
+// per-CU rates the two tile shapes sustain on MI355X with every CU busy (2.8 and 3.9 dense f16
 // TFLOP/s per CU, measured on the SmolLM3-3B and 2048x4096x8192 shapes), plus the f32 partial
 // sums a split writes and the reduction reads back.
 struct GemmPlan {
@@ -988,7 +988,7 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
   double best_t = 1e30;
   for (int wn : {2, 4}) {
     const int64_t tiles = mblocks * ((ntiles + 4 * wn - 1) / (4 * wn));
-    const double chunk_s = 2.0 * kGemmBM * 64.0 * wn * cw / (wn == 4 ? 3.5e12 : 2.8e12);
+    const double chunk_s = 2.0 * kGemmBM * 64.0 * wn * cw / (wn == 4 ? 3.9e12 : 2.8e12);
     for (int64_t splits = 1; splits <= 8; ++splits) {
       if (splits > 1 && 2 * splits > nchunks) break;
       const int64_t cps = (nchunks + splits - 1) / splits;
