@@ -94,6 +94,10 @@ MATMUL_CASES = [
     (8, 128, "none", 256, 50008, [1, 16], "f16", "f16", None),
     (4, 32, "packed", 4096, 12000, [1, 9], "f16", "f16", None),
     (4, 16, "packed", 512, 40000, [1, 5], "f16", "f16", None),
+    # prefill tile shapes with a ragged last m-block: 256x256 tiles over 8-bit weights, and a
+    # whole-GPU 256x256 grid over 4-bit weights
+    (8, 32, "packed", 2048, 8192, [300], "f16", "f16", None),
+    (4, 128, "packed", 4096, 8192, [2011], "f16", "f16", "f16"),
 ]
 
 
