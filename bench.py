@@ -34,6 +34,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA
 
 # Qwen3-0.6B decode projections: (name, K, N)
 QWEN3_06B = [("q", 1024, 2048), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 2048, 1024),
@@ -325,6 +326,57 @@ def moe_ffn(ctx, reps, per_graph=4):
             "weight_gbs": weight_bytes / (us * 1e-6) / 1e9}
 
 
+# ---------------------------------------------------------------- 8-bit integer path
+
+
+def int8_ops(ctx, reps, per_graph=8, m=2048, k=2048, n=2048):
+    """The dynamic-quantization path at a 2048 x 2048 x 2048 projection: DynamicQuantizeLinear of
+    f32 activations, MatMulInteger of u8 activations (one zero point) with u8 weights (a zero
+    point per column) into s32 on the int8 MFMA, and a per-axis DequantizeLinear of u8 [2048,
+    2048] to f32. `per_graph` calls per HIP graph."""
+    from transmuter_amd._lib import F32, U8, QPARAM_AXIS, lib
+
+    rng = np.random.default_rng(7)
+    x = ctx.put(rng.standard_normal((m, k), dtype=np.float32))
+    xq, xs, xz = ctx.empty((m, k), "u8"), ctx.empty((), "f32"), ctx.empty((), "u8")
+    bq = ctx.put(rng.integers(0, 256, (k, n), dtype=np.uint8))
+    bz = ctx.put(rng.integers(0, 256, n, dtype=np.uint8))
+    y = ctx.empty((m, n), "s32")
+    scale = ctx.put((np.abs(rng.standard_normal(k)) * 0.01 + 1e-3).astype(np.float32))
+    dq = ctx.empty((m, k), "f32")
+
+    def dql():
+        ctx.check(lib().tmh_dynamic_quantize_linear(ctx.handle, x.ptr, F32, m * k, xq.ptr, xs.ptr, xz.ptr, None))
+
+    def mmi():
+        ctx.check(lib().tmh_matmul_integer(ctx.handle, xq.ptr, U8, bq.ptr, U8, xz.ptr, 1, bz.ptr, n, 1, m, k, n, 0,
+                                           y.ptr, None))
+
+    def dl():
+        ctx.check(lib().tmh_dequantize_linear(ctx.handle, xq.ptr, U8, m, k, 1, scale.ptr, F32, None, 0, QPARAM_AXIS,
+                                              0, dq.ptr, None))
+
+    out = {}
+    for name, fn in (("dynamic_quantize_linear", dql), ("matmul_integer", mmi), ("dequantize_linear", dl)):
+        fn()  # eager first: sizes the workspace before capture
+        ctx.synchronize()
+        g = Graph(ctx, lambda fn=fn: [fn() for _ in range(per_graph)])
+        us = time_graphs(ctx, [g], reps, 3) * 1e3 / (reps * per_graph)
+        g.destroy()
+        out[name] = {"us": us}
+    out["dynamic_quantize_linear"]["gbs"] = m * k * 5 / (out["dynamic_quantize_linear"]["us"] * 1e-6) / 1e9
+    out["matmul_integer"]["tops"] = 2 * m * k * n / (out["matmul_integer"]["us"] * 1e-6) / 1e12
+    out["matmul_integer"]["frac_of_int8_peak"] = out["matmul_integer"]["tops"] / INT8_PEAK_TOPS
+    out["dequantize_linear"]["gbs"] = m * k * 5 / (out["dequantize_linear"]["us"] * 1e-6) / 1e9
+    log(f"int8 {m}x{k}x{n}: DynamicQuantizeLinear {out['dynamic_quantize_linear']['us']:.1f} us "
+        f"({out['dynamic_quantize_linear']['gbs']:.0f} GB/s), MatMulInteger {out['matmul_integer']['us']:.1f} us "
+        f"({out['matmul_integer']['tops']:.0f} TOP/s), DequantizeLinear {out['dequantize_linear']['us']:.1f} us "
+        f"({out['dequantize_linear']['gbs']:.0f} GB/s)")
+    for t in (x, xq, xs, xz, bq, bz, y, scale, dq):
+        t.free()
+    return out
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 
@@ -374,7 +426,8 @@ def profile_run(ctx, kind, steps):
     """A short, graph-free run for rocprofv3: `decode` runs the M=1 projection sweep over one
     weight copy plus one 256 MiB device copy (the calibration of the memory counters);
     `prefill` runs the SmolLM3-3B projections at M=2048; `moe` the quantized MoE layer; `vocab`
-    the lm_head MatMulNBits and the GatherBlockQuantized lookup at the 151936 x 1024 shape."""
+    the lm_head MatMulNBits and the GatherBlockQuantized lookup at the 151936 x 1024 shape; `int8`
+    DynamicQuantizeLinear, MatMulInteger and DequantizeLinear at 2048 x 2048 x 2048."""
     global USE_GRAPHS
     USE_GRAPHS = False
     if kind == "decode":
@@ -389,6 +442,8 @@ def profile_run(ctx, kind, steps):
         moe_ffn(ctx, steps, per_graph=1)
     elif kind == "vocab":
         large_vocab(ctx, steps, per_graph=3)
+    elif kind == "int8":
+        int8_ops(ctx, steps, per_graph=1)
     else:
         prefill(ctx, steps, [2048])
 
@@ -442,7 +497,7 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-graph", action="store_true", help="launch each call on the stream, no HIP graphs")
-    p.add_argument("--profile", choices=["decode", "prefill", "moe", "vocab"], help="a short graph-free run for rocprofv3")
+    p.add_argument("--profile", choices=["decode", "prefill", "moe", "vocab", "int8"], help="a short graph-free run for rocprofv3")
     p.add_argument("--summarize", nargs="*", metavar="PATH",
                    help="print a markdown summary of rocprofv3 output: a kernel_stats.csv, then --pmc directories")
     args = p.parse_args()
@@ -473,6 +528,7 @@ def main():
         extra["prefill"] = prefill(ctx, 20, [256, 2048])
         extra["large_vocab"] = large_vocab(ctx, 50)
         extra["moe"] = moe_ffn(ctx, 20)
+        extra["int8"] = int8_ops(ctx, 20)
     head = dec[1]
     roofline = {
         "bound": "hbm", "kernel": "k_gemv_lean<4,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
@@ -504,6 +560,7 @@ def main():
         line["prefill_frac_M2048"] = extra["prefill"][2048]["tflops"] / MFMA_F16_PEAK_TFLOPS
         line["large_vocab"] = extra["large_vocab"]
         line["moe"] = extra["moe"]
+        line["int8"] = extra["int8"]
     ctx.close()
     print(json.dumps(line), flush=True)
 
