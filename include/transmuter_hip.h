@@ -18,7 +18,7 @@
  *  - `stream` is a hipStream_t; NULL means the context's own stream. Calls are asynchronous
  *    on that stream unless stated otherwise.
  *  - Shapes are int64_t element counts; no call reads or writes outside the extents given.
- *  - Prefill MatMulNBits (split K), MatMulInteger, DynamicQuantizeLinear and QMoE keep
+ *  - Prefill MatMulNBits (split K), DynamicQuantizeLinear and QMoE keep
  *    intermediates in one workspace per context, grown outside graph capture. Calls of one
  *    context on two streams must not run at the same time; use a context per concurrent stream.
  */

@@ -215,204 +215,217 @@ __global__ __launch_bounds__(256) void k_dequantize_linear(
   store_as<OUT>(y, e, prod);
 }
 
-// ------------------------------------------------------------------ MatMulInteger
-
-constexpr int kMiTile = 16;
-constexpr int kMiK = 64;
-
-// y[bt, m, n] = sum_k (a - a_zero[m]) (b - b_zero[n]), wrapping mod 2^32. Each f32 chunk sum of
-// the reference is exact, so the exact integer sum is its value.
-__global__ __launch_bounds__(256) void k_matmul_integer(
-    const void* __restrict__ a, bool a_signed, const void* __restrict__ b, bool b_signed,
-    const void* __restrict__ a_zero, int64_t a_zero_count, const void* __restrict__ b_zero,
-    int64_t b_zero_count, int64_t M, int64_t K, int64_t N, bool b_batched, int32_t* __restrict__ y) {
-  __shared__ int32_t sa[kMiTile][kMiK + 1];
-  __shared__ int32_t sb[kMiK][kMiTile + 1];
-  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-  const int64_t bt = blockIdx.z;
-  const int64_t m = static_cast<int64_t>(blockIdx.y) * kMiTile + ty;
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * kMiTile + tx;
-  const auto* a8 = static_cast<const uint8_t*>(a) + bt * M * K;
-  const auto* b8 = static_cast<const uint8_t*>(b) + (b_batched ? bt * K * N : 0);
-  auto av = [&](int64_t mm, int64_t kk) -> int32_t {
-    const uint8_t raw = a8[mm * K + kk];
-    int32_t v = a_signed ? static_cast<int8_t>(raw) : raw;
-    if (a_zero) {
-      const uint8_t z = static_cast<const uint8_t*>(a_zero)[a_zero_count == 1 ? 0 : mm];
-      v -= a_signed ? static_cast<int8_t>(z) : z;
-    }
-    return v;
-  };
-  auto bv = [&](int64_t kk, int64_t nn) -> int32_t {
-    const uint8_t raw = b8[kk * N + nn];
-    int32_t v = b_signed ? static_cast<int8_t>(raw) : raw;
-    if (b_zero) {
-      const uint8_t z = static_cast<const uint8_t*>(b_zero)[b_zero_count == 1 ? 0 : nn];
-      v -= b_signed ? static_cast<int8_t>(z) : z;
-    }
-    return v;
-  };
-  uint32_t acc = 0;
-  for (int64_t k0 = 0; k0 < K; k0 += kMiK) {
-    for (int idx = threadIdx.x; idx < kMiTile * kMiK; idx += 256) {
-      const int rr = idx / kMiK, kk = idx % kMiK;
-      const int64_t gm = static_cast<int64_t>(blockIdx.y) * kMiTile + rr;
-      sa[rr][kk] = (gm < M && k0 + kk < K) ? av(gm, k0 + kk) : 0;
-      const int kb = idx / kMiTile, cc = idx % kMiTile;
-      const int64_t gn = static_cast<int64_t>(blockIdx.x) * kMiTile + cc;
-      sb[kb][cc] = (gn < N && k0 + kb < K) ? bv(k0 + kb, gn) : 0;
-    }
-    __syncthreads();
-#pragma unroll 8
-    for (int kk = 0; kk < kMiK; ++kk) acc += static_cast<uint32_t>(sa[ty][kk] * sb[kk][tx]);
-    __syncthreads();
-  }
-  if (m < M && n < N) y[(bt * M + m) * N + n] = static_cast<int32_t>(acc);
-}
-
-
 // ------------------------------------------------------------------ MatMulInteger on int8 MFMA
 
-// With a = sa + oa (sa the s8 form of a: the byte itself for s8 data, a ^ 0x80 = a - 128 for
-// u8 data, so oa is 0 or 128) and likewise b:
+// y[bt, m, n] = sum_k (a - a_zero[m]) (b - b_zero[n]), wrapping mod 2^32. Each f32 chunk sum of
+// the reference is exact, so the exact integer sum is its value. With a = sa + oa (sa the s8
+// form of a: the byte itself for s8 data, a ^ 0x80 = a - 128 for u8 data, so oa is 0 or 128)
+// and likewise b:
 //   sum_k (a - az_m)(b - bz_n) = sum_k sa sb + cb_n * rs_m + ca_m * cs_n + K * ca_m * cb_n
 // with ca_m = oa - az_m, cb_n = ob - bz_n, rs_m = sum_k sa[m][k], cs_n = sum_k sb[k][n], all
-// modulo 2^32 (the s32 wrap of the exact sum). The sa sb sums run on v_mfma_i32_16x16x64_i8.
-
-// rs for every row of every A batch, cs for every column of every B batch.
-__global__ __launch_bounds__(256) void k_int8_sums(const uint8_t* __restrict__ a, bool a_signed,
-                                                    const uint8_t* __restrict__ b, bool b_signed, int64_t a_rows,
-                                                    int64_t K, int64_t N, int64_t b_batches, int32_t* __restrict__ rs,
-                                                    int32_t* __restrict__ cs) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < a_rows) {
-    const uint8_t* row = a + i * K;
-    uint32_t sum = 0;
-    for (int64_t k = 0; k < K; ++k) sum += static_cast<uint32_t>(static_cast<int8_t>(a_signed ? row[k] : row[k] ^ 0x80));
-    rs[i] = static_cast<int32_t>(sum);
-  }
-  const int64_t j = i - a_rows;
-  if (j >= 0 && j < b_batches * N) {
-    const int64_t bt = j / N, n = j - bt * N;
-    const uint8_t* col = b + bt * K * N + n;
-    uint32_t sum = 0;
-    for (int64_t k = 0; k < K; ++k)
-      sum += static_cast<uint32_t>(static_cast<int8_t>(b_signed ? col[k * N] : col[k * N] ^ 0x80));
-    cs[j] = static_cast<int32_t>(sum);
-  }
-}
+// modulo 2^32. The sa sb sums run on v_mfma_i32_16x16x64_i8; rs and cs are summed (v_dot4
+// against ones) from the same bytes as they are staged into LDS.
 
 constexpr int kI8Tile = 128;  // output rows and columns per workgroup
-constexpr int kI8K = 64;      // k per step (one MFMA deep)
-constexpr int kI8Row = 80;    // LDS bytes per row of 64: 16-byte pieces of 8 consecutive rows on distinct banks
+constexpr int kI8K = 128;     // k per step: two MFMAs deep
 
-// 128 x 128 outputs per workgroup of four wavefronts (64 x 64 each, 4 x 4 MFMA tiles). Per
-// k-step A's rows and B's columns go to LDS as s8 bytes, B transposed through 4 x 4 byte
-// blocks, zeros outside the matrices.
+// LDS tiles hold 128 rows (A rows, or B columns) of 128 k-bytes, no padding; the 16-byte chunk
+// c of row x sits at chunk c ^ ((x & 7) ^ ((x >> 4) & 7)). Eight consecutive rows reading one
+// chunk (an MFMA fragment read) then hit eight different chunks, and so do the rows 16 apart
+// that one wavefront's 4-byte B writes cover.
+__device__ __forceinline__ int i8_lds_offset(int x, int chunk) {
+  return x * kI8K + ((chunk ^ ((x & 7) ^ ((x >> 4) & 7))) << 4);
+}
+
+__device__ __forceinline__ uint32_t dot4_ones(uint32_t w, uint32_t acc) {
+  return static_cast<uint32_t>(__builtin_amdgcn_sdot4(static_cast<int>(w), 0x01010101, static_cast<int>(acc), false));
+}
+
+// 128 x 128 outputs per workgroup of four wavefronts (64 x 64 each, 4 x 4 MFMA tiles). Each
+// k-step's A rows (16 bytes per load) and B rows (4 k-rows x 16 columns per thread) are read into
+// registers while the previous step's MFMAs run, then stored to LDS as s8: A as is, B transposed
+// to k-contiguous columns through 4 x 4 byte blocks (v_perm). Zeros outside the matrices.
+// VEC: K and N are multiples of 16, both matrices 16-byte aligned, (M + 128) K and (K + 128) N
+// below 2^31; every load is then one unconditional 16-byte buffer load (a branch per load makes
+// the compiler wait for each load before the next).
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_matmul_integer_mfma(
     const uint8_t* __restrict__ a, bool a_signed, const uint8_t* __restrict__ b, bool b_signed,
-    const void* __restrict__ a_zero, int64_t a_zero_count, const void* __restrict__ b_zero,
-    int64_t b_zero_count, int64_t M, int64_t K, int64_t N, bool b_batched, const int32_t* __restrict__ rs,
-    const int32_t* __restrict__ cs, int32_t* __restrict__ y) {
-  __shared__ __align__(16) uint8_t sA[kI8Tile * kI8Row];
-  __shared__ __align__(16) uint8_t sB[kI8Tile * kI8Row];
+    const uint8_t* __restrict__ a_zero, int64_t a_zero_count, const uint8_t* __restrict__ b_zero,
+    int64_t b_zero_count, int64_t M, int64_t K, int64_t N, bool b_batched, int32_t* __restrict__ y) {
+  __shared__ __align__(16) uint8_t sA[kI8Tile * kI8K];
+  __shared__ __align__(16) uint8_t sB[kI8Tile * kI8K];
+  __shared__ uint32_t sRs[kI8Tile];
+  __shared__ uint32_t sCs[4][kI8Tile];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int r = lane & 15, g = lane >> 4;
   const int64_t bt = blockIdx.z;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kI8Tile, n0 = static_cast<int64_t>(blockIdx.x) * kI8Tile;
+  // Workgroups go to the eight XCDs round-robin by linear id. When the tile count is a multiple
+  // of 8, XCD x takes tiles [x T/8, (x+1) T/8) of an order that walks groups of four m-tiles
+  // m-fastest, so one XCD's tiles share few A rows and B columns (its own L2).
+  uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
+  const uint32_t tiles = gridDim.x * gridDim.y;
+  if (tiles % 8 == 0) tile = (tile % 8) * (tiles / 8) + tile / 8;
+  const uint32_t group = tile / (4 * gridDim.x), first_m = 4 * group;
+  const uint32_t group_m = min(4u, gridDim.y - first_m), in_group = tile - group * 4 * gridDim.x;
+  const int64_t m0 = static_cast<int64_t>(first_m + in_group % group_m) * kI8Tile;
+  const int64_t n0 = static_cast<int64_t>(in_group / group_m) * kI8Tile;
   const uint8_t* a8 = a + bt * M * K;
   const uint8_t* b8 = b + (b_batched ? bt * K * N : 0);
   const uint32_t aflip = a_signed ? 0u : 0x80808080u, bflip = b_signed ? 0u : 0x80808080u;
-  const bool a_vec = (K % 16) == 0 && (reinterpret_cast<uintptr_t>(a) % 16) == 0;
-  const bool b_vec = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(b) % 4) == 0;
+  // This thread's share of a k-step: A row (tid >> 3) + 32h, chunk tid & 7 (h = 0..3); B k-rows
+  // 4 * (tid >> 3) + i, columns 16 * (tid & 7) + j.
+  const int a_row = tid >> 3, a_chunk = tid & 7;
+  const int b_kq = tid >> 3, b_nq = tid & 7;
+  // va/vb hold the loaded bytes. For VEC the loads are unconditional, and amask (bytes to keep)
+  // and bmask (flip to apply) are applied when the bytes go to LDS, so the loads of the next
+  // step are not waited for before this step's MFMAs. The buffer resources span this batch's
+  // matrices; every offset formed stays below 2^31 (checked on the host).
+  uint4_t va[4], vb[4];
+  uint32_t amask[4] = {0u, 0u, 0u, 0u}, bmask[4] = {0u, 0u, 0u, 0u};
+  const auto a_rsrc = buffer_rsrc(a8, VEC ? static_cast<uint32_t>(M * K) : 0u);
+  const auto b_rsrc = buffer_rsrc(b8, VEC ? static_cast<uint32_t>(K * N) : 0u);
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int64_t gm = m0 + a_row + 32 * h, gk = k0 + 16 * a_chunk;
+      if constexpr (VEC) {
+        // Rows past M are out of the buffer's range (zeros); bytes past K belong to the next
+        // row and are zeroed when staged (amask); only rows < M reach an output.
+        va[h] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, static_cast<uint32_t>(gm * K + gk), 0, 0);
+        amask[h] = gk < K ? 0xFFFFFFFFu : 0u;
+      } else {
+        uint4_t v = {0u, 0u, 0u, 0u};
+        if (gm < M && gk < K)
+          for (int e = 0; e < 16; ++e)
+            if (gk + e < K) v[e >> 2] |= static_cast<uint32_t>(a8[gm * K + gk + e] ^ (aflip & 0xFFu)) << (8 * (e & 3));
+        va[h] = v;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t gk = k0 + 4 * b_kq + i, gn = n0 + 16 * b_nq;
+      if constexpr (VEC) {
+        // k-rows past K are out of range (zeros, left unflipped); columns past N read the next
+        // row's bytes, which reach only columns that are never stored.
+        vb[i] = __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, static_cast<uint32_t>(gk * N + gn), 0, 0);
+        bmask[i] = gk < K ? bflip : 0u;
+      } else {
+        uint4_t v = {0u, 0u, 0u, 0u};
+        if (gk < K && gn < N)
+          for (int e = 0; e < 16; ++e)
+            if (gn + e < N) v[e >> 2] |= static_cast<uint32_t>(b8[gk * N + gn + e] ^ (bflip & 0xFFu)) << (8 * (e & 3));
+        vb[i] = v;
+      }
+    }
+  };
+  uint32_t rsum[4] = {0u, 0u, 0u, 0u};
+  uint32_t csum[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) csum[j] = 0u;
   int4_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = int4_t{0, 0, 0, 0};
+  if (K > 0) load(0);
   for (int64_t k0 = 0; k0 < K; k0 += kI8K) {
-    // A: 128 rows x 64 bytes, 16 bytes per thread and load.
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = tid + 256 * h;
-      const int row = c >> 2, kc = (c & 3) * 16;
-      const int64_t gm = m0 + row, gk = k0 + kc;
-      uint4_t v = {0u, 0u, 0u, 0u};
-      if (gm < M) {
-        if (a_vec && gk + 16 <= K) {
-          v = *reinterpret_cast<const uint4_t*>(a8 + gm * K + gk) ^ aflip;
-        } else {
-          for (int e = 0; e < 16; ++e)
-            if (gk + e < K) v[e >> 2] |= static_cast<uint32_t>(a8[gm * K + gk + e] ^ (aflip & 0xFFu)) << (8 * (e & 3));
-        }
-      }
-      *reinterpret_cast<uint4_t*>(sA + row * kI8Row + kc) = v;
+    for (int h = 0; h < 4; ++h) {
+      const int row = a_row + 32 * h;
+      if constexpr (VEC) va[h] = (va[h] ^ aflip) & amask[h];
+      *reinterpret_cast<uint4_t*>(sA + i8_lds_offset(row, a_chunk)) = va[h];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) rsum[h] = dot4_ones(va[h][q], rsum[h]);
     }
-    // B: 64 k x 128 columns as 4 x 4 byte blocks, stored column-major (sB[n][k]).
+    // Column c of the 4 x 16 block is bytes c of vb[0..3]; word c >> 2 of each, byte c & 3.
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int u = tid + 256 * h;
-      const int kq = u >> 5, nq = u & 31;
-      const int64_t gk = k0 + 4 * kq, gn = n0 + 4 * nq;
-      uint32_t rw[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        rw[i] = 0;
-        if (gk + i < K) {
-          if (b_vec && gn + 4 <= N) {
-            rw[i] = *reinterpret_cast<const uint32_t*>(b8 + (gk + i) * N + gn) ^ bflip;
-          } else {
-            for (int e = 0; e < 4; ++e)
-              if (gn + e < N) rw[i] |= static_cast<uint32_t>(b8[(gk + i) * N + gn + e] ^ (bflip & 0xFFu)) << (8 * e);
-          }
-        }
-      }
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t x0 = vb[0][q] ^ bmask[0], x1 = vb[1][q] ^ bmask[1], x2 = vb[2][q] ^ bmask[2], x3 = vb[3][q] ^ bmask[3];
+      const uint32_t lo01 = __builtin_amdgcn_perm(x1, x0, 0x05010400u), hi01 = __builtin_amdgcn_perm(x1, x0, 0x07030602u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(x3, x2, 0x05010400u), hi23 = __builtin_amdgcn_perm(x3, x2, 0x07030602u);
+      const uint32_t col[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                               __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t col = ((rw[0] >> (8 * e)) & 0xFFu) | (((rw[1] >> (8 * e)) & 0xFFu) << 8) |
-                             (((rw[2] >> (8 * e)) & 0xFFu) << 16) | (((rw[3] >> (8 * e)) & 0xFFu) << 24);
-        *reinterpret_cast<uint32_t*>(sB + (4 * nq + e) * kI8Row + 4 * kq) = col;
+        const int n = 16 * b_nq + 4 * q + e;
+        *reinterpret_cast<uint32_t*>(sB + i8_lds_offset(n, b_kq >> 2) + 4 * (b_kq & 3)) = col[e];
+        csum[4 * q + e] = dot4_ones(col[e], csum[4 * q + e]);
       }
     }
     __syncthreads();
-    int4_t af[4], bf[4];
+    if (k0 + kI8K < K) load(k0 + kI8K);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-      af[mt] = *reinterpret_cast<const int4_t*>(sA + (wm * 64 + mt * 16 + r) * kI8Row + g * 16);
+    for (int half = 0; half < 2; ++half) {
+      int4_t af[4], bf[4];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-      bf[nt] = *reinterpret_cast<const int4_t*>(sB + (wn * 64 + nt * 16 + r) * kI8Row + g * 16);
+      for (int mt = 0; mt < 4; ++mt)
+        af[mt] = *reinterpret_cast<const int4_t*>(sA + i8_lds_offset(wm * 64 + mt * 16 + r, 4 * half + g));
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+      for (int nt = 0; nt < 4; ++nt)
+        bf[nt] = *reinterpret_cast<const int4_t*>(sB + i8_lds_offset(wn * 64 + nt * 16 + r, 4 * half + g));
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)  // B first: a lane ends with 4 consecutive columns of one row
-        acc[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[nt], af[mt], acc[mt][nt], 0, 0, 0);
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)  // B first: a lane ends with 4 consecutive columns of one row
+          acc[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[nt], af[mt], acc[mt][nt], 0, 0, 0);
+    }
     __syncthreads();
   }
+  // rs: the 8 lanes of a row (consecutive) hold its 8 chunks' sums. cs: the 8 lanes of a
+  // wavefront with one tid & 7 hold 8 of the 32 k-quads' sums, the four wavefronts the rest.
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    uint32_t v = rsum[h];
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    if (a_chunk == 0) sRs[a_row + 32 * h] = v;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    uint32_t v = csum[j];
+    v += __shfl_xor(v, 8);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (lane < 8) sCs[wave][16 * b_nq + j] = v;
+  }
+  __syncthreads();
   const uint32_t oa = a_signed ? 0u : 128u, ob = b_signed ? 0u : 128u;
-  auto zero_of = [](const void* z, int64_t count, int64_t i, bool sgn) -> uint32_t {
+  auto zero_of = [](const uint8_t* z, int64_t count, int64_t i, bool sgn) -> uint32_t {
     if (!z) return 0u;
-    const uint8_t raw = static_cast<const uint8_t*>(z)[count == 1 ? 0 : i];
+    const uint8_t raw = z[count == 1 ? 0 : i];
     return sgn ? static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(raw))) : raw;
   };
   const uint32_t kk = static_cast<uint32_t>(K);
+  const bool y_vec = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(y) % 16) == 0;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
-    const int64_t m = m0 + wm * 64 + mt * 16 + r;
+    const int ml = wm * 64 + mt * 16 + r;
+    const int64_t m = m0 + ml;
     if (m >= M) continue;
     const uint32_t ca = oa - zero_of(a_zero, a_zero_count, m, a_signed);
-    const uint32_t rsm = static_cast<uint32_t>(rs[bt * M + m]);
+    const uint32_t rsm = sRs[ml];
+    int32_t* yrow = y + (bt * M + m) * N;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      const int64_t n = n0 + wn * 64 + nt * 16 + 4 * g;
+      const int nl = wn * 64 + nt * 16 + 4 * g;
+      const int64_t n = n0 + nl;
+      if (n >= N) continue;
+      int4_t out;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        if (n + e >= N) break;
-        const uint32_t cb = ob - zero_of(b_zero, b_zero_count, n + e, b_signed);
-        const uint32_t csn = static_cast<uint32_t>(cs[(b_batched ? bt * N : 0) + n + e]);
-        const uint32_t v = static_cast<uint32_t>(acc[mt][nt][e]) + cb * rsm + ca * csn + kk * ca * cb;
-        y[(bt * M + m) * N + n + e] = static_cast<int32_t>(v);
+        const uint32_t cb = ob - zero_of(b_zero, b_zero_count, n + e < N ? n + e : n, b_signed);
+        const uint32_t csn = sCs[0][nl + e] + sCs[1][nl + e] + sCs[2][nl + e] + sCs[3][nl + e];
+        out[e] = static_cast<int32_t>(static_cast<uint32_t>(acc[mt][nt][e]) + cb * rsm + ca * csn + kk * ca * cb);
+      }
+      if (y_vec) {
+        *reinterpret_cast<int4_t*>(yrow + n) = out;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) yrow[n + e] = out[e];
       }
     }
   }
@@ -432,16 +445,9 @@ __device__ __forceinline__ void dql_params(float low, float high, float* scale, 
   *zero = static_cast<uint8_t>(fminf(fmaxf(z, 0.f), 255.f));
 }
 
-// Minimum and maximum of the block's share of x; with one block, the scale and zero point.
-__global__ __launch_bounds__(256) void k_dql_minmax(const float* __restrict__ x, int64_t n, float* __restrict__ part,
-                                                     float* __restrict__ scale, uint8_t* __restrict__ zero) {
+// Minimum and maximum of 256 values per thread (one per lane) through LDS; thread 0 ends with both.
+__device__ __forceinline__ void dql_block_range(float& lo, float& hi) {
   __shared__ float lo_s[256], hi_s[256];
-  float lo = INFINITY, hi = -INFINITY;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    lo = fminf(lo, x[i]);
-    hi = fmaxf(hi, x[i]);
-  }
   lo_s[threadIdx.x] = lo;
   hi_s[threadIdx.x] = hi;
   __syncthreads();
@@ -452,24 +458,65 @@ __global__ __launch_bounds__(256) void k_dql_minmax(const float* __restrict__ x,
     }
     __syncthreads();
   }
+  lo = lo_s[0];
+  hi = hi_s[0];
+}
+
+// Minimum and maximum of the workgroup's share of x (16-byte loads, four in flight per thread
+// when x is 16-byte aligned); with one workgroup, the scale and zero point.
+__global__ __launch_bounds__(256) void k_dql_minmax(const float* __restrict__ x, int64_t n, float* __restrict__ part,
+                                                     float* __restrict__ scale, uint8_t* __restrict__ zero) {
+  float lo = INFINITY, hi = -INFINITY;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  int64_t tail = 0;
+  if ((reinterpret_cast<uintptr_t>(x) % 16) == 0) {
+    const int64_t n4 = n / 4;
+    const auto* x4 = reinterpret_cast<const float4_t*>(x);
+    int64_t i = t;
+    for (; i + 3 * stride < n4; i += 4 * stride) {
+      float4_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = x4[i + u * stride];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo = fminf(lo, v[u][e]);
+          hi = fmaxf(hi, v[u][e]);
+        }
+    }
+    for (; i < n4; i += stride)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo = fminf(lo, x4[i][e]);
+        hi = fmaxf(hi, x4[i][e]);
+      }
+    tail = n4 * 4;
+  }
+  for (int64_t i = tail + t; i < n; i += stride) {
+    lo = fminf(lo, x[i]);
+    hi = fmaxf(hi, x[i]);
+  }
+  dql_block_range(lo, hi);
   if (threadIdx.x != 0) return;
   if (gridDim.x == 1) {
-    dql_params(lo_s[0], hi_s[0], scale, zero);
+    dql_params(lo, hi, scale, zero);
   } else {
-    part[2 * blockIdx.x] = lo_s[0];
-    part[2 * blockIdx.x + 1] = hi_s[0];
+    part[2 * blockIdx.x] = lo;
+    part[2 * blockIdx.x + 1] = hi;
   }
 }
 
-__global__ __launch_bounds__(64) void k_dql_finalize(const float* __restrict__ part, int parts, float* __restrict__ scale,
-                                                      uint8_t* __restrict__ zero) {
-  if (threadIdx.x != 0) return;
+__global__ __launch_bounds__(256) void k_dql_finalize(const float* __restrict__ part, int parts, float* __restrict__ scale,
+                                                       uint8_t* __restrict__ zero) {
   float lo = INFINITY, hi = -INFINITY;
-  for (int i = 0; i < parts; ++i) {
+  for (int i = threadIdx.x; i < parts; i += blockDim.x) {
     lo = fminf(lo, part[2 * i]);
     hi = fmaxf(hi, part[2 * i + 1]);
   }
-  dql_params(lo, hi, scale, zero);
+  dql_block_range(lo, hi);
+  if (threadIdx.x == 0) dql_params(lo, hi, scale, zero);
 }
 
 // y = saturate(round(x / scale) + zero), four values per thread.
@@ -582,31 +629,19 @@ int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d
   if (batch == 0 || M == 0 || N == 0) return TMH_OK;
   if (!d_a || !d_b || !d_y) return fail(ctx, TMH_ERR_INVALID, "MatMulInteger: NULL pointer");
   if (batch > 65535) return fail(ctx, TMH_ERR_INVALID, "MatMulInteger batch must be below 65536");
+  if ((M + kI8Tile - 1) / kI8Tile > 65535)
+    return fail(ctx, TMH_ERR_INVALID, "MatMulInteger M=%lld exceeds %lld rows", (long long)M, 65535LL * kI8Tile);
   hipStream_t s = pick_stream(ctx, stream);
-  const bool a_sgn = a_dtype == TMH_S8, b_sgn = b_dtype == TMH_S8;
-  const int64_t b_batches = b_batched ? batch : 1;
-  const size_t sums_bytes = static_cast<size_t>(batch * M + b_batches * N) * sizeof(int32_t);
-  auto* sums = K > 0 ? static_cast<int32_t*>(workspace(ctx, sums_bytes, s)) : nullptr;
-  if (!sums) {
-    // K = 0, or no workspace inside a graph capture: the LDS-tiled kernel needs none.
-    const dim3 grid(static_cast<unsigned>((N + kMiTile - 1) / kMiTile), static_cast<unsigned>((M + kMiTile - 1) / kMiTile),
-                    static_cast<unsigned>(batch));
-    k_matmul_integer<<<grid, 256, 0, s>>>(d_a, a_sgn, d_b, b_sgn, d_a_zero, a_zero_count, d_b_zero, b_zero_count, M, K, N,
-                                          b_batched != 0, static_cast<int32_t*>(d_y));
-    return check_launch(ctx, "k_matmul_integer");
-  }
-  const auto* a8 = static_cast<const uint8_t*>(d_a);
-  const auto* b8 = static_cast<const uint8_t*>(d_b);
-  int32_t* rs = sums;
-  int32_t* cs = sums + batch * M;
-  const int64_t lines = batch * M + b_batches * N;
-  k_int8_sums<<<static_cast<unsigned>((lines + 255) / 256), 256, 0, s>>>(a8, a_sgn, b8, b_sgn, batch * M, K, N,
-                                                                        b_batches, rs, cs);
-  TMH_TRY(check_launch(ctx, "k_int8_sums"));
   const dim3 grid(static_cast<unsigned>((N + kI8Tile - 1) / kI8Tile), static_cast<unsigned>((M + kI8Tile - 1) / kI8Tile),
                   static_cast<unsigned>(batch));
-  k_matmul_integer_mfma<<<grid, 256, 0, s>>>(a8, a_sgn, b8, b_sgn, d_a_zero, a_zero_count, d_b_zero, b_zero_count, M,
-                                             K, N, b_batched != 0, rs, cs, static_cast<int32_t*>(d_y));
+  const bool vec = K % 16 == 0 && N % 16 == 0 && reinterpret_cast<uintptr_t>(d_a) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(d_b) % 16 == 0 && (M + kI8Tile) * K + kI8K < (int64_t{1} << 31) &&
+                   (K + kI8K) * N + kI8Tile < (int64_t{1} << 31);
+  auto* kernel = vec ? k_matmul_integer_mfma<true> : k_matmul_integer_mfma<false>;
+  kernel<<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(d_a), a_dtype == TMH_S8, static_cast<const uint8_t*>(d_b),
+                              b_dtype == TMH_S8, static_cast<const uint8_t*>(d_a_zero), a_zero_count,
+                              static_cast<const uint8_t*>(d_b_zero), b_zero_count, M, K, N, b_batched != 0,
+                              static_cast<int32_t*>(d_y));
   return check_launch(ctx, "k_matmul_integer_mfma");
 }
 
@@ -622,9 +657,9 @@ int tmh_dynamic_quantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int6
   const auto* x = static_cast<const float*>(d_x);
   auto* scale = static_cast<float*>(d_scale);
   auto* zero = static_cast<uint8_t*>(d_zero);
-  // One workgroup per 64 Ki values, at most 256; their partial ranges go through the workspace
+  // One workgroup per 16 Ki values, at most 2048; their partial ranges go through the workspace
   // (one workgroup does it all when there is none, inside a graph capture).
-  int parts = static_cast<int>(std::min<int64_t>(256, (n + 65535) / 65536));
+  int parts = static_cast<int>(std::min<int64_t>(2048, (n + 16383) / 16384));
   float* part = nullptr;
   if (parts > 1) {
     part = static_cast<float*>(workspace(ctx, static_cast<size_t>(parts) * 2 * sizeof(float), s));
@@ -633,7 +668,7 @@ int tmh_dynamic_quantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int6
   k_dql_minmax<<<static_cast<unsigned>(std::max(parts, 1)), 256, 0, s>>>(x, n, part, scale, zero);
   TMH_TRY(check_launch(ctx, "k_dql_minmax"));
   if (parts > 1) {
-    k_dql_finalize<<<1, 64, 0, s>>>(part, parts, scale, zero);
+    k_dql_finalize<<<1, 256, 0, s>>>(part, parts, scale, zero);
     TMH_TRY(check_launch(ctx, "k_dql_finalize"));
   }
   if (n == 0) return TMH_OK;
