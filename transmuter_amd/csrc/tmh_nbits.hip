@@ -973,7 +973,7 @@ void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
 // workspace and k_splitk_reduce adds them. During stream capture the workspace cannot grow,
 // so a capture that finds it too small runs without splitting.
 // Tile shape and K split of one prefill GEMM. Each candidate (256 x 128 or 256 x 256 tiles,
-// 1-8 splits of K) is priced as rounds of workgroups over the CUs times the work of one, at the
+// 1-16 splits of K) is priced as rounds of workgroups over the CUs times the work of one, at the
 // per-CU rates the two tile shapes sustain on MI355X with every CU busy (2.8 and 3.9 dense f16
 // TFLOP/s per CU, measured on the SmolLM3-3B and 2048x4096x8192 shapes), plus the f32 partial
 // sums a split writes and the reduction reads back.
@@ -989,7 +989,7 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
   for (int wn : {2, 4}) {
     const int64_t tiles = mblocks * ((ntiles + 4 * wn - 1) / (4 * wn));
     const double chunk_s = 2.0 * kGemmBM * 64.0 * wn * cw / (wn == 4 ? 3.9e12 : 2.8e12);
-    for (int64_t splits = 1; splits <= 8; ++splits) {
+    for (int64_t splits = 1; splits <= 16; ++splits) {
       if (splits > 1 && 2 * splits > nchunks) break;
       const int64_t cps = (nchunks + splits - 1) / splits;
       const int64_t used = (nchunks + cps - 1) / cps;
