@@ -24,6 +24,11 @@ MI_CASES = [
     (3, 40, 96, 48, "s8", "u8", "row", "col", True),
     (2, 17, 75, 9, "u8", "u8", "scalar", "col", False),      # K and N off every vector width
     (1, 300, 512, 520, "u8", "s8", "scalar", None, False),
+    # K and N multiples of 16 (16-byte buffer loads): ragged M and N tiles, a last k-step of 16
+    (1, 200, 272, 208, "u8", "u8", "row", "col", False),
+    (2, 129, 1040, 400, "s8", "u8", "scalar", "col", True),
+    (1, 513, 2048, 384, "u8", "s8", "scalar", None, False),
+    (1, 256, 512, 1024, "u8", "u8", "scalar", "col", False),  # 16 tiles: the XCD tile order
 ]
 
 

@@ -215,6 +215,65 @@ __global__ __launch_bounds__(256) void k_dequantize_linear(
   store_as<OUT>(y, e, prod);
 }
 
+// The same values for tensors of fewer than 2^31 elements: four consecutive elements per thread,
+// one 32-bit split of the first index into (outer, axis, inner) and a step for the rest, and an
+// 8- or 16-byte store when y is aligned for it.
+template <int OUT>
+__global__ __launch_bounds__(256) void k_dequantize_linear4(
+    const void* __restrict__ x, int x_dt, bool x_int, uint32_t dim, uint32_t inner,
+    const void* __restrict__ scale, int scale_dt, const void* __restrict__ zero, int zero_dt,
+    int mode, uint32_t bs, uint32_t nb, void* __restrict__ y, uint32_t total, bool y_vec) {
+  const uint32_t e0 = (blockIdx.x * blockDim.x + threadIdx.x) * 4u;
+  if (e0 >= total) return;
+  const uint32_t per_outer = dim * inner;
+  uint32_t o = e0 / per_outer;
+  const uint32_t rem = e0 - o * per_outer;
+  uint32_t d = rem / inner;
+  uint32_t in = rem - d * inner;
+  float out[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t e = e0 + j;
+    if (e < total) {
+      uint32_t p = 0;
+      if (mode == TMH_QPARAM_AXIS) p = d;
+      else if (mode == TMH_QPARAM_BLOCKED) p = (o * nb + d / bs) * inner + in;
+      float v;
+      if (x_int) {
+        uint32_t shifted = static_cast<uint32_t>(load_int_rt(x, x_dt, e));
+        if (zero) shifted -= static_cast<uint32_t>(load_int_rt(zero, zero_dt, p));
+        v = static_cast<float>(static_cast<int32_t>(shifted));
+      } else {
+        v = load_float_rt(x, x_dt, e);
+        if (zero) v = v - load_float_rt(zero, zero_dt, p);
+      }
+      out[j] = v * load_float_rt(scale, scale_dt, p);
+    }
+    if (++in == inner) {
+      in = 0;
+      if (++d == dim) {
+        d = 0;
+        ++o;
+      }
+    }
+  }
+  if (y_vec && e0 + 4 <= total) {
+    if constexpr (OUT == DT_F32) {
+      *reinterpret_cast<float4_t*>(static_cast<float*>(y) + e0) = float4_t{out[0], out[1], out[2], out[3]};
+    } else {
+      uint16_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = OUT == DT_F16 ? f32_to_f16_bits(out[j]) : f32_to_bf16_bits(out[j]);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + e0) =
+          make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (e0 + j < total) store_as<OUT>(y, e0 + j, out[j]);
+  }
+}
+
 // ------------------------------------------------------------------ MatMulInteger on int8 MFMA
 
 // y[bt, m, n] = sum_k (a - a_zero[m]) (b - b_zero[n]), wrapping mod 2^32. Each f32 chunk sum of
@@ -605,6 +664,19 @@ int tmh_dequantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t ou
   if (!d_x || !d_scale || !d_y) return fail(ctx, TMH_ERR_INVALID, "DequantizeLinear: NULL pointer");
   hipStream_t s = pick_stream(ctx, stream);
   const int64_t nb = mode == TMH_QPARAM_BLOCKED ? (dim + block_size - 1) / block_size : 1;
+  if (total < (int64_t{1} << 31) - 4) {
+    const int out_bytes = scale_dtype == TMH_F16 || scale_dtype == TMH_BF16 ? 2 : 4;
+    const bool y_vec = reinterpret_cast<uintptr_t>(d_y) % (4 * out_bytes) == 0;
+    const dim3 grid(static_cast<unsigned>((total + 1023) / 1024));
+    const auto d32 = static_cast<uint32_t>(dim), i32 = static_cast<uint32_t>(inner), t32 = static_cast<uint32_t>(total);
+    const auto bs32 = static_cast<uint32_t>(mode == TMH_QPARAM_BLOCKED ? block_size : 1), nb32 = static_cast<uint32_t>(nb);
+    switch (scale_dtype) {
+      case TMH_F16: k_dequantize_linear4<DT_F16><<<grid, 256, 0, s>>>(d_x, x_dtype, x_int, d32, i32, d_scale, scale_dtype, d_zero, zero_dtype, mode, bs32, nb32, d_y, t32, y_vec); break;
+      case TMH_BF16: k_dequantize_linear4<DT_BF16><<<grid, 256, 0, s>>>(d_x, x_dtype, x_int, d32, i32, d_scale, scale_dtype, d_zero, zero_dtype, mode, bs32, nb32, d_y, t32, y_vec); break;
+      default: k_dequantize_linear4<DT_F32><<<grid, 256, 0, s>>>(d_x, x_dtype, x_int, d32, i32, d_scale, scale_dtype, d_zero, zero_dtype, mode, bs32, nb32, d_y, t32, y_vec);
+    }
+    return check_launch(ctx, "k_dequantize_linear4");
+  }
   const dim3 grid(static_cast<unsigned>((total + 255) / 256));
   switch (scale_dtype) {
     case TMH_F16: k_dequantize_linear<DT_F16><<<grid, 256, 0, s>>>(d_x, x_dtype, x_int, dim, inner, d_scale, scale_dtype, d_zero, zero_dtype, mode, block_size, nb, d_y, total); break;

@@ -75,10 +75,13 @@ class Context:
         return DeviceTensor(self, self.alloc(nbytes), shape, dtype, nbytes)
 
     def put(self, array: np.ndarray, dtype: str | None = None) -> "DeviceTensor":
-        """Copies a host array to the device. `dtype` names bf16 for uint16 bit patterns."""
+        """Copies a host array to the device. `dtype` names bf16 for uint16 bit patterns. The
+        tensor keeps the array's shape, rank 0 included (np.ascontiguousarray alone makes a 0-d
+        array 1-d)."""
+        shape = np.shape(array)
         host = np.ascontiguousarray(array)
         dtype = dtype or nx_type(host)
-        t = self.empty(host.shape, dtype)
+        t = self.empty(shape, dtype)
         if t.nbytes:
             self.check(lib().tmh_upload(self.handle, t.ptr, host.ctypes.data_as(ctypes.c_void_p), t.nbytes))
         return t
