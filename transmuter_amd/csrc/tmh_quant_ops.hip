@@ -289,35 +289,38 @@ constexpr int kI8Tile = 128;  // output rows and columns per workgroup
 constexpr int kI8K = 128;     // k per step: two MFMAs deep
 
 // LDS tiles hold 128 rows (A rows, or B columns) of 128 k-bytes, no padding; the 16-byte chunk
-// c of row x sits at chunk c ^ ((x & 7) ^ ((x >> 4) & 7)). Eight consecutive rows reading one
-// chunk (an MFMA fragment read) then hit eight different chunks, and so do the rows 16 apart
-// that one wavefront's 4-byte B writes cover.
+// c of row x sits at chunk c ^ ((x & 7) ^ ((x >> 3) & 7)). Eight consecutive rows reading one
+// chunk (an MFMA fragment read) then hit eight different chunks, and the B columns one
+// wavefront's 4-byte writes cover (8 apart) spread over them too.
 __device__ __forceinline__ int i8_lds_offset(int x, int chunk) {
-  return x * kI8K + ((chunk ^ ((x & 7) ^ ((x >> 4) & 7))) << 4);
+  return x * kI8K + ((chunk ^ ((x & 7) ^ ((x >> 3) & 7))) << 4);
 }
 
 __device__ __forceinline__ uint32_t dot4_ones(uint32_t w, uint32_t acc) {
   return static_cast<uint32_t>(__builtin_amdgcn_sdot4(static_cast<int>(w), 0x01010101, static_cast<int>(acc), false));
 }
 
-// 128 x 128 outputs per workgroup of four wavefronts (64 x 64 each, 4 x 4 MFMA tiles). Each
-// k-step's A rows (16 bytes per load) and B rows (4 k-rows x 16 columns per thread) are read into
-// registers while the previous step's MFMAs run, then stored to LDS as s8: A as is, B transposed
-// to k-contiguous columns through 4 x 4 byte blocks (v_perm). Zeros outside the matrices.
+typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+
+// 128 x 128 outputs per workgroup of eight wavefronts, two per SIMD (64 x 32 each, 4 x 2 MFMA
+// tiles), so one wavefront's stalls are covered by the other's work. Each k-step's A rows
+// (16 bytes per load) and B rows (4 k-rows x 8 columns per thread) are read into registers while
+// the previous step's MFMAs run, then stored to LDS as s8: A as is, B transposed to k-contiguous
+// columns through 4 x 4 byte blocks (v_perm). Zeros outside the matrices.
 // VEC: K and N are multiples of 16, both matrices 16-byte aligned, (M + 128) K and (K + 128) N
-// below 2^31; every load is then one unconditional 16-byte buffer load (a branch per load makes
-// the compiler wait for each load before the next).
+// below 2^31; every load is then one unconditional buffer load at a 32-bit offset formed once
+// and advanced per step (a branch per load makes the compiler wait for each load in turn).
 template <bool VEC>
-__global__ __launch_bounds__(256) void k_matmul_integer_mfma(
+__global__ __launch_bounds__(512) void k_matmul_integer_mfma(
     const uint8_t* __restrict__ a, bool a_signed, const uint8_t* __restrict__ b, bool b_signed,
     const uint8_t* __restrict__ a_zero, int64_t a_zero_count, const uint8_t* __restrict__ b_zero,
     int64_t b_zero_count, int64_t M, int64_t K, int64_t N, bool b_batched, int32_t* __restrict__ y) {
   __shared__ __align__(16) uint8_t sA[kI8Tile * kI8K];
   __shared__ __align__(16) uint8_t sB[kI8Tile * kI8K];
   __shared__ uint32_t sRs[kI8Tile];
-  __shared__ uint32_t sCs[4][kI8Tile];
+  __shared__ uint32_t sCs[8][kI8Tile];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   const int r = lane & 15, g = lane >> 4;
   const int64_t bt = blockIdx.z;
   // Workgroups go to the eight XCDs round-robin by linear id. When the tile count is a multiple
@@ -333,28 +336,37 @@ __global__ __launch_bounds__(256) void k_matmul_integer_mfma(
   const uint8_t* a8 = a + bt * M * K;
   const uint8_t* b8 = b + (b_batched ? bt * K * N : 0);
   const uint32_t aflip = a_signed ? 0u : 0x80808080u, bflip = b_signed ? 0u : 0x80808080u;
-  // This thread's share of a k-step: A row (tid >> 3) + 32h, chunk tid & 7 (h = 0..3); B k-rows
-  // 4 * (tid >> 3) + i, columns 16 * (tid & 7) + j.
+  // This thread's share of a k-step: A rows (tid >> 3) + 64h, chunk tid & 7 (h = 0, 1); B k-rows
+  // 4 * (tid >> 4) + i (i = 0..3), columns 8 * (tid & 15) + j (j = 0..7).
   const int a_row = tid >> 3, a_chunk = tid & 7;
-  const int b_kq = tid >> 3, b_nq = tid & 7;
+  const int b_kq = tid >> 4, b_nq = tid & 15;
   // va/vb hold the loaded bytes. For VEC the loads are unconditional, and amask (bytes to keep)
   // and bmask (flip to apply) are applied when the bytes go to LDS, so the loads of the next
-  // step are not waited for before this step's MFMAs. The buffer resources span this batch's
-  // matrices; every offset formed stays below 2^31 (checked on the host).
-  uint4_t va[4], vb[4];
-  uint32_t amask[4] = {0u, 0u, 0u, 0u}, bmask[4] = {0u, 0u, 0u, 0u};
+  // step are not waited for before this step's MFMAs. Rows of A past M and k-rows of B past K
+  // lie outside the buffer ranges and read zeros; A bytes past K belong to the next row and are
+  // masked; B columns past N reach only outputs that are never stored.
+  uint4_t va[2];
+  uint2_t vb[4];
+  uint32_t amask[2] = {0u, 0u}, bmask[4] = {0u, 0u, 0u, 0u};
   const auto a_rsrc = buffer_rsrc(a8, VEC ? static_cast<uint32_t>(M * K) : 0u);
   const auto b_rsrc = buffer_rsrc(b8, VEC ? static_cast<uint32_t>(K * N) : 0u);
-  auto load = [&](int64_t k0) {
+  uint32_t a_off[2] = {0u, 0u}, b_off[4] = {0u, 0u, 0u, 0u};
+  if constexpr (VEC) {
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int64_t gm = m0 + a_row + 32 * h, gk = k0 + 16 * a_chunk;
+    for (int h = 0; h < 2; ++h) a_off[h] = static_cast<uint32_t>((m0 + a_row + 64 * h) * K + 16 * a_chunk);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b_off[i] = static_cast<uint32_t>((4 * b_kq + i) * N + n0 + 8 * b_nq);
+  }
+  const uint32_t b_step = static_cast<uint32_t>(kI8K * N);
+  auto load = [&](int64_t k0, uint32_t step) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t gk = k0 + 16 * a_chunk;
       if constexpr (VEC) {
-        // Rows past M are out of the buffer's range (zeros); bytes past K belong to the next
-        // row and are zeroed when staged (amask); only rows < M reach an output.
-        va[h] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, static_cast<uint32_t>(gm * K + gk), 0, 0);
+        va[h] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off[h] + step * kI8K, 0, 0);
         amask[h] = gk < K ? 0xFFFFFFFFu : 0u;
       } else {
+        const int64_t gm = m0 + a_row + 64 * h;
         uint4_t v = {0u, 0u, 0u, 0u};
         if (gm < M && gk < K)
           for (int e = 0; e < 16; ++e)
@@ -364,91 +376,98 @@ __global__ __launch_bounds__(256) void k_matmul_integer_mfma(
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t gk = k0 + 4 * b_kq + i, gn = n0 + 16 * b_nq;
+      const int64_t gk = k0 + 4 * b_kq + i;
       if constexpr (VEC) {
-        // k-rows past K are out of range (zeros, left unflipped); columns past N read the next
-        // row's bytes, which reach only columns that are never stored.
-        vb[i] = __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, static_cast<uint32_t>(gk * N + gn), 0, 0);
+        vb[i] = __builtin_amdgcn_raw_buffer_load_b64(b_rsrc, b_off[i] + step * b_step, 0, 0);
         bmask[i] = gk < K ? bflip : 0u;
       } else {
-        uint4_t v = {0u, 0u, 0u, 0u};
+        const int64_t gn = n0 + 8 * b_nq;
+        uint2_t v = {0u, 0u};
         if (gk < K && gn < N)
-          for (int e = 0; e < 16; ++e)
+          for (int e = 0; e < 8; ++e)
             if (gn + e < N) v[e >> 2] |= static_cast<uint32_t>(b8[gk * N + gn + e] ^ (bflip & 0xFFu)) << (8 * (e & 3));
         vb[i] = v;
       }
     }
   };
-  uint32_t rsum[4] = {0u, 0u, 0u, 0u};
-  uint32_t csum[16];
+  uint32_t rsum[2] = {0u, 0u};
+  uint32_t csum[8];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) csum[j] = 0u;
-  int4_t acc[4][4];
+  for (int j = 0; j < 8; ++j) csum[j] = 0u;
+  int4_t acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = int4_t{0, 0, 0, 0};
-  if (K > 0) load(0);
-  for (int64_t k0 = 0; k0 < K; k0 += kI8K) {
+    for (int j = 0; j < 2; ++j) acc[i][j] = int4_t{0, 0, 0, 0};
+  if (K > 0) load(0, 0u);
+  uint32_t step = 0;
+  for (int64_t k0 = 0; k0 < K; k0 += kI8K, ++step) {
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int row = a_row + 32 * h;
-      if constexpr (VEC) va[h] = (va[h] ^ aflip) & amask[h];
-      *reinterpret_cast<uint4_t*>(sA + i8_lds_offset(row, a_chunk)) = va[h];
+    for (int h = 0; h < 2; ++h) {
+      uint4_t v = va[h];
+      if constexpr (VEC) v = (v ^ aflip) & amask[h];
+      *reinterpret_cast<uint4_t*>(sA + i8_lds_offset(a_row + 64 * h, a_chunk)) = v;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) rsum[h] = dot4_ones(va[h][q], rsum[h]);
+      for (int q = 0; q < 4; ++q) rsum[h] = dot4_ones(v[q], rsum[h]);
     }
-    // Column c of the 4 x 16 block is bytes c of vb[0..3]; word c >> 2 of each, byte c & 3.
+    // Column c of the 4 x 8 block is bytes c of vb[0..3]: word c >> 2 of each, byte c & 3.
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t x0 = vb[0][q] ^ bmask[0], x1 = vb[1][q] ^ bmask[1], x2 = vb[2][q] ^ bmask[2], x3 = vb[3][q] ^ bmask[3];
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t x0 = vb[0][q] ^ bmask[0], x1 = vb[1][q] ^ bmask[1];
+      const uint32_t x2 = vb[2][q] ^ bmask[2], x3 = vb[3][q] ^ bmask[3];
       const uint32_t lo01 = __builtin_amdgcn_perm(x1, x0, 0x05010400u), hi01 = __builtin_amdgcn_perm(x1, x0, 0x07030602u);
       const uint32_t lo23 = __builtin_amdgcn_perm(x3, x2, 0x05010400u), hi23 = __builtin_amdgcn_perm(x3, x2, 0x07030602u);
       const uint32_t col[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
                                __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int n = 16 * b_nq + 4 * q + e;
+        const int n = 8 * b_nq + 4 * q + e;
         *reinterpret_cast<uint32_t*>(sB + i8_lds_offset(n, b_kq >> 2) + 4 * (b_kq & 3)) = col[e];
         csum[4 * q + e] = dot4_ones(col[e], csum[4 * q + e]);
       }
     }
     __syncthreads();
-    if (k0 + kI8K < K) load(k0 + kI8K);
+    if (k0 + kI8K < K) load(k0 + kI8K, step + 1);
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      int4_t af[4], bf[4];
+      int4_t af[4], bf[2];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
         af[mt] = *reinterpret_cast<const int4_t*>(sA + i8_lds_offset(wm * 64 + mt * 16 + r, 4 * half + g));
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        bf[nt] = *reinterpret_cast<const int4_t*>(sB + i8_lds_offset(wn * 64 + nt * 16 + r, 4 * half + g));
+      for (int nt = 0; nt < 2; ++nt)
+        bf[nt] = *reinterpret_cast<const int4_t*>(sB + i8_lds_offset(wn * 32 + nt * 16 + r, 4 * half + g));
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)  // B first: a lane ends with 4 consecutive columns of one row
+        for (int nt = 0; nt < 2; ++nt)  // B first: a lane ends with 4 consecutive columns of one row
           acc[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[nt], af[mt], acc[mt][nt], 0, 0, 0);
     }
     __syncthreads();
   }
-  // rs: the 8 lanes of a row (consecutive) hold its 8 chunks' sums. cs: the 8 lanes of a
-  // wavefront with one tid & 7 hold 8 of the 32 k-quads' sums, the four wavefronts the rest.
+  // rs: the 8 lanes of a row (consecutive) hold its 8 chunks' sums. cs: the 4 lanes of a
+  // wavefront with one tid & 15 hold 4 of the 32 k-quads' sums, the eight wavefronts the rest.
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
+  for (int h = 0; h < 2; ++h) {
     uint32_t v = rsum[h];
     v += __shfl_xor(v, 1);
     v += __shfl_xor(v, 2);
     v += __shfl_xor(v, 4);
-    if (a_chunk == 0) sRs[a_row + 32 * h] = v;
+    if (a_chunk == 0) sRs[a_row + 64 * h] = v;
   }
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < 8; ++j) {
     uint32_t v = csum[j];
-    v += __shfl_xor(v, 8);
     v += __shfl_xor(v, 16);
     v += __shfl_xor(v, 32);
-    if (lane < 8) sCs[wave][16 * b_nq + j] = v;
+    if (lane < 16) sCs[wave][8 * b_nq + j] = v;
+  }
+  __syncthreads();
+  if (tid < kI8Tile) {
+    uint32_t v = sCs[0][tid];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) v += sCs[w][tid];
+    sCs[0][tid] = v;
   }
   __syncthreads();
   const uint32_t oa = a_signed ? 0u : 128u, ob = b_signed ? 0u : 128u;
@@ -468,16 +487,15 @@ __global__ __launch_bounds__(256) void k_matmul_integer_mfma(
     const uint32_t rsm = sRs[ml];
     int32_t* yrow = y + (bt * M + m) * N;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int nl = wn * 64 + nt * 16 + 4 * g;
+    for (int nt = 0; nt < 2; ++nt) {
+      const int nl = wn * 32 + nt * 16 + 4 * g;
       const int64_t n = n0 + nl;
       if (n >= N) continue;
       int4_t out;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t cb = ob - zero_of(b_zero, b_zero_count, n + e < N ? n + e : n, b_signed);
-        const uint32_t csn = sCs[0][nl + e] + sCs[1][nl + e] + sCs[2][nl + e] + sCs[3][nl + e];
-        out[e] = static_cast<int32_t>(static_cast<uint32_t>(acc[mt][nt][e]) + cb * rsm + ca * csn + kk * ca * cb);
+        out[e] = static_cast<int32_t>(static_cast<uint32_t>(acc[mt][nt][e]) + cb * rsm + ca * sCs[0][nl + e] + kk * ca * cb);
       }
       if (y_vec) {
         *reinterpret_cast<int4_t*>(yrow + n) = out;
@@ -710,7 +728,7 @@ int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d
                    reinterpret_cast<uintptr_t>(d_b) % 16 == 0 && (M + kI8Tile) * K + kI8K < (int64_t{1} << 31) &&
                    (K + kI8K) * N + kI8Tile < (int64_t{1} << 31);
   auto* kernel = vec ? k_matmul_integer_mfma<true> : k_matmul_integer_mfma<false>;
-  kernel<<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(d_a), a_dtype == TMH_S8, static_cast<const uint8_t*>(d_b),
+  kernel<<<grid, 512, 0, s>>>(static_cast<const uint8_t*>(d_a), a_dtype == TMH_S8, static_cast<const uint8_t*>(d_b),
                               b_dtype == TMH_S8, static_cast<const uint8_t*>(d_a_zero), a_zero_count,
                               static_cast<const uint8_t*>(d_b_zero), b_zero_count, M, K, N, b_batched != 0,
                               static_cast<int32_t*>(d_y));
