@@ -180,3 +180,37 @@ def test_y_type_must_follow_the_reference(ctx):
     y_d = ctx.empty((1, 16), "f32")
     with pytest.raises(TmhArgumentError, match="Y must be f16"):
         ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, a_d.ptr, 10, 1, 64, None, 0, y_d.ptr, F32, 16, None))
+
+
+# Every prefill tile shape (BM x 64*WN: 256x128, 256x256, 128x128, 128x256), with and without K
+# splits, forced through TMH_GEMM_PLAN, over ragged M, N and K (a partial last k-block) and a bias.
+PLAN_CASES = [
+    # bits, block, zp, K, N, M list, bias
+    (4, 32, "packed", 1000, 1000, [200, 300], "f16"),
+    (4, 128, "packed", 2048, 520, [129], None),
+    (8, 64, "none", 768, 520, [130, 257], "f32"),
+]
+PLANS = [(256, 2, 1), (256, 4, 1), (128, 2, 1), (128, 4, 1), (256, 2, 3), (128, 2, 2), (128, 4, 4)]
+
+
+@pytest.mark.parametrize("plan", PLANS, ids=lambda p: "bm{}_wn{}_s{}".format(*p))
+@pytest.mark.parametrize("case", PLAN_CASES, ids=lambda c: "b{}_bs{}_{}_K{}_N{}".format(*c[:5]))
+def test_matmul_every_gemm_plan(ctx, monkeypatch, case, plan):
+    bits, bs, zp, k, n, ms, bias_dt = case
+    monkeypatch.setenv("TMH_GEMM_PLAN", ",".join(map(str, plan)))
+    rng = np.random.default_rng(zlib.crc32(repr(case[:5]).encode()))
+    b, s32, z = nbits_weight(rng, k, n, bits, bs, zp=zp, scale_dtype=np.float32)
+    scales = s32.astype(np.float16)
+    w = PackedWeight.upload(ctx, b, scales, z, k=k, n=n, bits=bits, block_size=bs, weight_dtype="f16",
+                            scales_dtype="f16")
+    bias = host_float(rng.standard_normal(n).astype(np.float32), bias_dt) if bias_dt else None
+    for m in ms:
+        print(f"matmul plan {plan} {case} M={m}", flush=True)
+        a = rng.standard_normal((m, k)).astype(np.float16)
+        y = matmul_nbits(ctx.put(a), w, ctx.put(bias, bias_dt) if bias is not None else None)
+        got = as_f64(y.numpy(), y.dtype)
+        ref = o.matmul_nbits(a, b, scales.astype(np.float32), z, bias, k=k, n=n, bits=bits, block_size=bs,
+                             weight_dtype="f16")
+        err = rel_err(got, np.asarray(ref, np.float64))
+        assert err <= TOL["f16"], f"M={m}: relative error {err}"
+    w.free()

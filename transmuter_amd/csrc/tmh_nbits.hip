@@ -16,6 +16,7 @@
 //   k_matmul_general  any float types and float zero points, f32 FMA on the vector ALUs
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <vector>
 
 #include "tmh_device.h"
@@ -445,23 +446,25 @@ __global__ __launch_bounds__(256) void k_gemm_f16(
   }
 }
 
-// Prefill GEMM: 256 x 64*WN output tile per workgroup of 2*WN wavefronts (WN = 2: 256 x 128,
-// one wavefront per SIMD; WN = 4: 256 x 256, two per SIMD), k-blocks of one chunk (CW weights).
-//  - A: the k-block's 256 rows x CW f16 go global -> LDS by buffer_load ... lds (no VGPRs),
+// Prefill GEMM: BM x 64*WN output tile per workgroup of 2*WN wavefronts (BM = 256 or 128; WN = 2:
+// one wavefront per SIMD, WN = 4: two per SIMD), k-blocks of one chunk (CW weights).
+//  - A: the k-block's BM rows x CW f16 go global -> LDS by buffer_load ... lds (no VGPRs),
 //    double buffered, rows of CW*2 bytes whose 16-byte pieces are XOR-swizzled by row so the
 //    MFMA fragment reads of 16 rows hit distinct banks. Rows past M lie outside the buffer
 //    range and read zeros (their outputs are never stored). A partial last k-block goes through
 //    registers and is zeroed past K.
-//  - B: with WN = 2, wavefront (wm, wn) computes rows 128*wm.. and columns 64*wn.. (four
-//    16-column weight tiles, each dequantized fragment feeding eight MFMAs); with WN = 4, each
-//    wavefront computes all 256 rows of two tiles (each fragment feeding sixteen). The tiles'
-//    weights, scales and zero points are loaded one k-block ahead and dequantized in registers
-//    (exact f16) for v_mfma_f32_16x16x32_f16.
-constexpr int kGemmBM = 256;
+//  - B: with BM = 256 and WN = 2, wavefront (wm, wn) computes rows 128*wm.. and columns 64*wn..
+//    (four 16-column weight tiles, each dequantized fragment feeding eight MFMAs); otherwise
+//    ("tall"), each wavefront computes all BM rows of two tiles (each fragment feeding BM/16).
+//    The tiles' weights, scales and zero points are loaded one k-block ahead and dequantized in
+//    registers (exact f16) for v_mfma_f32_16x16x32_f16.
+// BM = 128 gives shapes with few 256-row blocks (M = 2048, N = 2048) enough workgroups without
+// splitting K, and its 64 KiB of LDS lets two workgroups share a CU.
+constexpr int kGemmBM = 256;  // largest tile height: bounds the A rows a launch may touch
 
-template <int BITS>
+template <int BITS, int BM>
 constexpr size_t gemm_lds_bytes() {
-  return 2 * static_cast<size_t>(kGemmBM) * (512 / BITS) * 2;
+  return 2 * static_cast<size_t>(BM) * (512 / BITS) * 2;
 }
 
 // 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (buffer_load_dwordx4
@@ -481,7 +484,7 @@ __device__ __forceinline__ int a_slot(int row, int piece) {
   return BITS == 8 ? (piece ^ ((row >> 1) & 7)) : (piece ^ (row & 15));
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int WN>
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM>
 __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
@@ -494,14 +497,15 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   constexpr int ROWB = CW * 2;           // bytes per LDS row
   constexpr int PPR = CW / 8;            // 16-byte pieces per row
   constexpr int RPI = 64 / PPR;          // rows per wavefront load instruction
-  constexpr int RW = kGemmBM / (2 * WN); // A rows each wavefront brings into LDS
+  constexpr int RW = BM / (2 * WN);      // A rows each wavefront brings into LDS
   constexpr int LOADS = RW / RPI;        // load instructions per wavefront per k-block
   constexpr int NJ = SPLIT ? STEPS : 1;  // parameter entries per tile per k-block
-  // WN == 4 (eight wavefronts, two per SIMD): each wavefront takes all 256 rows and two weight
-  // tiles, so every dequantized fragment feeds 16 MFMAs. WN == 2 (four wavefronts): 128 rows and
-  // four tiles per wavefront.
-  constexpr bool TALL = WN == 4;
-  constexpr int MTW = TALL ? 16 : 8;
+  // Tall (WN == 4, eight wavefronts, two per SIMD; or BM == 128): each wavefront takes all BM
+  // rows and two weight tiles, so every dequantized fragment feeds BM/16 MFMAs. BM == 256 with
+  // WN == 2 (four wavefronts): 128 rows and four tiles per wavefront.
+  static_assert(BM == 128 || BM == 256, "tile height");
+  constexpr bool TALL = WN == 4 || BM == 128;
+  constexpr int MTW = TALL ? BM / 16 : 8;
   constexpr int NTW = TALL ? 2 : 4;
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x;
@@ -517,7 +521,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   const unsigned tile = blockIdx.x % tiles;
   const int mb = static_cast<int>(tile % static_cast<unsigned>(mblocks));
   const int nb = static_cast<int>(tile / static_cast<unsigned>(mblocks));
-  const int m0 = mb * kGemmBM;
+  const int m0 = mb * BM;
   const int t0 = TALL ? nb * 4 * WN + wave * NTW : (nb * WN + wn) * 4;
   const uint32_t nch = static_cast<uint32_t>(nchunks);
   const uint32_t kb0 = static_cast<uint32_t>(split) * static_cast<uint32_t>(chunks_per_split);
@@ -540,7 +544,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     return a_row0 + static_cast<uint32_t>(s2) * a_rstep + piece * 16;
   };
   auto load_a = [&](uint32_t kb, int buf, int s_lo = 0, int s_hi = 1 << 30) {
-    uint8_t* base = lds + buf * (kGemmBM * ROWB) + wave * RW * ROWB;
+    uint8_t* base = lds + buf * (BM * ROWB) + wave * RW * ROWB;
     if (static_cast<int64_t>(kb + 1) * CW <= K) {
 #pragma unroll
       for (int s2 = 0; s2 < LOADS; ++s2)
@@ -616,8 +620,8 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   // MFMAs, the same registers take fragment mt of step i+1 from LDS; step i+1's weights are
   // dequantized (into the other of two register sets) while step i's MFMAs run.
   auto compute = [&](int buf, const BStage& st, bool more, uint32_t kbn, BStage& nst) {
-    const uint8_t* abase = lds + buf * (kGemmBM * ROWB) + (wm * 128 + r) * ROWB;
-    if constexpr (WN == 4) {
+    const uint8_t* abase = lds + buf * (BM * ROWB) + (wm * 128 + r) * ROWB;
+    if constexpr (TALL) {
       // Two wavefronts per SIMD: each keeps few registers live and relies on the other to fill
       // its waits; one set of weight fragments per step, A fragments read one ahead of use.
 #pragma unroll
@@ -972,23 +976,32 @@ void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
 // Split K when the output tiles cannot fill the GPU: partial sums go to the context's
 // workspace and k_splitk_reduce adds them. During stream capture the workspace cannot grow,
 // so a capture that finds it too small runs without splitting.
-// Tile shape and K split of one prefill GEMM. Each candidate (256 x 128 or 256 x 256 tiles,
-// 1-16 splits of K) is priced as rounds of workgroups over the CUs times the work of one, at the
-// per-CU rates the two tile shapes sustain on MI355X with every CU busy (2.8 and 3.9 dense f16
-// TFLOP/s per CU, measured on the SmolLM3-3B and 2048x4096x8192 shapes), plus the f32 partial
-// sums a split writes and the reduction reads back.
+// Tile shape and K split of one prefill GEMM. Each candidate (BM x 64*WN tiles, 1-16 splits of
+// K) is priced as rounds of workgroups over the CUs times the work of one, at the per-CU rate
+// the tile shape sustains on MI355X with every CU busy (dense f16 TFLOP/s per CU, measured on the
+// SmolLM3-3B and 2048x4096x8192 shapes; with these rates the plan chosen for each SmolLM3-3B
+// projection at M = 256 and 2048 was the fastest of the candidates timed, or within 6% of it),
+// plus the f32 partial sums a split writes and the reduction reads back.
+// TMH_GEMM_PLAN="bm,wn,splits" in the environment forces a plan (tests use it to reach every
+// tile shape; an invalid value is ignored).
+struct GemmShape {
+  int bm, wn;
+  double rate;  // dense f16 FLOP/s per CU
+};
+constexpr GemmShape kGemmShapes[] = {{256, 2, 2.8e12}, {256, 4, 3.9e12}, {128, 2, 2.4e12}, {128, 4, 3.3e12}};
+
 struct GemmPlan {
-  int wn, splits, cps;
+  int bm, wn, splits, cps;
 };
 
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bits, int cus) {
   const double cw = 512.0 / bits;
-  const int64_t mblocks = (M + kGemmBM - 1) / kGemmBM;
-  GemmPlan best{2, 1, static_cast<int>(nchunks)};
+  GemmPlan best{256, 2, 1, static_cast<int>(nchunks)};
   double best_t = 1e30;
-  for (int wn : {2, 4}) {
-    const int64_t tiles = mblocks * ((ntiles + 4 * wn - 1) / (4 * wn));
-    const double chunk_s = 2.0 * kGemmBM * 64.0 * wn * cw / (wn == 4 ? 3.9e12 : 2.8e12);
+  for (const GemmShape& sh : kGemmShapes) {
+    const int64_t mblocks = (M + sh.bm - 1) / sh.bm;
+    const int64_t tiles = mblocks * ((ntiles + 4 * sh.wn - 1) / (4 * sh.wn));
+    const double chunk_s = 2.0 * sh.bm * 64.0 * sh.wn * cw / sh.rate;
     for (int64_t splits = 1; splits <= 16; ++splits) {
       if (splits > 1 && 2 * splits > nchunks) break;
       const int64_t cps = (nchunks + splits - 1) / splits;
@@ -1002,16 +1015,24 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
       if (splits > 1) t += 2.0 * splits * M * N * 4 / 5e12;
       if (t < best_t) {
         best_t = t;
-        best = GemmPlan{wn, static_cast<int>(splits), static_cast<int>(cps)};
+        best = GemmPlan{sh.bm, sh.wn, static_cast<int>(splits), static_cast<int>(cps)};
       }
+    }
+  }
+  if (const char* f = getenv("TMH_GEMM_PLAN")) {
+    int bm = 0, wn = 0, sp = 0;
+    if (sscanf(f, "%d,%d,%d", &bm, &wn, &sp) == 3 && (bm == 128 || bm == 256) && (wn == 2 || wn == 4) && sp >= 1 &&
+        sp <= nchunks) {
+      const int cps = static_cast<int>((nchunks + sp - 1) / sp);
+      best = GemmPlan{bm, wn, static_cast<int>((nchunks + cps - 1) / cps), cps};
     }
   }
   return best;
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int WN>
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM>
 void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s, int splits, int cps) {
-  const int mblocks = static_cast<int>((a.M + kGemmBM - 1) / kGemmBM);
+  const int mblocks = static_cast<int>((a.M + BM - 1) / BM);
   const int nblocks = static_cast<int>((w->ntiles + 4 * WN - 1) / (4 * WN));
   const int64_t tiles = static_cast<int64_t>(mblocks) * nblocks;
   float* ws = nullptr;
@@ -1024,10 +1045,10 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
   }
   const dim3 grid(static_cast<unsigned>(tiles * splits));
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN>), hipFuncAttributeMaxDynamicSharedMemorySize,
-      static_cast<int>(gemm_lds_bytes<BITS>()));
+      reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(gemm_lds_bytes<BITS, BM>()));
   (void)attr;
-  k_gemm_lds<BITS, HAS_ZP, SPLIT, WN><<<grid, 128 * WN, gemm_lds_bytes<BITS>(), s>>>(
+  k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM><<<grid, 128 * WN, gemm_lds_bytes<BITS, BM>(), s>>>(
       reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
       static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
       a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
@@ -1042,10 +1063,16 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
 template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, ctx->num_cus > 0 ? ctx->num_cus : 256);
-  if (p.wn == 4)
-    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4>(ctx, w, a, s, p.splits, p.cps);
-  else
-    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2>(ctx, w, a, s, p.splits, p.cps);
+  if (p.bm == 128) {
+    if (p.wn == 4)
+      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 128>(ctx, w, a, s, p.splits, p.cps);
+    else
+      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 128>(ctx, w, a, s, p.splits, p.cps);
+  } else if (p.wn == 4) {
+    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 256>(ctx, w, a, s, p.splits, p.cps);
+  } else {
+    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 256>(ctx, w, a, s, p.splits, p.cps);
+  }
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
