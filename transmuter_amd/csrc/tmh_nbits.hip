@@ -288,7 +288,10 @@ __global__ __launch_bounds__(1024) void k_gemv_lean(
   constexpr int NJ = SPLIT ? STEPS : 1;
   extern __shared__ float4_t red[];  // nwaves * TN * 64
   const int nwaves = blockDim.x >> 6;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wavefront index through readfirstlane: the compiler then knows it (and the chunk offsets
+  // formed from it) to be uniform and passes the chunk offset as the loads' scalar offset,
+  // instead of a loop over the lanes' distinct values around every weight load.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const uint32_t t0 = blockIdx.x * TN;
   const uint32_t nch = static_cast<uint32_t>(nchunks);
