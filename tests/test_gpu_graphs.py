@@ -62,3 +62,53 @@ def test_graph_replays_match_eager():
     finally:
         ctx.synchronize()
         ctx.close()
+
+
+def test_split_k_repeated_calls_and_replays_are_bit_exact(monkeypatch):
+    """Split-K GEMMs share the context's workspace of partial sums. Repeated eager calls,
+    several splits of one weight in one graph, and replays interleaved with eager calls must all
+    give the first call's bits."""
+    ctx = Context(0)
+    try:
+        rng = np.random.default_rng(22)
+        k, n, m = 2048, 1000, 300
+        b, s, z = nbits_weight(rng, k, n, 4, 128)
+        w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=4, block_size=128, weight_dtype="f16")
+        a = ctx.put(rng.standard_normal((m, k)).astype(np.float16))
+        ys = [ctx.empty((m, n), "f16") for _ in range(3)]
+        plans = ["128,2,4", "256,4,3", "128,4,2"]
+
+        def call(i):
+            monkeypatch.setenv("TMH_GEMM_PLAN", plans[i])
+            ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, a.ptr, F16, m, k, None, 0, ys[i].ptr, F16, n, None))
+
+        for i in range(3):  # eager first: sizes the workspace for the largest split
+            call(i)
+        ctx.synchronize()
+        first = [y.numpy() for y in ys]
+        for _ in range(2):
+            for i in range(3):
+                call(i)
+            ctx.synchronize()
+            for y, want in zip(ys, first):
+                assert np.array_equal(y.numpy(), want)
+        ctx.check(lib().tmh_graph_begin(ctx.handle, None))
+        for i in (0, 1, 2, 0):
+            call(i)
+        graph = ctypes.c_void_p()
+        ctx.check(lib().tmh_graph_end(ctx.handle, None, ctypes.byref(graph)))
+        for _ in range(3):
+            for y in ys:
+                ctx.check(lib().tmh_upload(ctx.handle, y.ptr, np.full(y.size, 7, np.uint16).ctypes.data_as(
+                    ctypes.c_void_p), y.nbytes))
+            ctx.check(lib().tmh_graph_launch(ctx.handle, graph, None))
+            ctx.synchronize()
+            for y, want in zip(ys, first):
+                assert np.array_equal(y.numpy(), want)
+            call(1)  # eager work on the same workspace between replays
+            ctx.synchronize()
+            assert np.array_equal(ys[1].numpy(), first[1])
+        ctx.check(lib().tmh_graph_destroy(ctx.handle, graph))
+    finally:
+        ctx.synchronize()
+        ctx.close()
