@@ -139,9 +139,12 @@ def time_graphs(ctx, graphs, steps, warmup):
 # ---------------------------------------------------------------- decode sweep (headline)
 
 
-def decode_sweep(ctx, steps, warmup, sets, ms, merged=False):
+def decode_sweep(ctx, steps, warmup, sets, ms, merged=False, full_step=False):
     """merged: q/k/v and gate/up run as one call each over concatenated weights, as the
-    reference's move/2 + Fusion.matmuls/2 leave a Qwen3 layer (4 calls instead of 7)."""
+    reference's move/2 + Fusion.matmuls/2 leave a Qwen3 layer (4 calls instead of 7).
+    full_step: also time a whole decode step, the 196 layer GEMVs and the 151936 x 1024
+    lm_head in one graph, and the host-observed latency of one eagerly launched 1024 -> 3072
+    GEMV (launch and synchronize)."""
     from transmuter_amd import PackedWeight
 
     rng = np.random.default_rng(20260101)
@@ -191,11 +194,51 @@ def decode_sweep(ctx, steps, warmup, sets, ms, merged=False):
             f"{results[m]['us_per_launch']:.2f} us/launch")
         for g in graphs:
             g.destroy()
+        if full_step:
+            results[m].update(full_decode_step(ctx, steps, warmup, weights, a, y, m))
     for ls in weights:
         for layer in ls:
             for w in layer:
                 w.free()
     return results
+
+
+def full_decode_step(ctx, steps, warmup, weights, a, y, m, vocab=151936, hidden=1024):
+    """A whole synthetic Qwen3-0.6B decode step (28 layers of 7 GEMVs, then the lm_head over
+    the tied 151936 x 1024 embedding) per graph, rotating over the layer weight copies, and the
+    host-observed latency of one eager 1024 -> 3072 GEMV."""
+    from transmuter_amd import PackedWeight
+
+    rng = np.random.default_rng(7)
+    b, sc, zp = make_weight_parts(rng, hidden, vocab)
+    lm = PackedWeight.upload(ctx, b, sc, zp, k=hidden, n=vocab, bits=4, block_size=32, weight_dtype="f16")
+    y_lm = ctx.empty((m, vocab), "f16")
+    graphs = []
+    for s in range(len(weights)):
+        def record(s=s):
+            for layer in range(QWEN3_LAYERS):
+                for w in weights[s][layer]:
+                    matmul_call(ctx, w, a[w.k], y[w.n], m)
+            matmul_call(ctx, lm, a[hidden], y_lm, m)
+        graphs.append(Graph(ctx, record))
+    ms_step = time_graphs(ctx, graphs, steps, warmup) / steps
+    for g in graphs:
+        g.destroy()
+    gate = weights[0][0][4]
+    for _ in range(20):
+        matmul_call(ctx, gate, a[gate.k], y[gate.n], m)
+        ctx.synchronize()
+    reps = 200
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        matmul_call(ctx, gate, a[gate.k], y[gate.n], m)
+        ctx.synchronize()
+    single_us = (time.perf_counter() - t0) * 1e6 / reps
+    lm.free()
+    log(f"decode step with lm_head M={m}: {ms_step * 1e3:.1f} us/step, {m * 1e3 / ms_step:.0f} tokens/s; "
+        f"one eager 1024->3072 GEMV, launch to synchronize: {single_us:.1f} us")
+    return {"ms_per_step_with_lm_head": ms_step, "tokens_per_s_with_lm_head": m * 1e3 / ms_step,
+            "single_launch_us": single_us}
 
 
 # ---------------------------------------------------------------- prefill GEMM
@@ -521,7 +564,7 @@ def main():
         ctx.close()
         return
     ms = [1] if args.quick else [1, 4, 8, 16]
-    dec = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms)
+    dec = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms, full_step=True)
     dec_merged = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms, merged=True)
     extra = {}
     if not args.quick:
@@ -547,7 +590,11 @@ def main():
                    "M": 1, "layers": QWEN3_LAYERS, "weight_copies": args.sets, "parallelism": "single GPU"},
         "tokens_per_s": head["tokens_per_s"],
         "decode_sweep": {str(m): {k: v for k, v in r.items() if k in ("gbs", "tflops", "ms_per_step", "us_per_launch",
-                                                                      "tokens_per_s")} for m, r in dec.items()},
+                                                                      "tokens_per_s", "ms_per_step_with_lm_head",
+                                                                      "tokens_per_s_with_lm_head", "single_launch_us")}
+                         for m, r in dec.items()},
+        "tokens_per_s_with_lm_head": head.get("tokens_per_s_with_lm_head"),
+        "single_launch_us": head.get("single_launch_us"),
         "decode_merged_qkv_gateup": {str(m): {k: v for k, v in r.items() if k in ("gbs", "ms_per_step", "us_per_launch",
                                                                                   "tokens_per_s")}
                                      for m, r in dec_merged.items()},
