@@ -1,8 +1,9 @@
 """DequantizeLinear on the GPU against the oracle, bit-exactly, on seeded random inputs: each
 parameter layout of expand_quant_param/3 (one value, one per axis entry, blocks along the axis),
 every integer value type and float values, f32/f16/bf16 scales, with and without zero points,
-shapes whose inner extent is not a multiple of the kernel's four elements per thread, and the
-2048 x 2048 u8 tensor of the int8 benchmark."""
+shapes whose inner extent is not a multiple of the kernel's four elements per thread, 1-byte
+values with per-tensor or last-axis parameters (the vectorized kernel), and the 2048 x 2048 u8
+tensor of the int8 benchmark."""
 
 import zlib
 
@@ -28,6 +29,13 @@ CASES = [
     ((6, 7), 1, 0, "tensor", "f16", "f16", True),
     ((), 0, 0, "tensor", "u8", "f32", True),
     ((2, 3, 1023), 2, 256, "blocked", "u8", "f16", True),
+    # 1-byte x, per tensor or along the last axis (a multiple of 4): four elements per 4-byte load
+    ((16, 64), 1, 0, "axis", "s8", "bf16", True),
+    ((8, 32), 1, 0, "axis", "u8", "f16", False),
+    ((4, 6, 8), 2, 0, "axis", "s8", "f32", False),
+    ((1024,), 0, 0, "tensor", "s8", "f16", True),
+    ((12, 20), 0, 0, "tensor", "u8", "f32", False),
+    ((2, 8), 0, 0, "tensor", "u8", "bf16", True),
 ]
 
 INT_RANGES = {"u8": (0, 256), "s8": (-128, 128), "u16": (0, 65536), "s16": (-32768, 32768),

@@ -274,6 +274,80 @@ __global__ __launch_bounds__(256) void k_dequantize_linear4(
   }
 }
 
+// DequantizeLinear of 1-byte integers (SIGNED: s8) with per-tensor parameters or parameters
+// along the last axis (AXIS, dim % 4 == 0): four elements per thread from one 4-byte load, their
+// four scales and zero points (1-byte, x's type) from one 8/16-byte and one 4-byte load. Same
+// arithmetic as k_dequantize_linear4: the exact integer x - zero in f32, times the scale read as
+// f32, rounded once to the scale's type OUT.
+template <int OUT, bool SIGNED, bool HAS_ZERO, bool AXIS>
+__global__ __launch_bounds__(256) void k_dequantize_linear_b4(const uint32_t* __restrict__ x,
+                                                              const void* __restrict__ scale,
+                                                              const uint32_t* __restrict__ zero, uint32_t dim,
+                                                              void* __restrict__ y, uint32_t quads) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= quads) return;
+  const uint32_t xv = x[t];
+  float sc[4];
+  uint32_t zv = 0;
+  if constexpr (AXIS) {
+    const uint32_t d4 = (t * 4u) % dim / 4u;  // the four elements share a row: parameters d .. d+3
+    if constexpr (OUT == DT_F32) {
+      const float4_t v = reinterpret_cast<const float4_t*>(scale)[d4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sc[j] = v[j];
+    } else {
+      const uint2 v = reinterpret_cast<const uint2*>(scale)[d4];
+      const uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const auto h = static_cast<uint16_t>(w[j / 2] >> (16 * (j % 2)));
+        sc[j] = OUT == DT_F16 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
+      }
+    }
+    if constexpr (HAS_ZERO) zv = zero[d4];
+  } else {
+    const float s0 = load_as_f32<OUT>(scale, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sc[j] = s0;
+    if constexpr (HAS_ZERO) zv = (reinterpret_cast<const uint8_t*>(zero)[0]) * 0x01010101u;
+  }
+  float out[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t xb = (xv >> (8 * j)) & 0xFFu, zb = (zv >> (8 * j)) & 0xFFu;
+    const int q = SIGNED ? static_cast<int>(static_cast<int8_t>(xb)) : static_cast<int>(xb);
+    const int z = SIGNED ? static_cast<int>(static_cast<int8_t>(zb)) : static_cast<int>(zb);
+    out[j] = static_cast<float>(q - z) * sc[j];
+  }
+  if constexpr (OUT == DT_F32) {
+    reinterpret_cast<float4_t*>(y)[t] = float4_t{out[0], out[1], out[2], out[3]};
+  } else {
+    uint16_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h[j] = OUT == DT_F16 ? f32_to_f16_bits(out[j]) : f32_to_bf16_bits(out[j]);
+    reinterpret_cast<uint2*>(y)[t] =
+        make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+  }
+}
+
+template <int OUT, bool SIGNED>
+void launch_dql_b4(const void* x, const void* scale, const void* zero, bool axis, uint32_t dim, void* y,
+                   uint32_t quads, hipStream_t s) {
+  const dim3 grid((quads + 255) / 256);
+  const auto* xq = static_cast<const uint32_t*>(x);
+  const auto* zq = static_cast<const uint32_t*>(zero);
+  if (axis) {
+    if (zero)
+      k_dequantize_linear_b4<OUT, SIGNED, true, true><<<grid, 256, 0, s>>>(xq, scale, zq, dim, y, quads);
+    else
+      k_dequantize_linear_b4<OUT, SIGNED, false, true><<<grid, 256, 0, s>>>(xq, scale, zq, dim, y, quads);
+  } else if (zero) {
+    k_dequantize_linear_b4<OUT, SIGNED, true, false><<<grid, 256, 0, s>>>(xq, scale, zq, dim, y, quads);
+  } else {
+    k_dequantize_linear_b4<OUT, SIGNED, false, false><<<grid, 256, 0, s>>>(xq, scale, zq, dim, y, quads);
+  }
+}
+
 // ------------------------------------------------------------------ MatMulInteger on int8 MFMA
 
 // y[bt, m, n] = sum_k (a - a_zero[m]) (b - b_zero[n]), wrapping mod 2^32. Each f32 chunk sum of
@@ -682,6 +756,33 @@ int tmh_dequantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t ou
   if (!d_x || !d_scale || !d_y) return fail(ctx, TMH_ERR_INVALID, "DequantizeLinear: NULL pointer");
   hipStream_t s = pick_stream(ctx, stream);
   const int64_t nb = mode == TMH_QPARAM_BLOCKED ? (dim + block_size - 1) / block_size : 1;
+  {
+    // 1-byte x with per-tensor or last-axis parameters: the vectorized kernel.
+    const int out_bytes = scale_dtype == TMH_F16 || scale_dtype == TMH_BF16 ? 2 : 4;
+    const auto aligned = [](const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };
+    const bool axis = mode == TMH_QPARAM_AXIS && inner == 1 && dim % 4 == 0;
+    if ((x_dtype == TMH_U8 || x_dtype == TMH_S8) && (!d_zero || zero_dtype == x_dtype) &&
+        (mode == TMH_QPARAM_TENSOR || axis) && total % 4 == 0 && total / 4 < (int64_t{1} << 31) &&
+        aligned(d_x, 4) && aligned(d_y, 4 * out_bytes) && (!axis || aligned(d_scale, 4 * out_bytes)) &&
+        (!axis || !d_zero || aligned(d_zero, 4))) {
+      const auto quads = static_cast<uint32_t>(total / 4), d32 = static_cast<uint32_t>(dim);
+      const bool sgn = x_dtype == TMH_S8;
+      switch (scale_dtype) {
+        case TMH_F16:
+          sgn ? launch_dql_b4<DT_F16, true>(d_x, d_scale, d_zero, axis, d32, d_y, quads, s)
+              : launch_dql_b4<DT_F16, false>(d_x, d_scale, d_zero, axis, d32, d_y, quads, s);
+          break;
+        case TMH_BF16:
+          sgn ? launch_dql_b4<DT_BF16, true>(d_x, d_scale, d_zero, axis, d32, d_y, quads, s)
+              : launch_dql_b4<DT_BF16, false>(d_x, d_scale, d_zero, axis, d32, d_y, quads, s);
+          break;
+        default:
+          sgn ? launch_dql_b4<DT_F32, true>(d_x, d_scale, d_zero, axis, d32, d_y, quads, s)
+              : launch_dql_b4<DT_F32, false>(d_x, d_scale, d_zero, axis, d32, d_y, quads, s);
+      }
+      return check_launch(ctx, "k_dequantize_linear_b4");
+    }
+  }
   if (total < (int64_t{1} << 31) - 4) {
     const int out_bytes = scale_dtype == TMH_F16 || scale_dtype == TMH_BF16 ? 2 : 4;
     const bool y_vec = reinterpret_cast<uintptr_t>(d_y) % (4 * out_bytes) == 0;
