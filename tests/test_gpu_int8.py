@@ -68,6 +68,9 @@ def test_matmul_integer_extremes_past_two_to_the_24(ctx):
 DQL_CASES = [
     ("normal", 1000), ("normal", 5), ("normal", 300_000), ("positive", 4097), ("negative", 77), ("constant", 64),
     ("zeros", 10), ("ties", 256), ("empty", 0),
+    # partial ranges over many workgroups, reduced in the quantize pass; grid-stride rounds and
+    # a ragged tail
+    ("normal", 2048 * 2048), ("positive", 2_000_003), ("negative", 1_048_577),
 ]
 
 

@@ -586,14 +586,21 @@ __global__ __launch_bounds__(512) void k_matmul_integer_mfma(
 
 // scale = (max(x, 0) - min(x, 0)) / 255 (1 when that is 0), zero = saturate(round(-low / scale)),
 // in f32 with round-half-even, as quantized.ex:94-103.
-__device__ __forceinline__ void dql_params(float low, float high, float* scale, uint8_t* zero) {
+__device__ __forceinline__ void dql_param_values(float low, float high, float& sc, uint8_t& zq) {
   low = fminf(low, 0.f);
   high = fmaxf(high, 0.f);
-  float sc = (high - low) / 255.f;
+  sc = (high - low) / 255.f;
   if (sc == 0.f) sc = 1.f;
   const float z = rintf(-low / sc);
+  zq = static_cast<uint8_t>(fminf(fmaxf(z, 0.f), 255.f));
+}
+
+__device__ __forceinline__ void dql_params(float low, float high, float* scale, uint8_t* zero) {
+  float sc;
+  uint8_t zq;
+  dql_param_values(low, high, sc, zq);
   *scale = sc;
-  *zero = static_cast<uint8_t>(fminf(fmaxf(z, 0.f), 255.f));
+  *zero = zq;
 }
 
 // Minimum and maximum of 256 values per thread (one per lane) through LDS; thread 0 ends with both.
@@ -659,17 +666,6 @@ __global__ __launch_bounds__(256) void k_dql_minmax(const float* __restrict__ x,
   }
 }
 
-__global__ __launch_bounds__(256) void k_dql_finalize(const float* __restrict__ part, int parts, float* __restrict__ scale,
-                                                       uint8_t* __restrict__ zero) {
-  float lo = INFINITY, hi = -INFINITY;
-  for (int i = threadIdx.x; i < parts; i += blockDim.x) {
-    lo = fminf(lo, part[2 * i]);
-    hi = fmaxf(hi, part[2 * i + 1]);
-  }
-  dql_block_range(lo, hi);
-  if (threadIdx.x == 0) dql_params(lo, hi, scale, zero);
-}
-
 // y = saturate(round(x / scale) + zero), four values per thread.
 __global__ __launch_bounds__(256) void k_dql_quantize(const float* __restrict__ x, int64_t n,
                                                        const float* __restrict__ scale, const uint8_t* __restrict__ zero,
@@ -683,6 +679,45 @@ __global__ __launch_bounds__(256) void k_dql_quantize(const float* __restrict__ 
     *reinterpret_cast<uint32_t*>(y + i) = q(v[0]) | (q(v[1]) << 8) | (q(v[2]) << 16) | (q(v[3]) << 24);
   } else {
     for (int e = 0; e < 4 && i + e < n; ++e) y[i + e] = static_cast<uint8_t>(q(x[i + e]));
+  }
+}
+
+// The quantize pass with the range reduction folded in: every workgroup issues its loads of x,
+// then reduces the `parts` partial ranges (through LDS) to the scale and zero point (all
+// workgroups compute the same values); workgroup 0 stores them. Grid-stride over groups of 1024 values,
+// four per thread, so that few workgroups repeat the reduction.
+__global__ __launch_bounds__(256) void k_dql_quantize_reduce(const float* __restrict__ x, int64_t n,
+                                                              const float* __restrict__ part, int parts,
+                                                              float* __restrict__ scale, uint8_t* __restrict__ zero,
+                                                              uint8_t* __restrict__ y) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 1024;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * 1024 + threadIdx.x * 4;
+  const bool vec = (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (reinterpret_cast<uintptr_t>(y) % 4) == 0;
+  float4_t v = float4_t{0.f, 0.f, 0.f, 0.f};
+  if (vec && i + 4 <= n) v = *reinterpret_cast<const float4_t*>(x + i);
+  float lo = INFINITY, hi = -INFINITY;
+  for (int p = threadIdx.x; p < parts; p += blockDim.x) {
+    lo = fminf(lo, part[2 * p]);
+    hi = fmaxf(hi, part[2 * p + 1]);
+  }
+  dql_block_range(lo, hi);
+  float sc;
+  uint8_t zq;
+  dql_param_values(lo, hi, sc, zq);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *scale = sc;
+    *zero = zq;
+  }
+  const float z = static_cast<float>(zq);
+  auto q = [&](float f) -> uint32_t { return static_cast<uint32_t>(fminf(fmaxf(rintf(f / sc) + z, 0.f), 255.f)); };
+  for (; i < n; i += stride) {
+    if (vec && i + 4 <= n) {
+      const float4_t w = v;
+      if (i + stride + 4 <= n) v = *reinterpret_cast<const float4_t*>(x + i + stride);
+      *reinterpret_cast<uint32_t*>(y + i) = q(w[0]) | (q(w[1]) << 8) | (q(w[2]) << 16) | (q(w[3]) << 24);
+    } else {
+      for (int e = 0; e < 4 && i + e < n; ++e) y[i + e] = static_cast<uint8_t>(q(x[i + e]));
+    }
   }
 }
 
@@ -859,8 +894,10 @@ int tmh_dynamic_quantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int6
   k_dql_minmax<<<static_cast<unsigned>(std::max(parts, 1)), 256, 0, s>>>(x, n, part, scale, zero);
   TMH_TRY(check_launch(ctx, "k_dql_minmax"));
   if (parts > 1) {
-    k_dql_finalize<<<1, 256, 0, s>>>(part, parts, scale, zero);
-    TMH_TRY(check_launch(ctx, "k_dql_finalize"));
+    const int64_t groups = (n + 1023) / 1024;
+    k_dql_quantize_reduce<<<static_cast<unsigned>(std::min<int64_t>(groups, 1024)), 256, 0, s>>>(
+        x, n, part, parts, scale, zero, static_cast<uint8_t*>(d_y));
+    return check_launch(ctx, "k_dql_quantize_reduce");
   }
   if (n == 0) return TMH_OK;
   k_dql_quantize<<<static_cast<unsigned>((n + 1023) / 1024), 256, 0, s>>>(x, n, scale, zero, static_cast<uint8_t*>(d_y));
