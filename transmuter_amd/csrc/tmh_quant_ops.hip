@@ -603,21 +603,28 @@ __device__ __forceinline__ void dql_params(float low, float high, float* scale, 
   *zero = zq;
 }
 
-// Minimum and maximum of 256 values per thread (one per lane) through LDS; thread 0 ends with both.
+// Minimum and maximum over the workgroup (up to 16 wavefronts, one value pair per lane): a
+// shuffle reduction inside each wavefront, then one exchange through LDS; every thread ends with
+// both. min and max do not depend on the order of their operands' combination.
 __device__ __forceinline__ void dql_block_range(float& lo, float& hi) {
-  __shared__ float lo_s[256], hi_s[256];
-  lo_s[threadIdx.x] = lo;
-  hi_s[threadIdx.x] = hi;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) {
-      lo_s[threadIdx.x] = fminf(lo_s[threadIdx.x], lo_s[threadIdx.x + w]);
-      hi_s[threadIdx.x] = fmaxf(hi_s[threadIdx.x], hi_s[threadIdx.x + w]);
-    }
-    __syncthreads();
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, o));
+    hi = fmaxf(hi, __shfl_xor(hi, o));
   }
+  __shared__ float lo_s[16], hi_s[16];
+  const int waves = static_cast<int>(blockDim.x >> 6);
+  if ((threadIdx.x & 63) == 0) {
+    lo_s[threadIdx.x >> 6] = lo;
+    hi_s[threadIdx.x >> 6] = hi;
+  }
+  __syncthreads();
   lo = lo_s[0];
   hi = hi_s[0];
+  for (int w = 1; w < waves; ++w) {
+    lo = fminf(lo, lo_s[w]);
+    hi = fmaxf(hi, hi_s[w]);
+  }
 }
 
 // Minimum and maximum of the workgroup's share of x (16-byte loads, four in flight per thread
