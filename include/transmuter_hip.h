@@ -191,8 +191,9 @@ int tmh_dequantize_nbits(tmh_ctx* ctx, const tmh_weight* w, void* d_out, int out
  *  d_y    [M, N] of y_dtype, rows ldy elements apart (ldy >= N)
  * The sums accumulate in f32 and round once to y_dtype. M >= 0 (M == 0 does nothing).
  * For M > 64 with f16 A the library picks the GEMM's tile shape and K split itself; the
- * environment variable TMH_GEMM_PLAN="bm,wn,splits" (bm 128 or 256, wn 2 or 4) forces them,
- * for tests and tuning (an invalid value is ignored).
+ * environment variable TMH_GEMM_PLAN="bm,wn,splits[,ks]" (bm 128 or 256, wn 2 or 4; ks 2, with
+ * bm 128 and wn 2 only, splits each k-block between two wavefronts) forces them, for tests and
+ * tuning (an invalid value is ignored).
  */
 int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
                      int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype,

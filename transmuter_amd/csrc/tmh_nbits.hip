@@ -16,6 +16,7 @@
 //   k_matmul_general  any float types and float zero points, f32 FMA on the vector ALUs
 #include <algorithm>
 #include <cstdio>
+#include <type_traits>
 #include <cstdlib>
 #include <vector>
 
@@ -465,9 +466,13 @@ __global__ __launch_bounds__(256) void k_gemm_f16(
 // splitting K, and its 64 KiB of LDS lets two workgroups share a CU.
 constexpr int kGemmBM = 256;  // largest tile height: bounds the A rows a launch may touch
 
-template <int BITS, int BM>
+// LDS of one workgroup: the double-buffered A tile, or (KS = 2) the partial sums of half the
+// wavefronts after the k-loop, whichever is larger.
+template <int BITS, int BM, int KS = 1>
 constexpr size_t gemm_lds_bytes() {
-  return 2 * static_cast<size_t>(BM) * (512 / BITS) * 2;
+  constexpr size_t a_tiles = 2 * static_cast<size_t>(BM) * (512 / BITS) * 2;
+  constexpr size_t partial = KS > 1 ? static_cast<size_t>(BM) * 128 * sizeof(float) : 0;
+  return a_tiles > partial ? a_tiles : partial;
 }
 
 // 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (buffer_load_dwordx4
@@ -487,8 +492,8 @@ __device__ __forceinline__ int a_slot(int row, int piece) {
   return BITS == 8 ? (piece ^ ((row >> 1) & 7)) : (piece ^ (row & 15));
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM>
-__global__ __launch_bounds__(128 * WN) void k_gemm_lds(
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS>
+__global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
     int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
@@ -500,7 +505,12 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   constexpr int ROWB = CW * 2;           // bytes per LDS row
   constexpr int PPR = CW / 8;            // 16-byte pieces per row
   constexpr int RPI = 64 / PPR;          // rows per wavefront load instruction
-  constexpr int RW = BM / (2 * WN);      // A rows each wavefront brings into LDS
+  constexpr int RW = BM / (2 * WN * KS); // A rows each wavefront brings into LDS
+  // KS == 2 (BM = 128, WN = 2 only): eight wavefronts, two per SIMD; wavefronts w and w + 4 share
+  // an output sub-tile and take the first and second half of each k-block's MFMA steps, and the
+  // second half's partial sums add to the first's through LDS after the k-loop.
+  static_assert(KS == 1 || (KS == 2 && BM == 128 && WN == 2), "K split inside the workgroup");
+  constexpr int LSTEPS = STEPS / KS;     // MFMA steps per k-block of one wavefront
   constexpr int LOADS = RW / RPI;        // load instructions per wavefront per k-block
   constexpr int NJ = SPLIT ? STEPS : 1;  // parameter entries per tile per k-block
   // Tall (WN == 4, eight wavefronts, two per SIMD; or BM == 128): each wavefront takes all BM
@@ -514,7 +524,9 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int wm = TALL ? 0 : wave / WN, wn = TALL ? wave : wave % WN;
+  const int wl = wave % (2 * WN);        // the wavefront's output sub-tile
+  const int kh = wave / (2 * WN);        // its half of the k-block's steps (KS == 2)
+  const int wm = TALL ? 0 : wl / WN, wn = TALL ? wl : wl % WN;
   // Consecutive workgroups take the m-blocks of one n-block, so each XCD keeps one m-block's
   // A rows in its L2 while the weights stream past.
   // With split K (ws != nullptr), workgroup blocks of mblocks*nblocks take consecutive ranges of
@@ -525,7 +537,7 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   const int mb = static_cast<int>(tile % static_cast<unsigned>(mblocks));
   const int nb = static_cast<int>(tile / static_cast<unsigned>(mblocks));
   const int m0 = mb * BM;
-  const int t0 = TALL ? nb * 4 * WN + wave * NTW : (nb * WN + wn) * 4;
+  const int t0 = TALL ? nb * 4 * WN + wl * NTW : (nb * WN + wn) * 4;
   const uint32_t nch = static_cast<uint32_t>(nchunks);
   const uint32_t kb0 = static_cast<uint32_t>(split) * static_cast<uint32_t>(chunks_per_split);
   const uint32_t kb1 = kb0 + chunks_per_split < nch ? kb0 + chunks_per_split : nch;
@@ -610,12 +622,12 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
   // The next k-block's loads, spread over the steps of this one so that the eight wavefronts
   // do not queue all of them on the CU's memory path at once after each barrier: A in the first
   // half of the steps, then the weights, so the A loads still precede the weight loads (WAIT_A).
-  constexpr int HA = STEPS > 1 ? STEPS / 2 : 1;
-  constexpr int HB = STEPS > 1 ? STEPS - HA : 1;
+  constexpr int HA = LSTEPS > 1 ? LSTEPS / 2 : 1;
+  constexpr int HB = LSTEPS > 1 ? LSTEPS - HA : 1;
   auto issue = [&](int i, uint32_t kb, int buf, BStage& st) {
     if (i < HA) load_a(kb, buf, i * LOADS / HA, (i + 1) * LOADS / HA);
-    if (STEPS == 1 || i >= HA) {
-      const int ib = STEPS == 1 ? 0 : i - HA;
+    if (LSTEPS == 1 || i >= HA) {
+      const int ib = LSTEPS == 1 ? 0 : i - HA;
       load_b(kb, st, ib * NTW / HB, (ib + 1) * NTW / HB);
     }
   };
@@ -627,9 +639,13 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     if constexpr (TALL) {
       // Two wavefronts per SIMD: each keeps few registers live and relies on the other to fill
       // its waits; one set of weight fragments per step, A fragments read one ahead of use.
+      // Step i = KH * LSTEPS + li stays a compile-time index (KH is the wavefront's half).
+      auto steps = [&](auto khc) {
+        constexpr int KH = decltype(khc)::value;
 #pragma unroll
-      for (int i = 0; i < STEPS; ++i) {
-        if (more) issue(i, kbn, buf ^ 1, nst);
+      for (int li = 0; li < LSTEPS; ++li) {
+        const int i = KH * LSTEPS + li;
+        if (more) issue(li, kbn, buf ^ 1, nst);
         half8_t bc[NTW];
         dequant(st, i, bc);
         // A fragment mt + 1 is read while fragment mt feeds its MFMAs; the scheduling
@@ -647,6 +663,14 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
           __builtin_amdgcn_sched_barrier(0);
           if (mt + 1 < MTW) a = an;
         }
+      }
+      };
+      if constexpr (KS == 1) {
+        steps(std::integral_constant<int, 0>{});
+      } else if (kh == 0) {
+        steps(std::integral_constant<int, 0>{});
+      } else {
+        steps(std::integral_constant<int, 1>{});
       }
       return;
     }
@@ -692,6 +716,23 @@ __global__ __launch_bounds__(128 * WN) void k_gemm_lds(
     }
     __syncthreads();
     if (more) cur = next;
+  }
+  if constexpr (KS == 2) {
+    // The second half's partial sums through LDS (free after the k-loop's last barrier: no
+    // load into it is in flight) into the first half's; the first half stores.
+    auto* part = reinterpret_cast<float4_t*>(lds);
+    if (kh == 1) {
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) part[((wl * MTW + mt) * NTW + nt) * 64 + lane] = acc[mt][nt];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] += part[((wl * MTW + mt) * NTW + nt) * 64 + lane];
   }
   // Lane (16g + r) holds, for each (mt, nt), row mt*16 + r and the 4 columns nt*16 + 4g ...
   const bool f16_out = y_dt == DT_F16 && dot_dt == DT_F16 && !bias;
@@ -979,27 +1020,29 @@ void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
 // Split K when the output tiles cannot fill the GPU: partial sums go to the context's
 // workspace and k_splitk_reduce adds them. During stream capture the workspace cannot grow,
 // so a capture that finds it too small runs without splitting.
-// Tile shape and K split of one prefill GEMM. Each candidate (BM x 64*WN tiles, 1-16 splits of
-// K) is priced as rounds of workgroups over the CUs times the work of one, at the per-CU rate
-// the tile shape sustains on MI355X with every CU busy (dense f16 TFLOP/s per CU, measured on the
-// SmolLM3-3B and 2048x4096x8192 shapes; with these rates the plan chosen for each SmolLM3-3B
-// projection at M = 256 and 2048 was the fastest of the candidates timed, or within 6% of it),
-// plus the f32 partial sums a split writes and the reduction reads back.
-// TMH_GEMM_PLAN="bm,wn,splits" in the environment forces a plan (tests use it to reach every
+// Tile shape and K split of one prefill GEMM. Each candidate (BM x 64*WN tiles; KS = 2 for the
+// 128x128 tile on eight wavefronts that split each k-block's steps; 1-16 splits of K) is priced
+// as rounds of workgroups over the CUs times the work of one, at the per-CU rate the tile shape
+// sustains on MI355X with every CU busy (dense f16 TFLOP/s per CU, measured on the SmolLM3-3B
+// and 2048x4096x8192 shapes; with these rates the plan chosen for each SmolLM3-3B projection at
+// M = 256 and 2048 was the fastest of the candidates timed, or within 6% of it), plus the f32
+// partial sums a split writes and the reduction reads back.
+// TMH_GEMM_PLAN="bm,wn,splits[,ks]" in the environment forces a plan (tests use it to reach every
 // tile shape; an invalid value is ignored).
 struct GemmShape {
-  int bm, wn;
+  int bm, wn, ks;
   double rate;  // dense f16 FLOP/s per CU
 };
-constexpr GemmShape kGemmShapes[] = {{256, 2, 2.8e12}, {256, 4, 3.9e12}, {128, 2, 2.4e12}, {128, 4, 3.3e12}};
+constexpr GemmShape kGemmShapes[] = {
+    {256, 2, 1, 2.8e12}, {256, 4, 1, 3.9e12}, {128, 2, 1, 2.4e12}, {128, 4, 1, 3.3e12}, {128, 2, 2, 2.9e12}};
 
 struct GemmPlan {
-  int bm, wn, splits, cps;
+  int bm, wn, splits, cps, ks = 1;
 };
 
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bits, int cus) {
   const double cw = 512.0 / bits;
-  GemmPlan best{256, 2, 1, static_cast<int>(nchunks)};
+  GemmPlan best{256, 2, 1, static_cast<int>(nchunks), 1};
   double best_t = 1e30;
   for (const GemmShape& sh : kGemmShapes) {
     const int64_t mblocks = (M + sh.bm - 1) / sh.bm;
@@ -1018,22 +1061,23 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
       if (splits > 1) t += 2.0 * splits * M * N * 4 / 5e12;
       if (t < best_t) {
         best_t = t;
-        best = GemmPlan{sh.bm, sh.wn, static_cast<int>(splits), static_cast<int>(cps)};
+        best = GemmPlan{sh.bm, sh.wn, static_cast<int>(splits), static_cast<int>(cps), sh.ks};
       }
     }
   }
   if (const char* f = getenv("TMH_GEMM_PLAN")) {
-    int bm = 0, wn = 0, sp = 0;
-    if (sscanf(f, "%d,%d,%d", &bm, &wn, &sp) == 3 && (bm == 128 || bm == 256) && (wn == 2 || wn == 4) && sp >= 1 &&
-        sp <= nchunks) {
+    int bm = 0, wn = 0, sp = 0, ks = 1;
+    const int got = sscanf(f, "%d,%d,%d,%d", &bm, &wn, &sp, &ks);
+    if ((got == 3 || got == 4) && (bm == 128 || bm == 256) && (wn == 2 || wn == 4) && sp >= 1 && sp <= nchunks &&
+        (ks == 1 || (ks == 2 && bm == 128 && wn == 2))) {
       const int cps = static_cast<int>((nchunks + sp - 1) / sp);
-      best = GemmPlan{bm, wn, static_cast<int>((nchunks + cps - 1) / cps), cps};
+      best = GemmPlan{bm, wn, static_cast<int>((nchunks + cps - 1) / cps), cps, ks};
     }
   }
   return best;
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM>
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS = 1>
 void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s, int splits, int cps) {
   const int mblocks = static_cast<int>((a.M + BM - 1) / BM);
   const int nblocks = static_cast<int>((w->ntiles + 4 * WN - 1) / (4 * WN));
@@ -1048,10 +1092,10 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
   }
   const dim3 grid(static_cast<unsigned>(tiles * splits));
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(gemm_lds_bytes<BITS, BM>()));
+      reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(gemm_lds_bytes<BITS, BM, KS>()));
   (void)attr;
-  k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM><<<grid, 128 * WN, gemm_lds_bytes<BITS, BM>(), s>>>(
+  k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS><<<grid, 128 * WN * KS, gemm_lds_bytes<BITS, BM, KS>(), s>>>(
       reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
       static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
       a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
@@ -1066,7 +1110,9 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
 template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, ctx->num_cus > 0 ? ctx->num_cus : 256);
-  if (p.bm == 128) {
+  if (p.bm == 128 && p.ks == 2) {
+    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 128, 2>(ctx, w, a, s, p.splits, p.cps);
+  } else if (p.bm == 128) {
     if (p.wn == 4)
       launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 128>(ctx, w, a, s, p.splits, p.cps);
     else
