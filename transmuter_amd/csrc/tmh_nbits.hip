@@ -643,27 +643,27 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
       auto steps = [&](auto khc) {
         constexpr int KH = decltype(khc)::value;
 #pragma unroll
-      for (int li = 0; li < LSTEPS; ++li) {
-        const int i = KH * LSTEPS + li;
-        if (more) issue(li, kbn, buf ^ 1, nst);
-        half8_t bc[NTW];
-        dequant(st, i, bc);
-        // A fragment mt + 1 is read while fragment mt feeds its MFMAs; the scheduling
-        // barriers keep the compiler from sinking each read next to its first use.
-        const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
-        half8_t a = *reinterpret_cast<const half8_t*>(abase + slot);
+        for (int li = 0; li < LSTEPS; ++li) {
+          const int i = KH * LSTEPS + li;
+          if (more) issue(li, kbn, buf ^ 1, nst);
+          half8_t bc[NTW];
+          dequant(st, i, bc);
+          // A fragment mt + 1 is read while fragment mt feeds its MFMAs; the scheduling
+          // barriers keep the compiler from sinking each read next to its first use.
+          const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
+          half8_t a = *reinterpret_cast<const half8_t*>(abase + slot);
 #pragma unroll
-        for (int mt = 0; mt < MTW; ++mt) {
-          half8_t an;
-          if (mt + 1 < MTW) an = *reinterpret_cast<const half8_t*>(abase + (mt + 1) * 16 * ROWB + slot);
-          __builtin_amdgcn_sched_barrier(0);
+          for (int mt = 0; mt < MTW; ++mt) {
+            half8_t an;
+            if (mt + 1 < MTW) an = *reinterpret_cast<const half8_t*>(abase + (mt + 1) * 16 * ROWB + slot);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int nt = 0; nt < NTW; ++nt)
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[nt], a, acc[mt][nt], 0, 0, 0);
-          __builtin_amdgcn_sched_barrier(0);
-          if (mt + 1 < MTW) a = an;
+            for (int nt = 0; nt < NTW; ++nt)
+              acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[nt], a, acc[mt][nt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (mt + 1 < MTW) a = an;
+          }
         }
-      }
       };
       if constexpr (KS == 1) {
         steps(std::integral_constant<int, 0>{});
