@@ -21,6 +21,10 @@
  *  - Prefill MatMulNBits (split K), DynamicQuantizeLinear and QMoE keep
  *    intermediates in one workspace per context, grown outside graph capture. Calls of one
  *    context on two streams must not run at the same time; use a context per concurrent stream.
+ *    A call that would have to grow the workspace while its stream is being captured into a
+ *    graph fails with TMH_ERR_UNSUPPORTED (run it once before the capture). A workspace that
+ *    grows is not freed: graphs captured earlier keep its address, so it stays allocated until
+ *    tmh_ctx_destroy, after which no graph that used it may be launched.
  */
 #ifndef TRANSMUTER_HIP_H
 #define TRANSMUTER_HIP_H
@@ -193,7 +197,9 @@ int tmh_dequantize_nbits(tmh_ctx* ctx, const tmh_weight* w, void* d_out, int out
  * For M > 64 with f16 A the library picks the GEMM's tile shape and K split itself; the
  * environment variable TMH_GEMM_PLAN="bm,wn,splits[,ks]" (bm 128 or 256, wn 2 or 4; ks 2, with
  * bm 128 and wn 2 only, splits each k-block between two wavefronts) forces them, for tests and
- * tuning (an invalid value is ignored).
+ * tuning (an invalid value is ignored). A call whose plan splits K keeps splits*M*N f32 partial
+ * sums in the context's workspace; during graph capture it fails with TMH_ERR_UNSUPPORTED when
+ * the workspace is too small, so a graph always computes what an eager call does.
  */
 int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
                      int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype,

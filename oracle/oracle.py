@@ -405,49 +405,121 @@ def _activate(h, activation, fusion, alpha, beta, limit):
     raise ValueError(activation)
 
 
+def _narrow_activate(h, activation, fusion, alpha, beta, limit, dtype):
+    """`MoE.activate/2` and `swiglu_gate/3` (moe.ex:176-206) on values of a narrow type: every Nx
+    operation computes in f32 and rounds once to `dtype` (f16 or bf16), as each Nx op returns a
+    tensor of its inputs' type (a Elixir float scalar takes the tensor's type)."""
+    r = lambda v: _narrow(v, dtype).astype(np.float32)  # noqa: E731
+    h = np.asarray(h, dtype=np.float32)
+
+    def sigmoid(v):
+        return r(1.0 / (1.0 + np.exp(-v.astype(np.float64))))
+
+    def gate(g, lin):
+        if limit != 0:
+            g = np.minimum(g, np.float32(limit))
+            lin = np.clip(lin, -np.float32(limit), np.float32(limit))
+        return r(r(g * sigmoid(r(np.float32(alpha) * g))) * r(lin + np.float32(beta)))
+
+    if activation == "relu":
+        return np.maximum(h, 0)
+    if activation == "silu":
+        return r(h * sigmoid(h))
+    if activation == "identity":
+        return h
+    if activation == "gelu":
+        from math import erf, sqrt
+        verf = np.vectorize(erf)
+        inner = r(verf(r(h * np.float32(1.0 / sqrt(2)))))
+        return r(h * r(np.float32(0.5) * r(np.float32(1.0) + inner)))
+    if activation == "swiglu":
+        if fusion == 2:
+            inter = h.shape[1] // 2
+            return gate(h[:, :inter], h[:, inter:])
+        pairs = h.reshape(h.shape[0], -1, 2)
+        return gate(pairs[..., 0], pairs[..., 1])
+    raise ValueError(activation)
+
+
 def qmoe(x, router, fc1, fc1_scales, fc2, fc2_scales, *, k: int, bits: int = 4, block_size: int = 0,
          activation: str = "relu", swiglu_fusion: int = 0, alpha: float = 1.0, beta: float = 0.0,
          limit: float = 0.0, fc1_bias=None, fc2_bias=None, fc3=None, fc3_scales=None, fc3_bias=None,
          fc1_zp=None, fc2_zp=None, fc3_zp=None) -> np.ndarray:
     """QMoE (moe.ex:42-61, 64-102), with the routed math: each token runs its top-k experts
     (top-k router values, then a softmax over those k values) and adds their outputs with the
-    routing weights. The reference's dense variant (every expert on every token with weight 0
-    for the others, moe.ex:108-138) gives the same sums; this restatement runs the routed rows.
-    Expert products accumulate in f64."""
-    x = np.asarray(x, dtype=np.float32)
+    routing weights.
+
+    The arithmetic follows the input's type (`type = Nx.type(input)`, moe.ex:47):
+    - f32 input (numpy float32): expert products accumulate in f64, the sums in f64, one
+      rounding to f32 at the end (the f32 arithmetic the ORT fixtures pin);
+    - f16 input (numpy float16; or bf16 as uint16 bit patterns): as the reference computes it.
+      The dequantized expert weights are cast to the input type (moe.ex:53, 225-253). Each
+      expert product is one dot of input-type operands, accumulated exactly and rounded once
+      to the input type (Nx.dot of f16 x f16 is f16). Bias adds, every operation of the
+      activation, the routing weights (Nx.as_type(type), moe.ex:90) and each weighted output
+      (Nx.multiply, moe.ex:97) each round to the input type. The slot sum (Nx.sum, moe.ex:99)
+      adds exactly and rounds once.
+    How the reference's backend orders and rounds its dot and sum accumulations is not fixed by
+    Nx: with t*k >= E it sums over all E experts in expert order with weight 0 for the others
+    (moe.ex:108-138), otherwise over the k slots. Parity for f16 is therefore a tolerance."""
+    x, xt = floats(x)
     h = x.shape[-1]
-    x2 = x.reshape(-1, h)
+    x2 = x.reshape(-1, h).astype(np.float32)
     top_vals, top_idx = topk_stable(np.asarray(router, dtype=np.float32), k)
     weights = _softmax_last(top_vals)
+    narrow = xt in (F16, BF16)
+    wtype = xt if narrow else F32
 
     def expert(fc, scales, zp, e):  # expert e's {N, K} weights: dequant/6 on its slice
         def part(t):
             return None if t is None else np.asarray(t)[e:e + 1]
-        return qmoe_dequant(part(fc), part(scales), part(zp), bits, block_size)[0]
-    # Each expert's routed rows at once (the same per-row f64 dot products), then the slots of
-    # every token added in slot order.
+        return np.asarray(qmoe_dequant(part(fc), part(scales), part(zp), bits, block_size, wtype)[0], np.float64)
+
+    def rnd(v, *types):  # one operation's result in the merged type of its operands
+        return _narrow(v, merge_types(*types)).astype(np.float64) if narrow else np.asarray(v, np.float64)
+
+    def bias_row(b, e):
+        b, bt = floats(np.asarray(b)[e])
+        return b.astype(np.float64), bt
+
     n_tok = x2.shape[0]
     outs = np.zeros((n_tok, k, h), dtype=np.float64)
     for e in np.unique(top_idx):
         rows_t, rows_j = np.nonzero(top_idx == e)
         xe = x2[rows_t].astype(np.float64)
-        h1 = (xe @ expert(fc1, fc1_scales, fc1_zp, e).astype(np.float64).T).astype(np.float32)
+        h1 = rnd(xe @ expert(fc1, fc1_scales, fc1_zp, e).T, xt)
+        if not narrow:
+            h1 = h1.astype(np.float32)
         if fc1_bias is not None:
-            h1 = h1 + np.asarray(fc1_bias)[e]
+            b, bt = bias_row(fc1_bias, e)
+            h1 = rnd(h1 + b, xt, bt) if narrow else (h1 + b.astype(np.float32)).astype(np.float32)
         if activation == "swiglu" and swiglu_fusion == 0 and fc3 is not None:
-            h3 = (xe @ expert(fc3, fc3_scales, fc3_zp, e).astype(np.float64).T).astype(np.float32)
+            h3 = rnd(xe @ expert(fc3, fc3_scales, fc3_zp, e).T, xt)
+            if not narrow:
+                h3 = h3.astype(np.float32)
             if fc3_bias is not None:
-                h3 = h3 + np.asarray(fc3_bias)[e]
-            act = _swiglu_gate(h1, h3, alpha, beta, limit)
+                b, bt = bias_row(fc3_bias, e)
+                h3 = rnd(h3 + b, xt, bt) if narrow else (h3 + b.astype(np.float32)).astype(np.float32)
+            if narrow:
+                act = _narrow_activate(np.concatenate([h1, h3], axis=1), "swiglu", 2, alpha, beta, limit, xt)
+            else:
+                act = _swiglu_gate(h1, h3, alpha, beta, limit)
+        elif narrow:
+            act = _narrow_activate(h1, activation, swiglu_fusion, alpha, beta, limit, xt)
         else:
             act = _activate(h1, activation, swiglu_fusion, alpha, beta, limit)
-        o = act.astype(np.float64) @ expert(fc2, fc2_scales, fc2_zp, e).astype(np.float64).T
+        o = np.asarray(act, np.float64) @ expert(fc2, fc2_scales, fc2_zp, e).T
+        if narrow:
+            o = rnd(o, xt)
         if fc2_bias is not None:
-            o = o + np.asarray(fc2_bias)[e]
+            b, bt = bias_row(fc2_bias, e)
+            o = rnd(o + b, xt, bt) if narrow else o + b
         outs[rows_t, rows_j] = o
     out = np.zeros_like(x2, dtype=np.float64)
+    wts = rnd(weights, xt) if narrow else weights.astype(np.float64)
     for j in range(k):
-        wt = weights[:, j]
+        wt = wts[:, j]
         live = wt != 0
-        out[live] += wt[live, None] * outs[live, j]
-    return out.astype(np.float32).reshape(x.shape)
+        term = wt[live, None] * outs[live, j]
+        out[live] += rnd(term, xt) if narrow else term
+    return export(_narrow(out, xt), xt).reshape(x.shape) if narrow else out.astype(np.float32).reshape(x.shape)

@@ -48,6 +48,13 @@ def tensor(name: str, array: np.ndarray, external: tuple[str, int] | None = None
     return out + _int(14, 1)
 
 
+def tensor_raw(name: str, dims: list[int], data_type: int, raw: bytes) -> bytes:
+    """A TensorProto of any ONNX data type from its raw bytes (e.g. UINT4 = 21, INT4 = 22, two
+    values per byte, the lower element in the low nibble)."""
+    out = b"".join(_int(1, d) for d in dims) + _int(2, data_type) + _len(8, name.encode())
+    return out + _len(9, raw)
+
+
 def attribute_int(name: str, value: int) -> bytes:
     return _len(1, name.encode()) + _int(20, 2) + _int(3, value)
 

@@ -61,16 +61,22 @@ def test_gather_matches_oracle(ctx, case):
     assert np.array_equal(np.ascontiguousarray(got).view(np.uint8), np.ascontiguousarray(ref).view(np.uint8))
 
 
-def test_gather_vocab_table(ctx):
-    """The tied-embedding lookup of a 151936 x 1024 q4 table, block 32, f16 scales: ids over the
-    whole table, including its first and last rows."""
+@pytest.mark.parametrize("zp", [False, True], ids=["no_zp", "packed_zp"])
+def test_gather_vocab_table(ctx, zp):
+    """The tied-embedding lookup at its benchmark shape: a 151936 x 1024 q4 table, block 32, f16
+    scales, ids [8, 512] uniform over the whole table (its first and last rows included), with
+    and without packed zero points."""
+    print(f"gather vocab 151936x1024 ids [8,512] zp={zp}", flush=True)
     rng = np.random.default_rng(5)
     rows, d, bs = 151936, 1024, 32
     data = rng.integers(0, 256, (rows, d // 2), dtype=np.uint8)
     scales = _scales(rng, (rows, d // bs), "f16")
-    ids = np.concatenate([[0, rows - 1, -1], rng.integers(0, rows, 509)]).astype(np.int64).reshape(2, 256)
-    node = NodeProto(op_type="GatherBlockQuantized", input=["data", "ids", "scales"], output=["out"],
-                     attribute=[AttributeProto(name="bits", type=ATTR_INT, i=4)])
-    got = quantized.apply(node, [ctx.put(data), ctx.put(ids), ctx.put(scales)])[0].numpy()
-    ref = o.gather_block_quantized(data, ids, scales, bits=4)
+    zero = rng.integers(0, 256, (rows, d // bs // 2), dtype=np.uint8) if zp else None
+    ids = np.concatenate([[0, rows - 1, -1], rng.integers(0, rows, 8 * 512 - 3)]).astype(np.int64).reshape(8, 512)
+    node = NodeProto(op_type="GatherBlockQuantized", input=["data", "ids", "scales"] + (["zp"] if zp else []),
+                     output=["out"], attribute=[AttributeProto(name="bits", type=ATTR_INT, i=4)])
+    args = [ctx.put(data), ctx.put(ids), ctx.put(scales)] + ([ctx.put(zero)] if zp else [])
+    got = quantized.apply(node, args)[0].numpy()
+    ref = o.gather_block_quantized(data, ids, scales, zero, bits=4)
+    assert got.shape == (8, 512, d)
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))

@@ -92,9 +92,9 @@ def test_move_keeps_raw_values_that_other_nodes_read(ctx):
     assert "B" in moved.params and "scales" in moved.static and "zp" not in moved.static
 
 
-def nbits_node(a, b, scales, out, n, k=1024, zp=""):
+def nbits_node(a, b, scales, out, n, k=1024, zp="", bits=4):
     attrs = [AttributeProto(name="K", type=ATTR_INT, i=k), AttributeProto(name="N", type=ATTR_INT, i=n),
-             AttributeProto(name="bits", type=ATTR_INT, i=4), AttributeProto(name="block_size", type=ATTR_INT, i=32)]
+             AttributeProto(name="bits", type=ATTR_INT, i=bits), AttributeProto(name="block_size", type=ATTR_INT, i=32)]
     inputs = [a, b, scales] + ([zp] if zp else [])
     return NodeProto(input=inputs, output=[out], name=out, op_type="MatMulNBits", domain="com.microsoft",
                      attribute=attrs)
@@ -140,3 +140,74 @@ def test_concat_is_the_rows_of_its_parts(ctx, ns):
     y = matmul_nbits(a, merged).numpy()
     ys = np.concatenate([matmul_nbits(a, p).numpy() for p in parts], axis=1)
     assert np.array_equal(y, ys)
+
+
+def test_mixed_precision_matmuls_on_one_input_merge_by_layout(ctx):
+    """q and k of 4 bits and v of 8 bits read x (a mixed-precision export): the move merges q
+    and k and leaves v alone, since packed weights of different bit widths do not concatenate;
+    every output equals the graph's without the rewrite."""
+    print("move mixed 4/8-bit", flush=True)
+    rng = np.random.default_rng(12)
+    params, nodes = {}, []
+    for name, n, bits in (("q", 48, 4), ("k", 16, 4), ("v", 32, 8)):
+        params["b" + name] = rng.integers(0, 256, (n, 32, 32 * bits // 8), dtype=np.uint8)
+        params["s" + name] = (np.abs(rng.standard_normal(n * 32)) * 0.01 + 1e-3).astype(np.float32)
+        nodes.append(nbits_node("x", "b" + name, "s" + name, name, n, bits=bits))
+    model = Model(nodes=nodes, params=params, outputs=["q", "k", "v"])
+    inputs = {"x": ctx.put(rng.standard_normal((2, 1024)).astype(np.float32))}
+    expected = run_nodes(model, inputs)
+    moved = move(model, ctx)
+    assert [n.op_type for n in moved.nodes] == ["MatMulNBits", "Split", "MatMulNBits"]
+    assert moved.nodes[0].input == ["x", "bq:packed:merged", "", ""] and moved.nodes[2].input[1] == "bv:packed"
+    got = run_nodes(moved, inputs)
+    for name in ("q", "k", "v"):
+        assert np.array_equal(got[name].numpy(), expected[name].numpy()), name
+
+
+def test_more_matmuls_on_one_input_than_one_concat_takes(ctx):
+    """Ten MatMulNBits on one input merge in runs of at most eight parts."""
+    print("move 10 matmuls on one input", flush=True)
+    rng = np.random.default_rng(13)
+    params, nodes = {}, []
+    for i in range(10):
+        n = 16 + 8 * i
+        params[f"b{i}"] = rng.integers(0, 256, (n, 32, 16), dtype=np.uint8)
+        params[f"s{i}"] = (np.abs(rng.standard_normal(n * 32)) * 0.01 + 1e-3).astype(np.float32)
+        nodes.append(nbits_node("x", f"b{i}", f"s{i}", f"y{i}", n))
+    model = Model(nodes=nodes, params=params, outputs=[f"y{i}" for i in range(10)])
+    inputs = {"x": ctx.put(rng.standard_normal((3, 1024)).astype(np.float32))}
+    expected = run_nodes(model, inputs)
+    moved = move(model, ctx)
+    assert [n.op_type for n in moved.nodes] == ["MatMulNBits", "Split", "MatMulNBits", "Split"]
+    assert [len(n.output) for n in moved.nodes if n.op_type == "Split"] == [8, 2]
+    got = run_nodes(moved, inputs)
+    for name in expected:
+        assert np.array_equal(got[name].numpy(), expected[name].numpy()), name
+
+
+def test_bf16_scales_move_and_run(ctx):
+    """bf16 scales (BF16Host bit patterns) with bf16 activations: the moved weight dequantizes in
+    bf16 (the scales' type, no compute type), as the graph's does in A's type (quantized.ex:42),
+    and both agree with each other and with the oracle."""
+    from transmuter_amd.device import bf16_host
+
+    print("move bf16 scales", flush=True)
+    rng = np.random.default_rng(14)
+    n, k = 40, 1024
+    b = rng.integers(0, 256, (n, 32, 16), dtype=np.uint8)
+    s32 = (np.abs(rng.standard_normal(n * 32)) * 0.01 + 1e-3).astype(np.float32)
+    scales = bf16_host(o.bf16_round(s32))
+    model = Model(nodes=[nbits_node("x", "B", "scales", "Y", n)], params={"B": b, "scales": scales}, outputs=["Y"])
+    a32 = rng.standard_normal((2, k)).astype(np.float32)
+    a = ctx.put(o.bf16_round(a32), "bf16")
+    expected = run_nodes(model, {"x": a})["Y"]
+    moved = move(model, ctx)
+    weight = moved.params["B:packed"]
+    assert isinstance(weight, PackedWeight) and weight.dtype == "bf16"
+    got = run_nodes(moved, {"x": a})["Y"]
+    assert got.dtype == "bf16" and expected.dtype == "bf16"
+    assert np.array_equal(np.asarray(got.numpy()), np.asarray(expected.numpy()))
+    ref = o.bf16_to_f32(o.matmul_nbits(o.bf16_round(a32), b, np.asarray(scales), None, k=k, n=n, bits=4,
+                                       block_size=32)).astype(np.float64)  # bf16 A and weights: bf16 Y
+    y = o.bf16_to_f32(np.asarray(got.numpy())).astype(np.float64)
+    assert np.abs(y - ref).max() <= 2e-2 * np.abs(ref).max()

@@ -4,7 +4,7 @@ path (f32 A [1, 1024], q4 block 32 B [3072, 32, 16], f32 scales, no zero points;
 16}), the SmolLM3-3B prefill
 projections (q4, block 128, M in {256, 2048}), the 151936 x 1024 lm_head (M = 8) and the
 Qwen3-30B-A3B QMoE layer (128 experts, top-8, 2048/768, swiglu, 512 tokens). Outputs within
-max|Y - Y_ref| / max|Y_ref| <= 1e-2 (f16 activations); QMoE within 2e-2 * max|ref|; the
+max|Y - Y_ref| / max|Y_ref| <= 1e-2 (f16 activations); QMoE (f16) within 1e-2 * max|ref| of the oracle's f16 mode; the
 dequantized decode weights bit-exactly. Shapes and seeds are printed before each case."""
 
 import zlib
@@ -118,7 +118,7 @@ def test_qmoe_layer(ctx):
                                 _attr("activation_type", "swiglu"), _attr("swiglu_fusion", 0)])
     (y,) = moe.apply(node, [ctx.put(x), ctx.put(router), w1, s1, None, w2, s2, None, w3, s3, None, None, None, None])
     got = y.numpy().astype(np.float64)
-    ref = o.qmoe(x.astype(np.float32), router, w1, s1, w2, s2, k=k, bits=4, block_size=32, activation="swiglu",
+    ref = o.qmoe(x, router, w1, s1, w2, s2, k=k, bits=4, block_size=32, activation="swiglu",
                  swiglu_fusion=0, fc3=w3, fc3_scales=s3).astype(np.float64)
     scale = np.abs(ref).max()
-    assert np.abs(got - ref).max() <= 2e-2 * scale, f"max difference {np.abs(got - ref).max()} (max |ref| {scale})"
+    assert np.abs(got - ref).max() <= 1e-2 * scale, f"max difference {np.abs(got - ref).max()} (max |ref| {scale})"

@@ -2,6 +2,8 @@
 tiny inputs, invariants, and mutations of the oracle that those checks (or the fixtures)
 catch. A mutation is planted in a copy of the oracle on the CPU, never in the product."""
 
+import zlib
+
 import numpy as np
 import pytest
 
@@ -253,3 +255,85 @@ def test_mutation_missing_zero_shift_is_caught():
     b = f.initializers["b"]
     y = o.matmul_integer(a, b)  # zero points dropped
     assert not np.array_equal(y, f.outputs["y"])
+
+
+# ---------------------------------------------------------------- QMoE in f16
+
+
+def _qmoe_exact_case(k, router):
+    """Two experts of identity MLPs whose every value is exact in f16: 4-bit weights in 6..10
+    with per-row scale 0.5 and the default zero 8 give weights in {-1, -0.5, 0, 0.5, 1}; inputs
+    in {-1, 0, 1}. fc1 sums stay at most 16 (multiples of 0.5), fc2 sums at most 256 (multiples
+    of 0.25), and 0.5-weighted pairs of those multiples of 0.125 below 256: all exact in f16."""
+    rng = np.random.default_rng(11)
+    e, h, n1 = 2, 16, 16
+    q1 = rng.integers(6, 11, (e, n1, h))
+    q2 = rng.integers(6, 11, (e, h, n1))
+    x = rng.integers(-1, 2, (len(router), h)).astype(np.float16)
+    s1 = np.full((e, n1), 0.5, np.float16)
+    s2 = np.full((e, h), 0.5, np.float16)
+    y = o.qmoe(x, np.asarray(router, np.float32), pack(q1.reshape(e * n1, h), 4).reshape(e, n1, h // 2), s1,
+               pack(q2.reshape(e * h, n1), 4).reshape(e, h, n1 // 2), s2, k=k, bits=4, block_size=0,
+               activation="identity")
+    w1 = (q1 - 8) * 0.5
+    w2 = (q2 - 8) * 0.5
+    return x.astype(np.float64), w1, w2, y
+
+
+def test_qmoe_f16_closed_form_top1():
+    """k = 1: each token's output is its one expert's MLP, weight softmax([v]) = 1 exactly."""
+    router = [[1.0, 0.0], [0.0, 2.0], [-3.0, 5.0], [4.0, 4.0]]
+    x, w1, w2, y = _qmoe_exact_case(1, router)
+    assert y.dtype == np.float16
+    for t, row in enumerate(router):
+        e = int(np.argmax(row))  # stable: expert 0 for the tie of token 3
+        assert np.array_equal(y[t].astype(np.float64), (x[t] @ w1[e].T) @ w2[e].T)
+
+
+def test_qmoe_f16_closed_form_top2_ties():
+    """k = 2 of 2 with equal router values: weights 0.5 and 0.5, y = (mlp_0 + mlp_1) / 2."""
+    router = [[0.25, 0.25], [-1.0, -1.0], [3.0, 3.0]]
+    x, w1, w2, y = _qmoe_exact_case(2, router)
+    for t in range(len(router)):
+        want = 0.5 * ((x[t] @ w1[0].T) @ w2[0].T) + 0.5 * ((x[t] @ w1[1].T) @ w2[1].T)
+        assert np.array_equal(y[t].astype(np.float64), want)
+
+
+@pytest.mark.parametrize("act,fusion,fc3,bs", [("silu", 0, False, 32), ("swiglu", 0, True, 32),
+                                               ("swiglu", 2, False, 0), ("gelu", 0, False, 16)])
+def test_qmoe_f16_agrees_with_f32_within_f16_rounding(act, fusion, fc3, bs):
+    """The f16 mode rounds the weights, products, activation steps and weighted outputs to f16:
+    it must stay within 4 f16 ulps of the largest output (2^-11 relative each; about 1.5 are
+    seen) of the f32 mode on the same values, and the rounding must be visible."""
+    rng = np.random.default_rng(zlib.crc32(repr((act, fusion, fc3, bs)).encode()))
+    e, k, t, h, n1 = 8, 2, 12, 64, 32
+    inter = n1 if (act != "swiglu" or fc3) else n1 // 2
+
+    def weight(n, kk):
+        packed = rng.integers(0, 256, (e, n, kk // 2), dtype=np.uint8)
+        shape = (e, n, kk // bs) if bs else (e, n)
+        return packed, (np.abs(rng.standard_normal(shape)) * 0.02 + 1e-3).astype(np.float16)
+
+    w1, s1 = weight(n1, h)
+    w2, s2 = weight(h, inter)
+    w3, s3 = weight(n1, h) if fc3 else (None, None)
+    x = rng.standard_normal((t, h)).astype(np.float16)
+    router = rng.standard_normal((t, e)).astype(np.float32)
+    kw = dict(k=k, bits=4, block_size=bs, activation=act, swiglu_fusion=fusion, fc3=w3, fc3_scales=s3)
+    y16 = o.qmoe(x, router, w1, s1, w2, s2, **kw).astype(np.float64)
+    y32 = o.qmoe(x.astype(np.float32), router, w1, s1, w2, s2, **kw).astype(np.float64)
+    scale = np.abs(y32).max()
+    diff = np.abs(y16 - y32).max()
+    assert 0 < diff <= 4 * 2.0 ** -11 * scale, (diff, scale)
+
+
+def test_routing_ties_keep_the_lower_expert_first():
+    """`MoE.topk/2` (moe.ex:157-165): a stable descending sort, so among equal router values the
+    lower expert index comes first; +0 and -0 compare equal."""
+    probs = np.array([[0.5, 0.5, 0.5, 0.1],
+                      [0.0, -0.0, 0.0, -1.0],
+                      [-0.0, 0.0, 1.0, 1.0],
+                      [2.0, 3.0, 3.0, 2.0]], np.float32)
+    vals, idx = o.topk_stable(probs, 3)
+    assert idx.tolist() == [[0, 1, 2], [0, 1, 2], [2, 3, 0], [1, 2, 0]]
+    assert np.array_equal(np.take_along_axis(probs, idx, axis=1), vals)

@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "../../include/transmuter_hip.h"
 
@@ -16,6 +17,9 @@ struct tmh_ctx {
   int num_cus = 0;
   void* ws = nullptr;  // workspace of split-K partial sums, grown on demand outside capture
   size_t ws_bytes = 0;
+  // Workspaces replaced by a larger one. A graph captured earlier keeps their addresses in its
+  // kernel arguments, so they stay allocated until the context is destroyed.
+  std::vector<void*> ws_retired;
 };
 
 // Tiled device layout of a MatMulNBits weight.

@@ -776,6 +776,12 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
   if (fc1->K != H || fc2->N / E != H)
     return fail(ctx, TMH_ERR_INVALID, "QMoE fc1 [%lld, %lld] and fc2 rows %lld do not fit hidden size %lld", (long long)n1,
                 (long long)fc1->K, (long long)(fc2->N / E), (long long)H);
+  // The grouped products give each expert whole 16-row weight tiles, and the final sum reads
+  // eight columns per thread: rows per expert (fc1, fc3) and H must be multiples of 16, as
+  // tmh_weight_upload_qmoe makes them.
+  if (n1 % 16 || H % 16)
+    return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE needs multiples of 16 rows per expert; fc1 has %lld and fc2 %lld",
+                (long long)n1, (long long)H);
   const bool two = activation == ACT_SWIGLU && swiglu_fusion == 0 && fc3;
   if (two && (fc3->N != fc1->N || fc3->K != fc1->K)) return fail(ctx, TMH_ERR_INVALID, "QMoE fc3 must match fc1");
   const int64_t inter = activation == ACT_SWIGLU && !two ? n1 / 2 : n1;
@@ -847,8 +853,13 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
   ep.alpha = alpha;
   ep.beta = beta;
   ep.limit = limit;
+  // The fused swiglu product reads fc3's tiles with fc1's layout parameters (bits, parameter
+  // entries per chunk, zero point kind); fc3 of another layout runs as its own product.
+  const bool same_layout = !two || (fc3->bits == fc1->bits && fc3->nbc == fc1->nbc &&
+                                    fc3->block_size == fc1->block_size && fc3->zp_kind == fc1->zp_kind &&
+                                    fc3->nchunks == fc1->nchunks && fc3->ntiles == fc1->ntiles);
   const bool fused = moe_fast(fc1, x_dtype, d_x, ti, hi) && (!two || moe_fast(fc3, x_dtype, d_x, ti, hi)) &&
-                     (activation != ACT_SWIGLU || two || (swiglu_fusion == 2 && inter % 16 == 0));
+                     same_layout && (activation != ACT_SWIGLU || two || (swiglu_fusion == 2 && inter % 16 == 0));
   if (fused) {
     if (activation == ACT_SWIGLU) {
       ep.kind = EPI_GLU;

@@ -918,6 +918,7 @@ struct MatArgs {
   void* y;
   int y_dt, dot_dt;
   int64_t ldy;
+  float* ws = nullptr;  // split-K partial sums (splitk_bytes() of them), resolved by the entry point
 };
 
 int bsc_shift_of(const tmh_weight* w) {
@@ -1040,6 +1041,8 @@ struct GemmPlan {
   int bm, wn, splits, cps, ks = 1;
 };
 
+int cus_of(const tmh_ctx* ctx) { return ctx->num_cus > 0 ? ctx->num_cus : 256; }
+
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bits, int cus) {
   const double cw = 512.0 / bits;
   GemmPlan best{256, 2, 1, static_cast<int>(nchunks), 1};
@@ -1082,14 +1085,8 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
   const int mblocks = static_cast<int>((a.M + BM - 1) / BM);
   const int nblocks = static_cast<int>((w->ntiles + 4 * WN - 1) / (4 * WN));
   const int64_t tiles = static_cast<int64_t>(mblocks) * nblocks;
-  float* ws = nullptr;
-  if (splits > 1) {
-    ws = static_cast<float*>(workspace(ctx, static_cast<size_t>(splits) * a.M * w->N * sizeof(float), s));
-    if (!ws) {
-      splits = 1;
-      cps = static_cast<int>(w->nchunks);
-    }
-  }
+  // The entry point provides splitk_bytes() of partial sums whenever the plan splits K.
+  float* ws = splits > 1 ? a.ws : nullptr;
   const dim3 grid(static_cast<unsigned>(tiles * splits));
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS>),
@@ -1109,7 +1106,7 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
-  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, ctx->num_cus > 0 ? ctx->num_cus : 256);
+  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, cus_of(ctx));
   if (p.bm == 128 && p.ks == 2) {
     launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 128, 2>(ctx, w, a, s, p.splits, p.cps);
   } else if (p.bm == 128) {
@@ -1124,6 +1121,27 @@ void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStr
   }
 }
 
+// f16 A, f16 weights, no float zero points: the MFMA kernels (GEMV, LDS-tiled GEMM).
+bool fast_path(const tmh_weight* w, const MatArgs& a) {
+  return a.a_dt == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT;
+}
+
+// The LDS-tiled prefill GEMM applies (on the fast path): M > 64, 4 or 8 bits, aligned A, and
+// 32-bit buffer offsets over A (with a tile of rows past M) and the weights.
+bool gemm_lds_ok(const tmh_weight* w, const MatArgs& a) {
+  return a.M > 64 && w->bits != 2 && a.a_vec && (a.M + kGemmBM) * a.lda * 2 < (int64_t(1) << 31) &&
+         w->ntiles * w->nchunks * 1024 + 16 * w->nchunks * 1024 < (int64_t(1) << 31);
+}
+
+// Bytes of f32 partial sums one call needs: splits * M * N when the prefill GEMM's plan splits
+// K, else 0 (the GEMVs and unsplit GEMMs use no scratch memory).
+size_t splitk_bytes(const tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a) {
+  if (!fast_path(w, a) || !gemm_lds_ok(w, a)) return 0;
+  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, w->bits, cus_of(ctx));
+  return p.splits > 1 ? static_cast<size_t>(p.splits) * static_cast<size_t>(a.M) * static_cast<size_t>(w->N) * sizeof(float)
+                      : 0;
+}
+
 template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_fast_variant(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   if (a.M <= 16) {
@@ -1133,9 +1151,7 @@ void launch_fast_variant(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hi
   } else if (a.M <= 64 || BITS == 2) {
     launch_gemv<BITS, 4, HAS_ZP, SPLIT>(w, a, s, ctx->num_cus);
   } else if constexpr (BITS != 2) {
-    const bool fits = (a.M + kGemmBM) * a.lda * 2 < (int64_t(1) << 31) &&
-                      w->ntiles * w->nchunks * 1024 + 16 * w->nchunks * 1024 < (int64_t(1) << 31);
-    if (a.a_vec && fits)
+    if (gemm_lds_ok(w, a))
       launch_gemm_lds<BITS, HAS_ZP, SPLIT>(ctx, w, a, s);
     else
       launch_gemm<BITS, HAS_ZP, SPLIT>(w, a, s);
@@ -1519,9 +1535,15 @@ int tmh_dequantize_nbits(tmh_ctx* ctx, const tmh_weight* w, void* d_out, int out
   return check_launch(ctx, "k_dequant");
 }
 
-int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
-                     int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype,
-                     int64_t ldy, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Validates a MatMulNBits call and fills its arguments; *run is false when there is nothing to do.
+int prepare_matmul(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M, int64_t lda,
+                   const void* d_bias, int bias_dtype, void* d_y, int y_dtype, int64_t ldy, MatArgs* out,
+                   bool* run) {
+  *run = false;
   TMH_TRY(use_device(ctx));
   if (!w) return fail(ctx, TMH_ERR_INVALID, "the weight is NULL");
   if (w->device != ctx->device) return fail(ctx, TMH_ERR_INVALID, "the weight lives on device %d, the context on %d", w->device, ctx->device);
@@ -1540,12 +1562,16 @@ int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_d
   if (M == 0) return TMH_OK;
   if (!d_a || !d_y) return fail(ctx, TMH_ERR_INVALID, "A and Y must not be NULL");
   if (M > (int64_t(1) << 31) / 2) return fail(ctx, TMH_ERR_INVALID, "M is too large");
-  hipStream_t s = pick_stream(ctx, stream);
-  MatArgs a{d_a, a_dtype, M, lda,
-            (reinterpret_cast<uintptr_t>(d_a) % 16 == 0) && (lda % 8 == 0) && (w->K % 8 == 0),
-            d_bias, bias_dtype, d_y, y_dtype, dot_dt, ldy};
-  const bool fast = a_dtype == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT;
-  if (fast) {
+  *out = MatArgs{d_a, a_dtype, M, lda,
+                 (reinterpret_cast<uintptr_t>(d_a) % 16 == 0) && (lda % 8 == 0) && (w->K % 8 == 0),
+                 d_bias, bias_dtype, d_y, y_dtype, dot_dt, ldy};
+  *run = true;
+  return TMH_OK;
+}
+
+// Launches a prepared MatMulNBits call (its split-K partial sums, if any, in a.ws).
+int launch_matmul(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  if (fast_path(w, a)) {
     switch (w->bits) {
       case 2: launch_fast_bits<2>(ctx, w, a, s); break;
       case 4: launch_fast_bits<4>(ctx, w, a, s); break;
@@ -1559,6 +1585,33 @@ int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_d
     default: launch_general_bits<8>(w, a, s);
   }
   return check_launch(ctx, "k_matmul_general");
+}
+
+}  // namespace
+
+extern "C" {
+
+int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
+                     int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype,
+                     int64_t ldy, void* stream) {
+  MatArgs a{};
+  bool run = false;
+  TMH_TRY(prepare_matmul(ctx, w, d_a, a_dtype, M, lda, d_bias, bias_dtype, d_y, y_dtype, ldy, &a, &run));
+  if (!run) return TMH_OK;
+  hipStream_t s = pick_stream(ctx, stream);
+  if (const size_t need = splitk_bytes(ctx, w, a)) {
+    // A graph must replay what an eager call computes, so a call that splits K never runs
+    // unsplit instead: without the workspace (it cannot grow while the stream is captured)
+    // the call fails.
+    a.ws = static_cast<float*>(workspace(ctx, need, s));
+    if (!a.ws)
+      return fail(ctx, TMH_ERR_UNSUPPORTED,
+                  "MatMulNBits with M=%lld, N=%lld, K=%lld splits K and needs a %zu-byte workspace, which cannot "
+                  "be allocated now (not while the stream is being captured into a graph): run the call once "
+                  "before capture",
+                  (long long)M, (long long)w->N, (long long)w->K, need);
+  }
+  return launch_matmul(ctx, w, a, s);
 }
 
 }  // extern "C"

@@ -68,24 +68,22 @@ void* workspace(tmh_ctx* ctx, size_t bytes, hipStream_t stream) {
     (void)hipGetLastError();
     return nullptr;
   }
-  // The old workspace may still be read by queued work: wait for the device before freeing it.
-  if (ctx->ws) {
-    if (hipDeviceSynchronize() != hipSuccess || hipFree(ctx->ws) != hipSuccess) {
+  // The old workspace is not freed: queued work and graphs captured earlier may still use it.
+  // It is retired until tmh_ctx_destroy, and the new one at least doubles, so the retired
+  // buffers together stay below the size of the current one.
+  size_t size = std::max(bytes, 2 * ctx->ws_bytes);
+  void* p = nullptr;
+  if (hipMalloc(&p, size) != hipSuccess) {
+    (void)hipGetLastError();
+    size = bytes;
+    if (hipMalloc(&p, size) != hipSuccess) {
       (void)hipGetLastError();
-      ctx->ws = nullptr;
-      ctx->ws_bytes = 0;
       return nullptr;
     }
-    ctx->ws = nullptr;
-    ctx->ws_bytes = 0;
   }
-  void* p = nullptr;
-  if (hipMalloc(&p, bytes) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
+  if (ctx->ws) ctx->ws_retired.push_back(ctx->ws);
   ctx->ws = p;
-  ctx->ws_bytes = bytes;
+  ctx->ws_bytes = size;
   return p;
 }
 
@@ -173,6 +171,7 @@ void tmh_ctx_destroy(tmh_ctx* ctx) {
     (void)hipStreamDestroy(ctx->stream);
   }
   if (ctx->ws) (void)hipFree(ctx->ws);
+  for (void* p : ctx->ws_retired) (void)hipFree(p);
   delete ctx;
 }
 

@@ -1,7 +1,7 @@
 """Device context and device-resident tensors over the C ABI of libtmhip.
 
 Types are named as Nx names them ("f32", "f16", "bf16", "u8", "s8", "s32", "s64", ...). bf16
-host arrays are uint16 bit patterns.
+host arrays are uint16 bit patterns in a `BF16Host` array, which `nx_type` names "bf16".
 """
 
 from __future__ import annotations
@@ -33,7 +33,53 @@ NUMPY_TO_NX = {
 FLOAT_TYPES = ("f32", "f16", "bf16")
 
 
+class BF16Host(np.ndarray):
+    """A host array of bfloat16 values held as their uint16 bit patterns (numpy has no bfloat16
+    type). Its views and slices keep the type; `nx_type` names it "bf16" where a plain uint16
+    array is "u16"."""
+
+
+def bf16_host(bits) -> BF16Host:
+    """uint16 bit patterns as a BF16Host array (a view when `bits` already is uint16)."""
+    return np.asarray(bits, dtype=np.uint16).view(BF16Host)
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """f32 values rounded to bfloat16 (to nearest, ties to even; NaN stays a quiet NaN)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    out = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    out[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return out
+
+
+def bf16_bits_to_f32(bits) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def float_values(array) -> np.ndarray:
+    """The f32 values of a float host array (f16, f32, or bf16 bit patterns)."""
+    if isinstance(array, BF16Host):
+        return bf16_bits_to_f32(array)
+    return np.asarray(array, dtype=np.float32)
+
+
+def cast_float(array, dtype: str) -> np.ndarray:
+    """A float host array in another float type ("f32", "f16" or "bf16"), each value rounded
+    once from its exact f32 value, as Nx.as_type/2 does."""
+    values = float_values(array)
+    if dtype == "f32":
+        return values
+    if dtype == "f16":
+        return values.astype(np.float16)
+    if dtype == "bf16":
+        return bf16_host(f32_to_bf16_bits(values))
+    raise ValueError(f"{dtype} is not a float type")
+
+
 def nx_type(array: np.ndarray) -> str:
+    if isinstance(array, BF16Host):
+        return "bf16"
     try:
         return NUMPY_TO_NX[np.asarray(array).dtype]
     except KeyError:
@@ -79,8 +125,8 @@ class Context:
         tensor keeps the array's shape, rank 0 included (np.ascontiguousarray alone makes a 0-d
         array 1-d)."""
         shape = np.shape(array)
+        dtype = dtype or nx_type(array)
         host = np.ascontiguousarray(array)
-        dtype = dtype or nx_type(host)
         t = self.empty(shape, dtype)
         if t.nbytes:
             self.check(lib().tmh_upload(self.handle, t.ptr, host.ctypes.data_as(ctypes.c_void_p), t.nbytes))
@@ -122,11 +168,12 @@ class DeviceTensor:
         return NX_TO_TMH[self.dtype]
 
     def numpy(self) -> np.ndarray:
+        """A host copy (bf16 as a BF16Host array of bit patterns)."""
         host = np.empty(self.shape, dtype=NX_TO_NUMPY[self.dtype])
         if self.nbytes:
             self.ctx.check(lib().tmh_download(self.ctx.handle, host.ctypes.data_as(ctypes.c_void_p),
                                               self.ptr, self.nbytes))
-        return host
+        return bf16_host(host) if self.dtype == "bf16" else host
 
     def reshape(self, shape) -> "DeviceTensor":
         """A view with another shape over the same buffer (the view does not own it)."""

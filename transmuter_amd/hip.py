@@ -20,7 +20,7 @@ from dataclasses import dataclass, field, replace
 
 import numpy as np
 
-from .device import Context, DeviceTensor
+from .device import FLOAT_TYPES, Context, DeviceTensor, cast_float, nx_type
 from .packed import PackedWeight
 from .quantized import nbits_sizes
 
@@ -56,15 +56,18 @@ def _host_value(value):
 
 
 def upcast(value, compute_type: str | None):
-    """`Transmuter.upcast/2` (lib/transmuter.ex:1323-1327): f16 and bf16 values take the
-    compute type; other values stay as they are. Returns (value, type)."""
+    """`Transmuter.upcast/2` (lib/transmuter.ex:1323-1324): f16 and bf16 values take the
+    compute type (Nx.as_type/2, one rounding from the exact value); other values stay as they
+    are. Returns (value, its float type or None)."""
     if value is None:
         return None, None
-    arr = np.asarray(value)
-    dtype = "f16" if arr.dtype == np.float16 else ("f32" if arr.dtype == np.float32 else None)
+    try:
+        dtype = nx_type(value)
+    except TypeError:
+        dtype = None
     if compute_type and dtype in ("f16", "bf16") and compute_type != dtype:
-        return arr.astype(np.float32), "f32"
-    return arr, dtype
+        return cast_float(value, compute_type), compute_type
+    return value, dtype if dtype in FLOAT_TYPES else None
 
 
 def compatible(node) -> bool:
@@ -166,10 +169,10 @@ def _to_device(value, ctx: Context, compute_type: str | None):
     file; a host array is uploaded, f16/bf16 taking the compute type first."""
     if isinstance(value, (PackedWeight, DeviceTensor)):
         return value
-    if _deferred(value) and not (compute_type and np.dtype(value.dtype) == np.float16):
+    if _deferred(value) and not (compute_type and value.nx_dtype in ("f16", "bf16")):
         return value.to_device(ctx)
-    arr, dtype = upcast(_host_value(value), compute_type)
-    return ctx.put(np.ascontiguousarray(arr))
+    arr, _dtype = upcast(_host_value(value), compute_type)
+    return ctx.put(arr)
 
 
 # ---------------------------------------------------------------- merged matmuls
@@ -202,11 +205,19 @@ def merge_matmuls(model: Model) -> Model:
     for node in model.nodes:
         if _mergeable(node, model, uses):
             weight = model.params[node.input[1]]
-            key = (node.op_type, node.input[0], weight.dtype, weight.k)
+            # The reference's merge key is (op_type, A, type, K) (fusion.ex:467-488); packed
+            # weights concatenate only when they also share bits, block size and zero point
+            # kind, so a mixed-precision group (an 8-bit v_proj beside 4-bit q/k) splits by
+            # layout. Each merged part still computes exactly what its own node did.
+            key = (node.op_type, node.input[0], weight.dtype, weight.k, weight.bits, weight.block_size,
+                   weight.zp_kind)
             groups.setdefault(key, []).append(node)
+    # tmh_weight_concat_nbits takes at most MAX_CONCAT parts: larger groups merge in runs.
+    runs = [group[i:i + PackedWeight.MAX_CONCAT] for group in groups.values()
+            for i in range(0, len(group), PackedWeight.MAX_CONCAT)]
     params = dict(model.params)
     replacements = {}
-    for group in groups.values():
+    for group in runs:
         if len(group) < 2:
             continue
         first = group[0]

@@ -50,11 +50,15 @@ class DeferredTensor:
         """The tensor, as a read-only memory map of the file (DeferredTensor.value/1)."""
         return onnx_wire.tensor_view(self.proto, self.directory)
 
+    @property
+    def nx_dtype(self) -> str:
+        """The tensor's Nx type ("bf16" for bfloat16 initializers, held as uint16 bits)."""
+        return "bf16" if self.proto.data_type == onnx_wire.BFLOAT16 else nx_type(np.zeros(0, self.dtype))
+
     def to_device(self, ctx: Context) -> DeviceTensor:
         """The tensor on the device, copied from the file without a host copy."""
         path, offset, _length = onnx_wire.external_location(self.proto, self.directory)
-        dtype = "bf16" if self.proto.data_type == onnx_wire.BFLOAT16 else nx_type(np.zeros(0, self.dtype))
-        return ctx.put_file(path, offset, self.shape, dtype)
+        return ctx.put_file(path, offset, self.shape, self.nx_dtype)
 
 
 def static_initializer(shape: tuple, dtype: np.dtype, trainable: bool = False) -> bool:
@@ -80,7 +84,7 @@ def load(path: str, ctx: Context | None = None, compute_type: str | None = None,
         if value is None:
             value = onnx_wire.tensor_view(t, directory)
         if static_initializer(value.shape, value.dtype, trainable):
-            static[t.name] = upcast(np.array(value), compute_type)[0]
+            static[t.name] = upcast(_host_copy(value), compute_type)[0]
         else:
             params[t.name] = value
     initializers = {t.name for t in graph.initializer}
@@ -88,5 +92,12 @@ def load(path: str, ctx: Context | None = None, compute_type: str | None = None,
                   compute_type=compute_type, inputs=[i for i in graph.input if i not in initializers])
     if ctx is not None:
         return move(model, ctx)
-    model.params = {name: upcast(np.asarray(v), compute_type)[0] for name, v in params.items()}
+    model.params = {name: upcast(v, compute_type)[0] for name, v in params.items()}
     return model
+
+
+def _host_copy(value) -> np.ndarray:
+    """An in-memory copy of an initializer (of its file mapping), keeping a bf16 tag."""
+    if isinstance(value, DeferredTensor):
+        value = value.value()
+    return np.array(value, subok=True)

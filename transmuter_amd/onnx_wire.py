@@ -20,6 +20,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
+from .device import bf16_host
+
 # ONNX TensorProto.DataType -> numpy dtype (lib/transmuter/ops.ex:700-713).
 ONNX_DTYPES = {
     1: np.float32,
@@ -306,8 +308,8 @@ def tensor(t: TensorProto, directory: str | None = None) -> np.ndarray:
     """The value of an initializer, as `Ops.tensor/2` gives it (lib/transmuter/ops.ex:597-670).
 
     uint4/int4 tensors stay packed: the last axis holds ceil(last/2) bytes, u8 for uint4 and s8
-    for int4 (ops.ex:632-639). bfloat16 data returns as a uint16 array of the raw bits, with
-    `.dtype` uint16; callers that compute read it with `bf16_to_f32`.
+    for int4 (ops.ex:632-639). bfloat16 data returns as a BF16Host array of the raw bits
+    (uint16 elements that nx_type names "bf16"); callers that compute read it with `bf16_to_f32`.
     """
     if t.data_location == 1:
         t = _read_external(t, directory)
@@ -323,7 +325,7 @@ def tensor(t: TensorProto, directory: str | None = None) -> np.ndarray:
             flat = np.frombuffer(t.raw_data, dtype=np.uint16)
         else:
             flat = np.asarray(t.int32_data, dtype=np.uint16)
-        return flat.reshape(dims).copy()
+        return bf16_host(flat.reshape(dims).copy())
     if t.data_type not in ONNX_DTYPES:
         raise ValueError(f"ONNX type {t.data_type} has no array type here")
     dtype = ONNX_DTYPES[t.data_type]
@@ -382,10 +384,12 @@ def tensor_view(t: TensorProto, directory: str | None = None) -> np.ndarray:
         shape, dtype = st
         if length != int(np.prod(shape, dtype=np.int64)) * dtype.itemsize:
             raise ValueError(f"tensor {t.name}: {length} bytes in {path} do not hold {shape} {dtype}")
-        return np.memmap(path, dtype=dtype, mode="r", offset=offset, shape=shape)
+        view = np.memmap(path, dtype=dtype, mode="r", offset=offset, shape=shape)
+        return bf16_host(view) if t.data_type == BFLOAT16 else view
     if st is not None and len(t.raw_data):
         shape, dtype = st
-        return np.frombuffer(t.raw_data, dtype=dtype).reshape(shape)
+        view = np.frombuffer(t.raw_data, dtype=dtype).reshape(shape)
+        return bf16_host(view) if t.data_type == BFLOAT16 else view
     return tensor(t, directory)
 
 

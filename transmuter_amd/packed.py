@@ -24,19 +24,21 @@ def _host(x, name: str):
         return None, None
     if isinstance(x, DeviceTensor):
         return np.ascontiguousarray(x.numpy()), x.dtype
-    arr = np.ascontiguousarray(x)
-    return arr, nx_type(arr)
+    return np.ascontiguousarray(x), nx_type(x)
 
 
 class PackedWeight:
     """One MatMulNBits weight on the device, in the library's tiled layout."""
 
+    MAX_CONCAT = 8  # parts tmh_weight_concat_nbits takes at once
+
     def __init__(self, ctx: Context, handle: ctypes.c_void_p, k: int, n: int, bits: int, block_size: int,
-                 dtype: str):
+                 dtype: str, zp_kind: int = _lib.ZP_NONE):
         self.ctx = ctx
         self.handle = handle
         self.k, self.n, self.bits, self.block_size = k, n, bits, block_size
         self.dtype = dtype  # the type the weights dequantize in
+        self.zp_kind = zp_kind  # ZP_NONE, ZP_PACKED or ZP_FLOAT
 
     @property
     def shape(self) -> tuple[int, int]:
@@ -48,7 +50,8 @@ class PackedWeight:
                ) -> "PackedWeight":
         """Packs B [N, blocks, block_size*bits/8] (u8), scales [N*blocks] and zero points (none,
         packed u8 rows, or floats) into a device weight whose values dequantize in weight_dtype.
-        bf16 host arrays are uint16 bit patterns and need scales_dtype / zero_points_dtype."""
+        bf16 host values come as BF16Host arrays; plain uint16 bit patterns need scales_dtype /
+        zero_points_dtype."""
         if weight_dtype not in FLOAT_TYPES:
             raise ValueError(f"weight type must be one of {FLOAT_TYPES}, got {weight_dtype}")
         hb, bdt = _host(b, "B")
@@ -70,7 +73,7 @@ class PackedWeight:
             hz.size if hz is not None else 0, k, n, bits, block_size, NX_TO_TMH[weight_dtype],
             ctypes.byref(handle))
         ctx.check(status)
-        return cls(ctx, handle, k, n, bits, block_size, weight_dtype)
+        return cls(ctx, handle, k, n, bits, block_size, weight_dtype, zp_kind)
 
     @classmethod
     def concat(cls, parts: list["PackedWeight"]) -> "PackedWeight":
@@ -83,7 +86,7 @@ class PackedWeight:
         handle = ctypes.c_void_p()
         ctx.check(lib().tmh_weight_concat_nbits(ctx.handle, handles, len(parts), ctypes.byref(handle)))
         p0 = parts[0]
-        return cls(ctx, handle, p0.k, sum(p.n for p in parts), p0.bits, p0.block_size, p0.dtype)
+        return cls(ctx, handle, p0.k, sum(p.n for p in parts), p0.bits, p0.block_size, p0.dtype, p0.zp_kind)
 
     def device_bytes(self) -> int:
         size = ctypes.c_size_t()
