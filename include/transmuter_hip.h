@@ -205,6 +205,21 @@ int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_d
                      int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype,
                      int64_t ldy, void* stream);
 
+/*
+ * tmh_matmul_nbits for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. Same arguments, checks and results (the same kernels and plan, bit for bit), but a
+ * prefill GEMM whose plan splits K keeps its f32 partial sums in a fixed 64 MiB scratch area per
+ * device (set up by tmh_ctx_create) instead of the context's workspace, and the call neither
+ * allocates nor frees. A call whose partial sums exceed 64 MiB fails with TMH_ERR_INVALID (the
+ * message gives the size). Every call on one device shares that device's scratch, which keeps
+ * the last call's partial sums: calls on one device that overlap in time (other streams, other
+ * contexts, other threads) race and must be serialized by the caller.
+ */
+int tmh_matmul_nbits_noalloc(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
+                             int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype,
+                             int64_t ldy, void* stream);
+
 /* ------------------------------------------------------------------ GatherBlockQuantized */
 
 /*

@@ -62,6 +62,7 @@ SIGNATURES = {
                              ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_sz)]),
     "tmh_dequantize_nbits": (_i, [_vp, _vp, _vp, _i, _vp]),
     "tmh_matmul_nbits": (_i, [_vp, _vp, _vp, _i, _i64, _i64, _vp, _i, _vp, _i, _i64, _vp]),
+    "tmh_matmul_nbits_noalloc": (_i, [_vp, _vp, _vp, _i, _i64, _i64, _vp, _i, _vp, _i, _i64, _vp]),
     "tmh_gather_block_quantized": (_i, [_vp, _vp, _i, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i, _i,
                                         _vp, _vp]),
     "tmh_dequantize_linear": (_i, [_vp, _vp, _i, _i64, _i64, _i64, _vp, _i, _vp, _i, _i, _i64, _vp, _vp]),

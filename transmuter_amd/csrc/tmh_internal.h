@@ -92,6 +92,10 @@ float bf16_to_f32(uint16_t h);
 uint16_t f32_to_bf16(float f);
 float load_float(const void* p, int dt, size_t i);  // host read of a float array element
 
+// Looks up, once per device and with that device current, the device address of the scratch
+// memory tmh_matmul_nbits_noalloc uses (a failure is reported by that call).
+void noalloc_scratch_init(int device);
+
 }  // namespace tmh
 
 #define TMH_TRY(expr)          \

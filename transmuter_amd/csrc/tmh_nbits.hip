@@ -16,6 +16,7 @@
 //   k_matmul_general  any float types and float zero points, f32 FMA on the vector ALUs
 #include <algorithm>
 #include <cstdio>
+#include <mutex>
 #include <type_traits>
 #include <cstdlib>
 #include <vector>
@@ -24,6 +25,14 @@
 #include "tmh_internal.h"
 
 using namespace tmh;
+
+// Scratch memory of tmh_matmul_nbits_noalloc: the split-K partial sums of its prefill GEMMs,
+// for callers that cannot allocate (graph capture, serving loops). Each device the library
+// runs on holds its own copy until the process ends. In host code `scratch` names a host-side
+// stand-in, not device memory: kernels get the address that hipGetSymbolAddress gives for
+// each device (noalloc_scratch_init).
+constexpr size_t kNoallocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) float scratch[kNoallocScratchBytes / sizeof(float)];
 
 namespace {
 
@@ -1539,6 +1548,13 @@ int tmh_dequantize_nbits(tmh_ctx* ctx, const tmh_weight* w, void* d_out, int out
 
 namespace {
 
+// The device address of `scratch` per device, looked up once per device with that device
+// current (tmh_ctx_create calls noalloc_scratch_init), or the error of the lookup.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
+hipError_t g_scratch_err[kMaxDevices] = {};
+
 // Validates a MatMulNBits call and fills its arguments; *run is false when there is nothing to do.
 int prepare_matmul(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M, int64_t lda,
                    const void* d_bias, int bias_dtype, void* d_y, int y_dtype, int64_t ldy, MatArgs* out,
@@ -1589,6 +1605,25 @@ int launch_matmul(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream
 
 }  // namespace
 
+namespace tmh {
+
+void noalloc_scratch_init(int device) {
+  if (device < 0 || device >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[device]) return;
+  void* p = nullptr;
+  const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    g_scratch_err[device] = err;
+    return;
+  }
+  g_scratch[device] = static_cast<float*>(p);
+  g_scratch_err[device] = hipSuccess;
+}
+
+}  // namespace tmh
+
 extern "C" {
 
 int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
@@ -1612,6 +1647,32 @@ int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_d
                   (long long)M, (long long)w->N, (long long)w->K, need);
   }
   return launch_matmul(ctx, w, a, s);
+}
+
+int tmh_matmul_nbits_noalloc(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
+                             int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype, int64_t ldy,
+                             void* stream) {
+  MatArgs a{};
+  bool run = false;
+  TMH_TRY(prepare_matmul(ctx, w, d_a, a_dtype, M, lda, d_bias, bias_dtype, d_y, y_dtype, ldy, &a, &run));
+  if (!run) return TMH_OK;
+  if (const size_t need = splitk_bytes(ctx, w, a)) {
+    if (need > kNoallocScratchBytes)
+      return fail(ctx, TMH_ERR_INVALID,
+                  "MatMulNBits with M=%lld, N=%lld, K=%lld splits K into %zu bytes of partial sums; "
+                  "tmh_matmul_nbits_noalloc holds at most %zu bytes (use tmh_matmul_nbits)",
+                  (long long)M, (long long)w->N, (long long)w->K, need, kNoallocScratchBytes);
+    float* p = nullptr;
+    hipError_t err = hipErrorInvalidDevice;
+    if (ctx->device >= 0 && ctx->device < kMaxDevices) {
+      std::lock_guard<std::mutex> lock(g_scratch_mu);
+      p = g_scratch[ctx->device];
+      err = g_scratch_err[ctx->device];
+    }
+    if (!p) return check_hip(ctx, err == hipSuccess ? hipErrorInvalidDevice : err, "the scratch memory of tmh_matmul_nbits_noalloc");
+    a.ws = p;
+  }
+  return launch_matmul(ctx, w, a, pick_stream(ctx, stream));
 }
 
 }  // extern "C"

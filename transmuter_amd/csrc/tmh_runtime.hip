@@ -151,6 +151,7 @@ int tmh_ctx_create(int device, tmh_ctx** out) {
                 device, prop.gcnArchName);
   err = hipSetDevice(device);
   if (err != hipSuccess) return check_hip(nullptr, err, "hipSetDevice");
+  noalloc_scratch_init(device);
   tmh_ctx* ctx = new tmh_ctx();
   ctx->device = device;
   ctx->num_cus = prop.multiProcessorCount;
