@@ -144,7 +144,8 @@ def decode_sweep(ctx, steps, warmup, sets, ms, merged=False, full_step=False):
     reference's move/2 + Fusion.matmuls/2 leave a Qwen3 layer (4 calls instead of 7).
     full_step: also time a whole decode step, the 196 layer GEMVs and the 151936 x 1024
     lm_head in one graph, and the host-observed latency of one eagerly launched 1024 -> 3072
-    GEMV (launch and synchronize)."""
+    GEMV (launch and synchronize); at M=1 also the floors (an empty kernel per projection, a
+    plain read of each projection's packed weights) and the step launched eagerly."""
     from transmuter_amd import PackedWeight
 
     rng = np.random.default_rng(20260101)
@@ -194,6 +195,9 @@ def decode_sweep(ctx, steps, warmup, sets, ms, merged=False, full_step=False):
             f"{results[m]['us_per_launch']:.2f} us/launch")
         for g in graphs:
             g.destroy()
+        if full_step and m == 1:
+            results[m].update(decode_floors(ctx, steps, warmup, weights, lambda s: [
+                matmul_call(ctx, w, a[w.k], y[w.n], m) for layer in range(QWEN3_LAYERS) for w in weights[s][layer]]))
         if full_step:
             results[m].update(full_decode_step(ctx, steps, warmup, weights, a, y, m))
     for ls in weights:
@@ -201,6 +205,41 @@ def decode_sweep(ctx, steps, warmup, sets, ms, merged=False, full_step=False):
             for w in layer:
                 w.free()
     return results
+
+
+def decode_floors(ctx, steps, warmup, weights, eager_step):
+    """What one launch per projection costs without the GEMV's work, in graphs of the same 196
+    launches rotating over the same weight copies: an empty kernel (the launch floor) and a plain
+    read of each projection's packed weights with the GEMV's load pattern (the read floor). Also
+    the decode step's 196 GEMVs launched eagerly, back to back, with one synchronize at the end."""
+    from transmuter_amd._lib import lib
+
+    per_step = QWEN3_LAYERS * len(weights[0][0])
+    empty = [Graph(ctx, lambda: [ctx.check(lib().tmh_floor_empty(ctx.handle, 256, None)) for _ in range(per_step)])]
+    launch_us = time_graphs(ctx, empty, steps, warmup) * 1e3 / (steps * per_step)
+    empty[0].destroy()
+    sink = ctx.empty((16,), "u8")
+    reads = [Graph(ctx, lambda s=s: [ctx.check(lib().tmh_floor_read(ctx.handle, w.handle, sink.ptr, None))
+                                     for layer in range(QWEN3_LAYERS) for w in weights[s][layer]])
+             for s in range(len(weights))]
+    read_us = time_graphs(ctx, reads, steps, warmup) * 1e3 / (steps * per_step)
+    for g in reads:
+        g.destroy()
+    q_bytes = QWEN3_LAYERS * sum(-(-w.n // 16) * -(-(w.k * w.bits // 8) // 64) * 1024 for w in weights[0][0])
+    for i in range(warmup):
+        eager_step(i % len(weights))
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        eager_step(i % len(weights))
+    ctx.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+    log(f"decode floors: empty kernel {launch_us:.2f} us/launch, plain read of the packed weights {read_us:.2f} "
+        f"us/launch ({q_bytes / (read_us * per_step * 1e-6) / 1e9:.0f} GB/s); eager step {eager_ms * 1e3:.0f} us "
+        f"({1e3 / eager_ms:.0f} tokens/s)")
+    return {"launch_floor_us": launch_us, "read_floor_us": read_us,
+            "read_floor_gbs": q_bytes / (read_us * per_step * 1e-6) / 1e9,
+            "eager_ms_per_step": eager_ms, "eager_tokens_per_s": 1e3 / eager_ms}
 
 
 def full_decode_step(ctx, steps, warmup, weights, a, y, m, vocab=151936, hidden=1024):
@@ -239,6 +278,37 @@ def full_decode_step(ctx, steps, warmup, weights, a, y, m, vocab=151936, hidden=
         f"one eager 1024->3072 GEMV, launch to synchronize: {single_us:.1f} us")
     return {"ms_per_step_with_lm_head": ms_step, "tokens_per_s_with_lm_head": m * 1e3 / ms_step,
             "single_launch_us": single_us}
+
+
+# ---------------------------------------------------------------- single op (the CPU-path config)
+
+
+def single_op(ctx, reps, copies=160):
+    """The single MatMulNBits op of the reference's EXLA-CPU configuration: A f32 [1, 1024],
+    B [3072, 32, 16] of uniform nibbles, f32 scales |N(0,1)|*0.01+1e-4, no zero points, Y f32
+    [1, 3072]. Weights dequantize in the scales' type (f32), as move/2 leaves them. One graph of
+    `copies` calls over distinct weight copies (304 MB, more than the 256 MB last-level cache)."""
+    from transmuter_amd import PackedWeight
+    from transmuter_amd._lib import F32, lib
+
+    rng = np.random.default_rng(1)
+    k, n = 1024, 3072
+    ws = []
+    for _ in range(copies):
+        b = rng.integers(0, 256, (n, k // 32, 16), dtype=np.uint8)
+        sc = (np.abs(rng.standard_normal(n * k // 32, dtype=np.float32)) * 0.01 + 1e-4).astype(np.float32)
+        ws.append(PackedWeight.upload(ctx, b, sc, None, k=k, n=n, bits=4, block_size=32, weight_dtype="f32"))
+    a = ctx.put(rng.standard_normal((1, k), dtype=np.float32))
+    y = ctx.empty((1, n), "f32")
+    g = Graph(ctx, lambda: [ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, a.ptr, F32, 1, k, None, 0, y.ptr,
+                                                             F32, n, None)) for w in ws])
+    us = time_graphs(ctx, [g], reps, 2) * 1e3 / (reps * copies)
+    g.destroy()
+    for w in ws:
+        w.free()
+    nbytes = nbits_bytes(k, n, 1, scale_bytes=4, zp=False, a_bytes=4, y_bytes=4)
+    log(f"single op K=1024 N=3072 f32: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s")
+    return {"us": us, "gbs": nbytes / (us * 1e-6) / 1e9}
 
 
 # ---------------------------------------------------------------- prefill GEMM
@@ -423,40 +493,88 @@ def int8_ops(ctx, reps, per_graph=8, m=2048, k=2048, n=2048):
 # ---------------------------------------------------------------- CPU baseline
 
 
-def cpu_baseline(seconds=10.0):
-    """The reference's EXLA-CPU path after move/2 restated in C: the q4 weights of a sample of
-    layers dequantized once to f16 (the scales' type), then Y = A . W^T with f32 accumulation on
-    host threads. Timed over whole decode steps of the sample; reported in the same GB/s
-    (algorithmic q4 bytes) as the GPU."""
-    from oracle import coracle
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    threads = min(16, os.cpu_count() or 1)
-    rng = np.random.default_rng(5)
-    layers = 2
-    ws = []
-    for _layer in range(layers):
-        for _name, k, n in QWEN3_06B:
-            b, sc, zp = make_weight_parts(rng, k, n)
-            w16 = coracle.dequantize_nbits(b, sc.astype(np.float32), zp, k, n, 4, 32, out_f16=True)
-            ws.append((k, n, w16))
-    a = {k: rng.standard_normal((1, k), dtype=np.float32) for k in (1024, 2048, 3072)}
-    step_bytes = layers * sum(nbits_bytes(k, n, 1) for _name, k, n in QWEN3_06B)
-    for k, _n, w16 in ws:  # warm-up
-        coracle.gemm(a[k], w16, threads)
+
+def _timed(fn, seconds):
+    fn()  # warm-up
     done, t0 = 0, time.perf_counter()
     while True:
-        for k, _n, w16 in ws:
-            coracle.gemm(a[k], w16, threads)
+        fn()
         done += 1
         elapsed = time.perf_counter() - t0
         if elapsed >= seconds:
-            break
+            return done, elapsed
+
+
+def cpu_baseline(seconds=10.0):
+    """The reference's EXLA-CPU path restated in C (oracle/oracle.c), on this host's cores:
+    - headline: the whole Qwen3-0.6B decode step (28 layers x 7 q4 GEMVs, M = 1) after move/2,
+      weights dequantized once to f16 (the scales' type), then an f32-accumulating dot (AVX2 FMA,
+      f16 widened by F16C) on every host thread, and the same on one thread;
+    - in-graph: the same GEMVs without move/2, dequantizing W in the graph on every call
+      (quantized.ex:39-44), on a 4-layer sample;
+    - the single f32 op of the CPU configuration (K=1024, N=3072, f32 scales, no zero points),
+      after move/2 (f32 weights).
+    Reported in the same algorithmic GB/s as the GPU. `seconds` is the time of the headline leg;
+    the other legs take a quarter of it each."""
+    from oracle import coracle
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    rng = np.random.default_rng(5)
+    ws, raw = [], []
+    for layer in range(QWEN3_LAYERS):
+        for _name, k, n in QWEN3_06B:
+            b, sc, zp = make_weight_parts(rng, k, n)
+            ws.append((k, n, coracle.dequantize_nbits(b, sc.astype(np.float32), zp, k, n, 4, 32, out_f16=True)))
+            if layer < 4:
+                raw.append((k, n, b, sc.astype(np.float32), zp))
+    a = {k: rng.standard_normal((1, k), dtype=np.float32) for k in (1024, 2048, 3072)}
+    step_bytes = QWEN3_LAYERS * sum(nbits_bytes(k, n, 1) for _name, k, n in QWEN3_06B)
+
+    def step(t):
+        for k, _n, w16 in ws:
+            coracle.gemm(a[k], w16, t)
+
+    done, elapsed = _timed(lambda: step(threads), seconds)
     gbs = done * step_bytes / elapsed / 1e9
-    log(f"cpu baseline: {done} samples in {elapsed:.1f} s, {gbs:.2f} GB/s on {threads} threads")
+    done1, elapsed1 = _timed(lambda: step(1), seconds / 4)
+    gbs1 = done1 * step_bytes / elapsed1 / 1e9
+    scratch = np.empty((3072, 3072), np.uint16)
+
+    def in_graph():
+        for k, n, b, sc, zp in raw:
+            coracle.matmul_nbits_in_graph(a[k], b, sc, zp, k, n, 4, 32, True, threads, scratch[:n, :k])
+
+    done_g, elapsed_g = _timed(in_graph, seconds / 4)
+    gbs_g = done_g * 4 * sum(nbits_bytes(k, n, 1) for _name, k, n in QWEN3_06B) / elapsed_g / 1e9
+    k1, n1 = 1024, 3072
+    b1 = rng.integers(0, 256, (n1, k1 // 32, 16), dtype=np.uint8)
+    s1 = (np.abs(rng.standard_normal(n1 * k1 // 32, dtype=np.float32)) * 0.01 + 1e-4).astype(np.float32)
+    w1 = coracle.dequantize_nbits(b1, s1, None, k1, n1, 4, 32, out_f16=False)
+    a1 = rng.standard_normal((1, k1), dtype=np.float32)
+    c1_bytes = nbits_bytes(k1, n1, 1, scale_bytes=4, zp=False, a_bytes=4, y_bytes=4)
+    done_c, elapsed_c = _timed(lambda: coracle.gemm(a1, w1, threads), seconds / 4)
+    c1_us = elapsed_c / done_c * 1e6
+    done_c1, elapsed_c1 = _timed(lambda: coracle.gemm(a1, w1, 1), seconds / 8)
+    c1_us1 = elapsed_c1 / done_c1 * 1e6
+    model = _cpu_model()
+    log(f"cpu baseline ({model}, {threads} threads): decode {gbs:.2f} GB/s ({elapsed / done * 1e3:.1f} ms/step), "
+        f"1 thread {gbs1:.2f} GB/s; in-graph dequant {gbs_g:.2f} GB/s; single op {c1_us:.1f} us "
+        f"({c1_bytes / c1_us / 1e3:.2f} GB/s), 1 thread {c1_us1:.1f} us")
     return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{layers} of 28 Qwen3-0.6B layers (14 q4 GEMVs, M=1) per sample, weights dequantized "
-                      f"once to f16, f32-accumulating GEMV on {threads} threads, {done} samples in {elapsed:.1f} s",
-            "ms_per_decode_step_28_layers": elapsed / done * 1e3 * 28 / layers}
+            "sample": f"whole Qwen3-0.6B decode steps (28 layers x 7 q4 GEMVs, M=1), weights dequantized once to "
+                      f"f16, f32-accumulating dot on {threads} threads, {done} steps in {elapsed:.1f} s",
+            "cpu_model": model, "nproc": os.cpu_count(), "ms_per_decode_step": elapsed / done * 1e3,
+            "one_thread_gbs": gbs1, "in_graph_dequant_gbs": gbs_g,
+            "single_op_us": c1_us, "single_op_gbs": c1_bytes / (c1_us * 1e-6) / 1e9, "single_op_one_thread_us": c1_us1}
 
 
 # ---------------------------------------------------------------- profiling runs
@@ -568,17 +686,23 @@ def main():
     dec_merged = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms, merged=True)
     extra = {}
     if not args.quick:
+        extra["single_op"] = single_op(ctx, 10)
         extra["prefill"] = prefill(ctx, 20, [256, 2048])
         extra["large_vocab"] = large_vocab(ctx, 50)
         extra["moe"] = moe_ffn(ctx, 20)
         extra["int8"] = int8_ops(ctx, 20)
     head = dec[1]
     roofline = {
-        "bound": "hbm", "kernel": "k_gemv_lean<4,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
+        "bound": "hbm", "kernel": "k_gemv_dec<4,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
         "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "traffic": traffic_per_launch(),
     }
     roofline["frac"] = roofline["achieved"] / HBM_PEAK_GBS
+    for key in ("launch_floor_us", "read_floor_us", "read_floor_gbs"):
+        roofline[key] = head.get(key)
+    if head.get("read_floor_us"):
+        # The GEMV's launch time against a launch that only reads the same packed weights.
+        roofline["read_floor_over_launch"] = head["read_floor_us"] / head["us_per_launch"]
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": "MatMulNBits q4: GB/s @M=1 and TFLOP/s @M=2048, % of MI355X roofline",
@@ -595,6 +719,7 @@ def main():
                          for m, r in dec.items()},
         "tokens_per_s_with_lm_head": head.get("tokens_per_s_with_lm_head"),
         "single_launch_us": head.get("single_launch_us"),
+        "eager_tokens_per_s": head.get("eager_tokens_per_s"),
         "decode_merged_qkv_gateup": {str(m): {k: v for k, v in r.items() if k in ("gbs", "ms_per_step", "us_per_launch",
                                                                                   "tokens_per_s")}
                                      for m, r in dec_merged.items()},
@@ -606,6 +731,7 @@ def main():
         line["prefill_tflops_M2048"] = extra["prefill"][2048]["tflops"]
         line["prefill_frac_M2048"] = extra["prefill"][2048]["tflops"] / MFMA_F16_PEAK_TFLOPS
         line["large_vocab"] = extra["large_vocab"]
+        line["single_op_f32_k1024_n3072"] = extra["single_op"]
         line["moe"] = extra["moe"]
         line["int8"] = extra["int8"]
     ctx.close()

@@ -324,6 +324,18 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
              int bias_dtype, int activation, int swiglu_fusion, float alpha, float beta, float limit,
              void* d_y, void* stream);
 
+/* ------------------------------------------------------------------ measurement floors */
+
+/*
+ * Launch and read floors for benchmarks (no reference counterpart). tmh_floor_empty launches an
+ * empty kernel of `workgroups` one-wavefront workgroups: the cost of one launch. tmh_floor_read
+ * reads the packed weight bytes of `w` once with the decode GEMV's load pattern (one 16-byte
+ * load per lane, 1 KiB per wavefront) and writes nothing to d_sink (4 bytes) unless the bytes
+ * xor to a marker: the cost of a kernel that only reads the weights. Asynchronous.
+ */
+int tmh_floor_empty(tmh_ctx* ctx, int workgroups, void* stream);
+int tmh_floor_read(tmh_ctx* ctx, const tmh_weight* w, void* d_sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

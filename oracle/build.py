@@ -17,7 +17,7 @@ LIB = os.path.join(BUILD, "liboracle.so")
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     tmp = LIB + ".tmp"
-    cmd = ["gcc", "-O3", "-march=x86-64-v3", "-fPIC", "-shared", "-Wall", "-pthread",
+    cmd = ["gcc", "-O3", "-march=x86-64-v3", "-fPIC", "-shared", "-Wall", "-fopenmp",
            "-o", tmp, os.path.join(HERE, "oracle.c"), "-lm"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:

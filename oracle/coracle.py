@@ -22,6 +22,7 @@ def lib() -> ctypes.CDLL:
         h.oracle_dequantize_nbits.argtypes = [vp, vp, vp, vp, i64, i64, i, i, i, vp]
         h.oracle_gemm_f32.argtypes = [vp, vp, i64, i64, i64, vp, i]
         h.oracle_gemm_f16w.argtypes = [vp, vp, i64, i64, i64, vp, i]
+        h.oracle_matmul_nbits_in_graph.argtypes = [vp, vp, vp, vp, i64, i64, i64, i, i, i, vp, vp, i]
         h.oracle_matmul_integer.argtypes = [vp, i, vp, i, vp, i64, vp, i64, i64, i64, i64, i64, i, vp]
         h.oracle_f32_to_f16_array.argtypes = [vp, vp, i64]
         h.oracle_f16_to_f32_array.argtypes = [vp, vp, i64]
@@ -62,6 +63,21 @@ def gemm(a, w, threads=1):
         lib().oracle_gemm_f16w(_p(a), _p(w.view(np.uint16)), m, n, k, _p(y), threads)
     else:
         lib().oracle_gemm_f32(_p(a), _p(np.ascontiguousarray(w, np.float32)), m, n, k, _p(y), threads)
+    return y
+
+
+def matmul_nbits_in_graph(a, b, scales, zp, k, n, bits, block_size, f16_weights, threads=1, scratch=None):
+    """MatMulNBits without move/2: dequantize W (f16 or f32) on every call, then Y = A . W^T."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    zp = None if zp is None else np.ascontiguousarray(zp, np.uint8)
+    if scratch is None:
+        scratch = np.empty((n, k), np.uint16 if f16_weights else np.float32)
+    y = np.empty((a.shape[0], n), np.float32)
+    if lib().oracle_matmul_nbits_in_graph(_p(a), _p(b), _p(scales), _p(zp), a.shape[0], k, n, bits, block_size,
+                                          1 if f16_weights else 0, _p(scratch), _p(y), threads):
+        raise ValueError("bad arguments")
     return y
 
 

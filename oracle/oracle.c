@@ -11,13 +11,16 @@
  *    (lib/transmuter.ex:1230-1240), in f32 or f16 (each operation rounded to the type).
  *  - oracle_gemm_f32 / oracle_gemm_f16w: the matmul that runs after move/2 on the EXLA CPU
  *    backend, Nx.dot(a, [-1], w, [1]) (quantized.ex:44) over the dequantized {N, K} weights,
- *    f32 accumulation, on `threads` POSIX threads (XLA runs Eigen on a thread pool).
+ *    f32 accumulation (AVX2 FMA, f16 weights widened with F16C), on `threads` OpenMP threads
+ *    (XLA runs Eigen on a persistent thread pool).
+ *  - oracle_matmul_nbits_in_graph: the same call without move/2, which dequantizes the weights
+ *    in the graph on every call (quantized.ex:39-44), then the dot.
  *  - oracle_matmul_integer: MatMulInteger's exact s32 sums (quantized.ex:105-110,
  *    lib/transmuter/ops/nn.ex:537-555), wrapping like s32.
  * Pinned by tests/test_oracle_c.py against oracle/oracle.py and the reference's fixtures.
  */
+#include <immintrin.h>
 #include <math.h>
-#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -115,72 +118,48 @@ int oracle_dequantize_nbits(const uint8_t* b, const float* scales, const uint8_t
   return 0;
 }
 
-typedef struct {
-  const float* a;
-  const void* w;
-  int w_f16;
-  int64_t M, N, K, n0, n1;
-  float* y;
-} gemm_job;
-
-static void* gemm_worker(void* arg) {
-  const gemm_job* j = (const gemm_job*)arg;
-  float* row = j->w_f16 ? (float*)malloc((size_t)j->K * sizeof(float)) : NULL;
-  for (int64_t n = j->n0; n < j->n1; ++n) {
-    const float* wn;
-    if (j->w_f16) {
-      const uint16_t* src = (const uint16_t*)j->w + n * j->K;
-      for (int64_t k = 0; k < j->K; ++k) row[k] = f16_to_f32(src[k]);
-      wn = row;
-    } else {
-      wn = (const float*)j->w + n * j->K;
-    }
-    for (int64_t m = 0; m < j->M; ++m) {
-      const float* am = j->a + m * j->K;
-      float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
-      int64_t k = 0;
-      for (; k + 4 <= j->K; k += 4) {
-        acc0 += am[k] * wn[k];
-        acc1 += am[k + 1] * wn[k + 1];
-        acc2 += am[k + 2] * wn[k + 2];
-        acc3 += am[k + 3] * wn[k + 3];
+/* One output row n of Y = A . W^T: f32 products accumulated in f32 (8 lanes of AVX2 FMA, then
+ * the lanes added), W read as f32 or widened from f16 with F16C as it is read. */
+static void gemm_row(const float* a, const void* w, int w_f16, int64_t M, int64_t N, int64_t K, float* y, int64_t n) {
+  for (int64_t m = 0; m < M; ++m) {
+    const float* am = a + m * K;
+    __m256 acc0 = _mm256_setzero_ps(), acc1 = _mm256_setzero_ps();
+    int64_t k = 0;
+    if (w_f16) {
+      const uint16_t* wn = (const uint16_t*)w + n * K;
+      for (; k + 16 <= K; k += 16) {
+        const __m256 w0 = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(wn + k)));
+        const __m256 w1 = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(wn + k + 8)));
+        acc0 = _mm256_fmadd_ps(_mm256_loadu_ps(am + k), w0, acc0);
+        acc1 = _mm256_fmadd_ps(_mm256_loadu_ps(am + k + 8), w1, acc1);
       }
-      for (; k < j->K; ++k) acc0 += am[k] * wn[k];
-      j->y[m * j->N + n] = (acc0 + acc1) + (acc2 + acc3);
+      float tail = 0.f;
+      for (; k < K; ++k) tail += am[k] * f16_to_f32(wn[k]);
+      float lanes[8];
+      _mm256_storeu_ps(lanes, _mm256_add_ps(acc0, acc1));
+      y[m * N + n] = ((lanes[0] + lanes[1]) + (lanes[2] + lanes[3])) + ((lanes[4] + lanes[5]) + (lanes[6] + lanes[7])) + tail;
+    } else {
+      const float* wn = (const float*)w + n * K;
+      for (; k + 16 <= K; k += 16) {
+        acc0 = _mm256_fmadd_ps(_mm256_loadu_ps(am + k), _mm256_loadu_ps(wn + k), acc0);
+        acc1 = _mm256_fmadd_ps(_mm256_loadu_ps(am + k + 8), _mm256_loadu_ps(wn + k + 8), acc1);
+      }
+      float tail = 0.f;
+      for (; k < K; ++k) tail += am[k] * wn[k];
+      float lanes[8];
+      _mm256_storeu_ps(lanes, _mm256_add_ps(acc0, acc1));
+      y[m * N + n] = ((lanes[0] + lanes[1]) + (lanes[2] + lanes[3])) + ((lanes[4] + lanes[5]) + (lanes[6] + lanes[7])) + tail;
     }
   }
-  free(row);
-  return NULL;
 }
 
+/* Rows split over `threads` OpenMP threads (a persistent team, as XLA's CPU backend runs its dot
+ * on a persistent Eigen thread pool). */
 static int gemm(const float* a, const void* w, int w_f16, int64_t M, int64_t N, int64_t K, float* y,
                 int threads) {
   if (threads < 1) threads = 1;
-  if (threads > 256) threads = 256;
-  pthread_t tid[256];
-  gemm_job jobs[256];
-  const int64_t per = (N + threads - 1) / threads;
-  int started = 0;
-  for (int t = 0; t < threads; ++t) {
-    const int64_t n0 = t * per, n1 = n0 + per < N ? n0 + per : N;
-    if (n0 >= n1) break;
-    jobs[t] = (gemm_job){a, w, w_f16, M, N, K, n0, n1, y};
-    if (threads == 1) {
-      gemm_worker(&jobs[t]);
-    } else if (pthread_create(&tid[t], NULL, gemm_worker, &jobs[t]) != 0) {
-      gemm_worker(&jobs[t]);
-      continue;
-    } else {
-      ++started;
-    }
-    (void)started;
-  }
-  if (threads > 1)
-    for (int t = 0; t < threads; ++t) {
-      const int64_t n0 = t * per, n1 = n0 + per < N ? n0 + per : N;
-      if (n0 >= n1) break;
-      pthread_join(tid[t], NULL);
-    }
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t n = 0; n < N; ++n) gemm_row(a, w, w_f16, M, N, K, y, n);
   return 0;
 }
 
@@ -195,6 +174,27 @@ int oracle_gemm_f16w(const float* a, const uint16_t* w, int64_t M, int64_t N, in
   return gemm(a, w, 1, M, N, K, y, threads);
 }
 
+/* MatMulNBits without a moved weight (quantized.ex:39-44): every call dequantizes W in the
+ * activations' type (f16 or f32, out_f16) into `scratch` (N*K values), then runs the dot. The
+ * dequantization splits over the same threads by rows. */
+int oracle_matmul_nbits_in_graph(const float* a, const uint8_t* b, const float* scales, const uint8_t* zp_packed,
+                                 int64_t M, int64_t K, int64_t N, int bits, int block_size, int out_f16,
+                                 void* scratch, float* y, int threads) {
+  if (threads < 1) threads = 1;
+  if (bits != 2 && bits != 4 && bits != 8) return 1;
+  const int64_t blocks = (K + block_size - 1) / block_size;
+  const int64_t row_bytes = blocks * block_size * bits / 8;
+  const int64_t zrow = (blocks * bits + 7) / 8;
+  int bad = 0;
+#pragma omp parallel for num_threads(threads) schedule(static) reduction(| : bad)
+  for (int64_t n = 0; n < N; ++n) {
+    void* out = out_f16 ? (void*)((uint16_t*)scratch + n * K) : (void*)((float*)scratch + n * K);
+    bad |= oracle_dequantize_nbits(b + n * row_bytes, scales + n * blocks, zp_packed ? zp_packed + n * zrow : NULL,
+                                   NULL, K, 1, bits, block_size, out_f16, out);
+  }
+  if (bad) return 1;
+  return gemm(a, scratch, out_f16, M, N, K, y, threads);
+}
 /* y[b, m, n] = sum_k (a - az[m]) (b - bz[n]) mod 2^32; a_signed / b_signed select s8 data. */
 int oracle_matmul_integer(const uint8_t* a, int a_signed, const uint8_t* bm, int b_signed,
                           const uint8_t* az, int64_t az_count, const uint8_t* bz, int64_t bz_count,

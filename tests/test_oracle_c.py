@@ -60,3 +60,17 @@ def test_matmul_nbits_fixture_through_c():
     y = coracle.gemm(A.reshape(-1, 512), w, 2).reshape(2, 3, 40)
     expected = f.outputs["Y"]
     assert np.abs(y - expected).max() <= 1e-4 + 1e-3 * np.abs(expected).max()
+
+
+@pytest.mark.parametrize("f16,zp,threads", [(True, True, 1), (True, False, 3), (False, True, 2)])
+def test_in_graph_matmul_matches_the_numpy_oracle(f16, zp, threads):
+    """oracle_matmul_nbits_in_graph (dequantize on every call, then the dot) against
+    oracle.matmul_nbits with W in the activations' type."""
+    rng = np.random.default_rng(int(f16) * 4 + int(zp) * 2 + threads)
+    k, n, m = 200, 37, 3
+    b, s, z = nbits_weight(rng, k, n, 4, 32, zp="packed" if zp else "none")
+    a = rng.standard_normal((m, k)).astype(np.float16 if f16 else np.float32)
+    got = coracle.matmul_nbits_in_graph(a.astype(np.float32), b, s.astype(np.float32), z, k, n, 4, 32, f16, threads)
+    want = o.matmul_nbits(a, b, s.astype(np.float16 if f16 else np.float32), z, k=k, n=n, bits=4,
+                          block_size=32).astype(np.float64)
+    assert np.abs(got - want).max() <= (1e-2 if f16 else 1e-4) * np.abs(want).max()

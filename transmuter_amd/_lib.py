@@ -70,6 +70,8 @@ SIGNATURES = {
                                 _vp]),
     "tmh_dynamic_quantize_linear": (_i, [_vp, _vp, _i, _i64, _vp, _vp, _vp, _vp]),
     "tmh_upload_file": (_i, [_vp, _vp, ctypes.c_char_p, _i64, _sz]),
+    "tmh_floor_empty": (_i, [_vp, _i, _vp]),
+    "tmh_floor_read": (_i, [_vp, _vp, _vp, _vp]),
     "tmh_weight_upload_qmoe": (_i, [_vp, _vp, _sz, _vp, _i, _sz, _vp, _sz, _i64, _i64, _i64, _i, _i64, _i,
                                     ctypes.POINTER(_vp)]),
     "tmh_qmoe": (_i, [_vp, _vp, _i, _i64, _i64, _vp, _i, _i64, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,

@@ -1,0 +1,156 @@
+// Decode GEMV kernel (M <= 16): f16 A, f16 weights from the tiled packed layout, f16 Y, no bias.
+//
+// Reference: MatMulNBits (lib/transmuter/ops/quantized.ex:30-46) after move/2, the dot of
+// quantized.ex:44 over dequantized {N, K} weights (Quantized.dequantize_weight/4, :234-240).
+//
+// A workgroup of NW wavefronts covers TN consecutive 16-column tiles. Its wavefronts split the
+// chunks of K, U chunks each and round: every load of a round (the weights of U chunks x TN
+// tiles, their scales and zero points, and the A fragments) issues before the first is used.
+// Each lane unpacks its 16 weight bytes in registers into exact f16 (q - zero) * scale and feeds
+// v_mfma_f32_16x16x32_f16 with the weights as the first operand, so a lane ends with 4
+// consecutive columns of one row of Y; the wavefronts' partial sums add through LDS and the lanes
+// of rows below M store 8 bytes each.
+//
+// A fragments: lane (g, r) needs A[r][chunk*CW + g*GW + 8i ..] for step i. With ALDS false each
+// lane loads its own four 16-byte pieces (16 rows x 4 scattered pieces per instruction, cheap
+// while few rows are real). With ALDS true (M > 4) a wavefront loads its chunk's rows as whole
+// 256-byte rows (4 rows per instruction, contiguous), writes them to its own LDS area and reads
+// the fragments back (XOR-swizzled by row, no barrier: a wavefront's LDS accesses stay in order).
+// At M = 16 that takes a 1024 -> 3072 launch from 3.63 to 3.25 us; at M <= 4 it costs 0.03-0.16 us.
+//
+// The arguments the first loads need come first (12 dwords): the library compiles this kernel
+// with its leading arguments preloaded into SGPRs at wave launch, so a wavefront issues its
+// weight loads without first waiting for a kernel-argument load. Addressing is 32-bit through
+// buffer resources: rows of A past M and tiles past the weight read zeros.
+#pragma once
+
+#include "tmh_device.h"
+
+namespace tmh {
+
+// shape = M | nbc << 8 | bsc_shift << 16: rows of A (1..16), parameter entries per row and
+// chunk, and log2 of the weights one parameter entry covers.
+template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS>
+__global__ __launch_bounds__(64 * NW) void k_gemv_dec(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
+  constexpr int CW = 512 / BITS;   // weights per chunk row
+  constexpr int GW = CW / 4;       // weights per lane per chunk
+  constexpr int STEPS = GW / 8;    // MFMA steps per chunk
+  constexpr int NJ = SPLIT ? STEPS : 1;
+  constexpr int RB = CW * 2 / 16;  // 16-byte pieces per A row of a chunk
+  __shared__ float4_t red[NW > 1 ? NW * TN * 64 : 1];
+  __shared__ uint4_t a_lds[ALDS ? NW * U * 16 * RB : 1];
+  const uint32_t M = shape & 0xFFu, nbc = (shape >> 8) & 0xFFu, bsc_shift = shape >> 16;
+  const int lane = threadIdx.x & 63;
+  // Wavefront-uniform through readfirstlane, so chunk offsets go to the loads' scalar offset.
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t t0 = blockIdx.x * TN;
+  const uint32_t n_params = ntiles * nch * nbc * 16;
+  const auto q_rsrc = buffer_rsrc(qt, ntiles * nch * 1024);
+  const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+  const auto a_rsrc = buffer_rsrc(A, M * lda * 2);
+  const uint32_t a_row = static_cast<uint32_t>(r) < M ? static_cast<uint32_t>(r) * lda * 2 : 0x80000000u;
+  float4_t acc[TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) acc[tn] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (uint32_t base = wave * U; base < nch; base += NW * U) {
+    uint4_t w[U][TN];
+    uint32_t sv[U][TN][NJ], zv[U][TN][NJ];
+    half8_t af[U][STEPS];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t c = base + u < nch ? base + u : nch - 1;
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t t = t0 + tn;  // t >= ntiles reads zeros
+        w[u][tn] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, (t * nch * 64 + lane) * 16, c * 1024, 0);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const uint32_t e = ((t * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
+          sv[u][tn][j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, 0, 0);
+          if constexpr (HAS_ZP) zv[u][tn][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0);
+        }
+      }
+      if constexpr (ALDS) {
+        // Rows of the chunk in order: instruction j loads rows (64/RB)*j + lane/RB, piece lane%RB.
+        constexpr int RPI = 64 / RB;
+        uint4_t rows[16 / RPI];
+#pragma unroll
+        for (int j = 0; j < 16 / RPI; ++j) {
+          const uint32_t row = RPI * j + lane / RB, p = lane % RB;
+          const uint32_t off = (base + u < nch && row < M) ? row * lda * 2 + ((base + u) * CW + 8 * p) * 2 : 0x80000000u;
+          rows[j] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0);
+        }
+        uint4_t* mine = a_lds + (wave * U + u) * 16 * RB;
+#pragma unroll
+        for (int j = 0; j < 16 / RPI; ++j) {
+          const uint32_t row = RPI * j + lane / RB, p = lane % RB;
+          mine[row * RB + (p ^ (row % RB))] = rows[j];
+        }
+#pragma unroll
+        for (int i = 0; i < STEPS; ++i) {
+          const uint32_t p = g * (GW / 8) + i;
+          af[u][i] = __builtin_bit_cast(half8_t, mine[r * RB + (p ^ (r % RB))]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < STEPS; ++i) {
+          const uint32_t k = (base + u) * CW + g * GW + 8 * i;
+          const uint32_t off = base + u < nch ? a_row + k * 2 : 0x80000000u;
+          af[u][i] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
+        }
+      }
+    }
+    // Every chunk of the round is computed, also one past K (its A fragments are zeros, so it
+    // adds 0): a branch here would let the compiler sink that chunk's loads behind the first
+    // chunk's wait and MFMAs, one memory latency per chunk.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int i = 0; i < STEPS; ++i) {
+        const int j = SPLIT ? i : 0;
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+          const uint32_t zq = HAS_ZP ? 0x6400u + zv[u][tn][j] : 0x6400u + (1u << (BITS - 1));
+          const half8_t b = unpack_step<BITS>(w[u][tn], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
+                                              __builtin_bit_cast(half2_t, sv[u][tn][j] | (sv[u][tn][j] << 16)));
+          acc[tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[u][i], acc[tn], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if constexpr (NW > 1) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) red[(wave * TN + tn) * 64 + lane] = acc[tn];
+    __syncthreads();
+  }
+  if (static_cast<uint32_t>(r) >= M) return;
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    if constexpr (NW > 1) {
+      if (tn % NW != static_cast<int>(wave)) continue;
+      acc[tn] = red[tn * 64 + lane];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) acc[tn] += red[(w2 * TN + tn) * 64 + lane];
+    } else if (wave != 0) {
+      continue;
+    }
+    const uint32_t n = (t0 + tn) * 16 + 4 * g;
+    if (n >= N) continue;
+    _Float16* dst = Y + r * ldy + n;
+    const float4_t v = acc[tn];
+    if (n + 4 <= N && (ldy % 4) == 0) {
+      const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
+      const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+      *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+    } else {
+      for (uint32_t e = 0; e < 4 && n + e < N; ++e) dst[e] = static_cast<_Float16>(v[e]);
+    }
+  }
+}
+
+}  // namespace tmh

@@ -1,0 +1,135 @@
+// Launch plan of the decode GEMV (k_gemv_dec, tmh_gemv.h): MatMulNBits with M <= 16 rows of f16
+// A, f16 weights, f16 Y, no bias (lib/transmuter/ops/quantized.ex:30-46 after move/2).
+//
+// This file is compiled with the kernels' leading arguments preloaded into SGPRs
+// (-mllvm -amdgpu-kernarg-preload-count): at the Qwen3-0.6B projection shapes that takes a
+// launch from 3.16 to 2.78 us, and a plain read of the same bytes from 1.99 to 1.82 us.
+//
+// Two regimes, measured on MI355X inside HIP graphs:
+//  - one-shot (the whole grid resident at once: the Qwen3-0.6B projections): one chunk per
+//    wavefront and round (U = 1), as many wavefronts as chunks (NW = nch, up to 16), one tile
+//    per workgroup. Latency-bound: more chunks per wavefront or more tiles per workgroup were
+//    0.07-0.4 us slower per launch. A is staged through LDS for M > 4.
+//  - streaming (lm_head-sized N): U = 1, NW = nch / 2 wavefronts (two rounds each), two tiles per
+//    workgroup for M <= 4 and four for M > 4, so every A fragment serves two or four tiles. On
+//    151936 x 1024 this reached 5.7-5.9 TB/s at M = 1 and 5.5 TB/s at M = 8 (plain reads of the
+//    same bytes: 6.6-6.75 TB/s); grid-stride persistent variants were 10-60% slower.
+#include <algorithm>
+
+#include "tmh_gemv.h"
+#include "tmh_internal.h"
+
+namespace tmh {
+namespace {
+
+constexpr size_t kStaticLds = 64 * 1024;
+
+struct DecArgs {
+  const uint4_t* qt;
+  const uint16_t* sc;
+  const uint8_t* zp;
+  const _Float16* a;
+  uint32_t nch, ntiles, lda, shape;
+  _Float16* y;
+  uint32_t ldy, n;
+};
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int NW, int TN, bool ALDS>
+void go(const DecArgs& d, hipStream_t s) {
+  // The LDS-staged A needs NW * 16 rows of a chunk beside the partial sums; shapes where that
+  // exceeds the static LDS of a workgroup load A directly.
+  constexpr size_t rb = (512 / BITS) * 2 / 16;
+  constexpr size_t red = NW > 1 ? static_cast<size_t>(NW) * TN * 64 * 16 : 0;
+  constexpr bool A_LDS = ALDS && red + static_cast<size_t>(NW) * 16 * rb * 16 <= kStaticLds;
+  static_assert(red <= kStaticLds, "partial sums exceed the static LDS");
+  const unsigned grid = (d.ntiles + TN - 1) / TN;
+  k_gemv_dec<BITS, HAS_ZP, SPLIT, 1, NW, TN, A_LDS><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles,
+                                                                              d.lda, d.shape, d.y, d.ldy, d.n);
+}
+
+// Wavefront counts the one-shot kernels are built for: the chunk count rounded up to one of
+// them (the extra wavefronts find no chunk and add zeros).
+int round_waves(int64_t w) {
+  for (int c : {1, 2, 4, 8, 12}) if (w <= c) return c;
+  return 16;
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT, bool ALDS>
+void one_shot(const DecArgs& d, int nw, hipStream_t s) {
+  switch (nw) {
+    case 1: go<BITS, HAS_ZP, SPLIT, 1, 1, ALDS>(d, s); break;
+    case 2: go<BITS, HAS_ZP, SPLIT, 2, 1, ALDS>(d, s); break;
+    case 4: go<BITS, HAS_ZP, SPLIT, 4, 1, ALDS>(d, s); break;
+    case 8: go<BITS, HAS_ZP, SPLIT, 8, 1, ALDS>(d, s); break;
+    case 12: go<BITS, HAS_ZP, SPLIT, 12, 1, ALDS>(d, s); break;
+    default: go<BITS, HAS_ZP, SPLIT, 16, 1, ALDS>(d, s);
+  }
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int TN>
+void streaming(const DecArgs& d, int nw, hipStream_t s) {
+  switch (nw) {
+    case 1: go<BITS, HAS_ZP, SPLIT, 1, TN, false>(d, s); break;
+    case 2: go<BITS, HAS_ZP, SPLIT, 2, TN, false>(d, s); break;
+    case 4: go<BITS, HAS_ZP, SPLIT, 4, TN, false>(d, s); break;
+    default: go<BITS, HAS_ZP, SPLIT, 8, TN, false>(d, s);
+  }
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT>
+void launch_bits(const DecArgs& d, int64_t M, int num_cus, hipStream_t s) {
+  const int64_t nch = d.nch;
+  const int64_t resident = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * 24;
+  if (static_cast<int64_t>(d.ntiles) * std::min<int64_t>(nch, 16) <= resident) {
+    const int nw = round_waves(nch);
+    if (M > 4)
+      one_shot<BITS, HAS_ZP, SPLIT, true>(d, nw, s);
+    else
+      one_shot<BITS, HAS_ZP, SPLIT, false>(d, nw, s);
+    return;
+  }
+  // Streaming: two rounds of one chunk per wavefront (at most 8 wavefronts, more rounds for
+  // larger K), two or four tiles per workgroup.
+  const int nw = std::min(8, round_waves((nch + 1) / 2));
+  if (M > 4)
+    streaming<BITS, HAS_ZP, SPLIT, 4>(d, nw, s);
+  else
+    streaming<BITS, HAS_ZP, SPLIT, 2>(d, nw, s);
+}
+
+}  // namespace
+
+bool decode_gemv_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, const void* a, const void* y) {
+  return M >= 1 && M <= 16 && reinterpret_cast<uintptr_t>(a) % 16 == 0 && lda % 8 == 0 && w->K % 8 == 0 &&
+         M * lda * 2 < (int64_t(1) << 31) && w->ntiles * w->nchunks * 1024 < (int64_t(1) << 31) &&
+         w->ntiles * w->nchunks * w->nbc * 16 * 2 < (int64_t(1) << 31) && ldy < (int64_t(1) << 30) &&
+         (reinterpret_cast<uintptr_t>(y) & 7) == 0 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT;
+}
+
+void launch_decode_gemv(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,
+                        hipStream_t s, int num_cus) {
+  const int cw = chunk_weights(w->bits);
+  const int bsc = std::min(w->block_size, cw);
+  int shift = 0;
+  while ((1 << shift) < bsc) ++shift;
+  const DecArgs d{reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+                  static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a),
+                  static_cast<uint32_t>(w->nchunks), static_cast<uint32_t>(w->ntiles), static_cast<uint32_t>(lda),
+                  static_cast<uint32_t>(M) | (static_cast<uint32_t>(w->nbc) << 8) | (static_cast<uint32_t>(shift) << 16),
+                  static_cast<_Float16*>(y), static_cast<uint32_t>(ldy), static_cast<uint32_t>(w->N)};
+  const bool zp = w->zp_kind == TMH_ZP_PACKED;
+  const bool split = w->block_size < cw / 4;  // a lane's k-group spans several blocks
+#define TMH_DEC(B)                                                   \
+  if (zp && split) launch_bits<B, true, true>(d, M, num_cus, s);      \
+  else if (zp) launch_bits<B, true, false>(d, M, num_cus, s);         \
+  else if (split) launch_bits<B, false, true>(d, M, num_cus, s);      \
+  else launch_bits<B, false, false>(d, M, num_cus, s);
+  switch (w->bits) {
+    case 2: { TMH_DEC(2) } break;
+    case 4: { TMH_DEC(4) } break;
+    default: { TMH_DEC(8) }
+  }
+#undef TMH_DEC
+}
+
+}  // namespace tmh

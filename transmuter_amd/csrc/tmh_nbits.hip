@@ -9,6 +9,7 @@
 //
 // Kernels
 //   k_dequant         the {N, K} weights, bit-exact, in any float type
+//   k_gemv_dec        (tmh_gemv.h) decode GEMV for M <= 16, f16 Y without bias
 //   k_gemv_f16        f16 A and f16 weights, M <= 16*MT per block row: every lane unpacks its
 //                     16 bytes in registers into exact f16 weights (q - zero) * scale and feeds
 //                     v_mfma_f32_16x16x32_f16; four wavefronts split K and add through LDS
@@ -279,110 +280,6 @@ __global__ __launch_bounds__(1024) void k_gemv_f16(
   gemv_epilogue<MT>(acc, red, nwaves, t, m0, M, N, bias, bias_dt, Y, y_dt, dot_dt, ldy);
 }
 
-
-// Decode GEMV for the common case: M <= 16, f16 A (16-byte aligned rows, K a multiple of 8),
-// f16 weights, f16 Y, no bias. A workgroup covers TN consecutive 16-column tiles; its wavefronts
-// split the chunks of K, U chunks per wavefront and round, and every A fragment a wavefront loads
-// serves all TN tiles. Addressing is 32-bit through buffer resources: rows of A past M and tiles
-// past N read zeros from the range check. The weights are the MFMA's first operand, so a lane
-// ends with 4 consecutive columns of one row, reduced across wavefronts through LDS and stored
-// as one 8-byte write by the lanes that own rows below M.
-template <int BITS, bool HAS_ZP, bool SPLIT, int U, int TN>
-__global__ __launch_bounds__(1024) void k_gemv_lean(
-    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
-    const _Float16* __restrict__ A, int M, int K, int lda, _Float16* __restrict__ Y, int ldy, int N, int nchunks,
-    int ntiles, int nbc, int bsc_shift) {
-  constexpr int CW = 512 / BITS;
-  constexpr int GW = CW / 4;
-  constexpr int STEPS = GW / 8;
-  constexpr int NJ = SPLIT ? STEPS : 1;
-  extern __shared__ float4_t red[];  // nwaves * TN * 64
-  const int nwaves = blockDim.x >> 6;
-  // The wavefront index through readfirstlane: the compiler then knows it (and the chunk offsets
-  // formed from it) to be uniform and passes the chunk offset as the loads' scalar offset,
-  // instead of a loop over the lanes' distinct values around every weight load.
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r = lane & 15, g = lane >> 4;
-  const uint32_t t0 = blockIdx.x * TN;
-  const uint32_t nch = static_cast<uint32_t>(nchunks);
-  const uint32_t n_params = static_cast<uint32_t>(ntiles) * nch * nbc * 16;
-  const auto q_rsrc = buffer_rsrc(qt, static_cast<uint32_t>(ntiles) * nch * 1024);
-  const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
-  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
-  const auto a_rsrc = buffer_rsrc(A, static_cast<uint32_t>(M) * lda * 2);
-  const uint32_t a_row = r < M ? static_cast<uint32_t>(r) * lda * 2 : 0x80000000u;  // outside the range
-  float4_t acc[TN];
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) acc[tn] = float4_t{0.f, 0.f, 0.f, 0.f};
-  for (uint32_t base = wave * U; base < nch; base += nwaves * U) {
-    uint4_t w[U][TN];
-    uint32_t sv[U][TN][NJ], zv[U][TN][NJ];
-    half8_t af[U][STEPS];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t c = base + u < nch ? base + u : nch - 1;
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const uint32_t t = t0 + tn;  // t >= ntiles reads zeros
-        w[u][tn] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, (t * nch * 64 + lane) * 16, c * 1024, 0);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const uint32_t e = ((t * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
-          sv[u][tn][j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, 0, 0);
-          if constexpr (HAS_ZP) zv[u][tn][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < STEPS; ++i) {
-        const uint32_t k = (base + u) * CW + g * GW + 8 * i;
-        const uint32_t off = (base + u < nch && k < static_cast<uint32_t>(K)) ? a_row + k * 2 : 0x80000000u;
-        af[u][i] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (base + u >= nch) break;
-#pragma unroll
-      for (int i = 0; i < STEPS; ++i) {
-        const int j = SPLIT ? i : 0;
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-          const uint32_t zq = HAS_ZP ? 0x6400u + zv[u][tn][j] : 0x6400u + (1u << (BITS - 1));
-          const half8_t b = unpack_step<BITS>(w[u][tn], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
-                                              __builtin_bit_cast(half2_t, sv[u][tn][j] | (sv[u][tn][j] << 16)));
-          acc[tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[u][i], acc[tn], 0, 0, 0);
-        }
-      }
-    }
-  }
-  if (nwaves > 1) {
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn) red[(wave * TN + tn) * 64 + lane] = acc[tn];
-    __syncthreads();
-  }
-  if (r >= M) return;
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) {
-    if (nwaves > 1) {
-      if (tn % nwaves != wave) continue;
-      acc[tn] = red[tn * 64 + lane];
-      for (int w2 = 1; w2 < nwaves; ++w2) acc[tn] += red[(w2 * TN + tn) * 64 + lane];
-    } else if (wave != 0) {
-      continue;
-    }
-    const int n = static_cast<int>(t0 + tn) * 16 + 4 * g;
-    if (n >= N) continue;
-    _Float16* dst = Y + static_cast<int64_t>(r) * ldy + n;
-    const float4_t v = acc[tn];
-    if (n + 4 <= N && (ldy % 4) == 0) {
-      const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
-      const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
-      *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-    } else {
-      for (int e = 0; e < 4 && n + e < N; ++e) dst[e] = static_cast<_Float16>(v[e]);
-    }
-  }
-}
 
 // 128 x 128 output tile per workgroup: wave (wm, wn) computes rows 64*wm.. and columns
 // 64*wn.. (four 16-row tiles by four 16-column tiles) over all of K.
@@ -950,62 +847,15 @@ void launch_gemv_u(const tmh_weight* w, const MatArgs& a, hipStream_t s, int wav
       bsc_shift_of(w));
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int U, int TN>
-void launch_gemv_lean_ut(const tmh_weight* w, const MatArgs& a, hipStream_t s, int waves) {
-  const unsigned blocks = static_cast<unsigned>((w->ntiles + TN - 1) / TN);
-  const size_t lds = waves > 1 ? static_cast<size_t>(waves) * TN * 64 * sizeof(float4_t) : 0;
-  k_gemv_lean<BITS, HAS_ZP, SPLIT, U, TN><<<blocks, 64 * waves, lds, s>>>(
-      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
-      static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), static_cast<int>(a.M),
-      static_cast<int>(w->K), static_cast<int>(a.lda), static_cast<_Float16*>(a.y), static_cast<int>(a.ldy),
-      static_cast<int>(w->N), static_cast<int>(w->nchunks), static_cast<int>(w->ntiles), w->nbc, bsc_shift_of(w));
-}
-
-template <int BITS, bool HAS_ZP, bool SPLIT, int U>
-void launch_gemv_lean_u(const tmh_weight* w, const MatArgs& a, hipStream_t s, int waves, int tn) {
-  if (tn >= 4)
-    launch_gemv_lean_ut<BITS, HAS_ZP, SPLIT, U, 4>(w, a, s, waves);
-  else if (tn == 2)
-    launch_gemv_lean_ut<BITS, HAS_ZP, SPLIT, U, 2>(w, a, s, waves);
-  else
-    launch_gemv_lean_ut<BITS, HAS_ZP, SPLIT, U, 1>(w, a, s, waves);
-}
-
-// The lean decode GEMV applies: M <= 16, aligned f16 A with K % 8 == 0, f16 Y, no bias, and
-// every buffer addressable with 32-bit byte offsets.
-bool lean_gemv_ok(const tmh_weight* w, const MatArgs& a) {
-  return a.M <= 16 && a.a_vec && a.y_dt == TMH_F16 && a.dot_dt == TMH_F16 && !a.bias &&
-         a.M * a.lda * 2 < (int64_t(1) << 31) && w->ntiles * w->nchunks * 1024 < (int64_t(1) << 31) &&
-         a.ldy < (int64_t(1) << 30) && (reinterpret_cast<uintptr_t>(a.y) & 7) == 0;
-}
-
 // Chunks per wavefront round (U) and wavefronts per block: up to 16 wavefronts, each with
 // 1, 2 or 4 chunk loads in flight, so that K of up to 64 chunks needs one round.
 template <int BITS, int MT, bool HAS_ZP, bool SPLIT>
 void launch_gemv(const tmh_weight* w, const MatArgs& a, hipStream_t s, int num_cus) {
   const int64_t c = w->nchunks;
-  if (MT == 1 && lean_gemv_ok(w, a)) {
-    // While the whole grid is resident at once, one chunk and one tile per wavefront keeps the
-    // most loads in parallel. Beyond that (lm_head-sized N), each wavefront takes two tiles and
-    // two chunks per round, and a workgroup of 4-16 wavefronts covers K in one or two rounds:
-    // measured on 151936x1024, 65536x2048 and 32000x4096 q4 this beats wider tile groups (TN=4)
-    // and four-chunk rounds by 3-20%.
-    const int64_t resident = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * 24;
-    int u = c <= 16 ? 1 : (c <= 32 ? 2 : 4), tn = 1;
-    int64_t waves = (c + u - 1) / u;
-    if (w->ntiles * waves > resident) {
-      u = 2;
-      tn = 2;
-      waves = std::max<int64_t>(4, (c + 3) / 4);
-    }
-    waves = std::min<int64_t>(16, waves);
-    const int nw = static_cast<int>(waves);
-    if (u == 1)
-      launch_gemv_lean_u<BITS, HAS_ZP, SPLIT, 1>(w, a, s, nw, tn);
-    else if (u == 2)
-      launch_gemv_lean_u<BITS, HAS_ZP, SPLIT, 2>(w, a, s, nw, tn);
-    else
-      launch_gemv_lean_u<BITS, HAS_ZP, SPLIT, 4>(w, a, s, nw, tn);
+  // The decode GEMV (tmh_gemv.hip): f16 Y without bias, aligned A, 32-bit offsets.
+  if (MT == 1 && a.y_dt == TMH_F16 && a.dot_dt == TMH_F16 && !a.bias &&
+      decode_gemv_ok(w, a.M, a.lda, a.ldy, a.a, a.y)) {
+    launch_decode_gemv(w, a.a, a.M, a.lda, a.y, a.ldy, s, num_cus);
     return;
   }
   if (c <= 16) {
