@@ -658,6 +658,9 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-graph", action="store_true", help="launch each call on the stream, no HIP graphs")
+    p.add_argument("--sections", default="all",
+                   help="comma list of parts to run besides the M=1 decode headline: decode (M=4/8/16 and merged), "
+                        "single, prefill, vocab, moe, int8, cpu (default all)")
     p.add_argument("--profile", choices=["decode", "prefill", "moe", "vocab", "int8"], help="a short graph-free run for rocprofv3")
     p.add_argument("--summarize", nargs="*", metavar="PATH",
                    help="print a markdown summary of rocprofv3 output: a kernel_stats.csv, then --pmc directories")
@@ -681,15 +684,23 @@ def main():
         profile_run(ctx, args.profile, args.steps)
         ctx.close()
         return
-    ms = [1] if args.quick else [1, 4, 8, 16]
+    parts = {"decode", "single", "prefill", "vocab", "moe", "int8", "cpu"} if args.sections == "all" \
+        else set(args.sections.split(","))
+    if args.quick:
+        parts = set()
+    ms = [1, 4, 8, 16] if "decode" in parts else [1]
     dec = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms, full_step=True)
-    dec_merged = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms, merged=True)
+    dec_merged = decode_sweep(ctx, args.steps, args.warmup, args.sets, ms, merged=True) if "decode" in parts else {}
     extra = {}
-    if not args.quick:
+    if "single" in parts:
         extra["single_op"] = single_op(ctx, 10)
+    if "prefill" in parts:
         extra["prefill"] = prefill(ctx, 20, [256, 2048])
+    if "vocab" in parts:
         extra["large_vocab"] = large_vocab(ctx, 50)
+    if "moe" in parts:
         extra["moe"] = moe_ffn(ctx, 20)
+    if "int8" in parts:
         extra["int8"] = int8_ops(ctx, 20)
     head = dec[1]
     roofline = {
@@ -703,7 +714,7 @@ def main():
     if head.get("read_floor_us"):
         # The GEMV's launch time against a launch that only reads the same packed weights.
         roofline["read_floor_over_launch"] = head["read_floor_us"] / head["us_per_launch"]
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    cpu = None if args.no_cpu or "cpu" not in parts else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": "MatMulNBits q4: GB/s @M=1 and TFLOP/s @M=2048, % of MI355X roofline",
         "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -730,10 +741,10 @@ def main():
         line["prefill"] = {str(m): v for m, v in extra["prefill"].items()}
         line["prefill_tflops_M2048"] = extra["prefill"][2048]["tflops"]
         line["prefill_frac_M2048"] = extra["prefill"][2048]["tflops"] / MFMA_F16_PEAK_TFLOPS
-        line["large_vocab"] = extra["large_vocab"]
-        line["single_op_f32_k1024_n3072"] = extra["single_op"]
-        line["moe"] = extra["moe"]
-        line["int8"] = extra["int8"]
+    for key, name in (("large_vocab", "large_vocab"), ("single_op", "single_op_f32_k1024_n3072"), ("moe", "moe"),
+                      ("int8", "int8")):
+        if key in extra:
+            line[name] = extra[key]
     ctx.close()
     print(json.dumps(line), flush=True)
 

@@ -1,7 +1,9 @@
 """GatherBlockQuantized on the GPU against the oracle, bit-exactly, over the kernel's variants:
 4-byte and 1-byte row units, one or several quantization blocks per thread, vector or scalar
 stores; u8 and s8 data; no, packed (u8 / s8) and float zero points; f32, f16 and bf16 scales;
-negative ids (counted from the end). Seeds and shapes are printed before each case."""
+negative ids (counted from the end); s64 and s32 ids; and the multi-slice kernel of rows of whole
+256-byte slices (4- and 8-bit data, no or packed zero points, slice counts that leave the last
+wavefront partly empty). Seeds and shapes are printed before each case."""
 
 import zlib
 
@@ -25,6 +27,11 @@ CASES = [
     (8, 30, 12, 3, "u8", "u8", "f16", (11,)),          # rows of 24 bytes out: scalar stores
     (2, 64, 64, 16, "u8", "u8", "f16", (9, 7)),        # q2, bs 16: 32-byte stores
     (2, 16, 4, 1, "u8", None, "f32", (5,)),
+    # rows of whole 256-byte slices: several slices per wavefront
+    (8, 200, 256, 8, "u8", "u8", "bf16", (13,), np.int32),   # q8, 13 slices: a partial last wavefront
+    (4, 100, 768, 48, "s8", "s8", "f32", (7, 3), np.int32),  # 3 slices per row, signed data and zero points
+    (8, 64, 512, 16, "s8", None, "f16", (5,)),               # q8 signed, no zero points
+    (4, 500, 256, 16, "u8", None, "bf16", (1,)),             # one id, one slice
 ]
 
 
@@ -33,9 +40,11 @@ def _scales(rng, shape, dtype):
     return o.bf16_round(s) if dtype == "bf16" else s.astype(np.float16 if dtype == "f16" else np.float32)
 
 
-@pytest.mark.parametrize("case", CASES, ids=lambda c: "b{}_r{}_B{}_blk{}_{}_{}_{}".format(*c[:7]))
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "b{}_r{}_B{}_blk{}_{}_{}_{}".format(*c[:7]) +
+                         ("_ids32" if len(c) > 8 else ""))
 def test_gather_matches_oracle(ctx, case):
-    bits, rows, row_bytes, blocks, dtype, zp, sdt, ids_shape = case
+    bits, rows, row_bytes, blocks, dtype, zp, sdt, ids_shape = case[:8]
+    ids_dtype = case[8] if len(case) > 8 else np.int64
     print(f"gather {case}", flush=True)
     rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
     data = rng.integers(0, 256, (rows, row_bytes), dtype=np.uint8)
@@ -50,7 +59,7 @@ def test_gather_matches_oracle(ctx, case):
     else:
         zero = rng.integers(0, 256, (rows, zrow), dtype=np.uint8)
         zero = zero.view(np.int8) if zp == "s8" else zero
-    ids = rng.integers(-rows, rows, ids_shape, dtype=np.int64)
+    ids = rng.integers(-rows, rows, ids_shape, dtype=np.int64).astype(ids_dtype)
     node = NodeProto(op_type="GatherBlockQuantized", input=["data", "ids", "scales"] + (["zp"] if zp else []),
                      output=["out"], attribute=[AttributeProto(name="bits", type=ATTR_INT, i=bits)])
     sc_in = ctx.put(scales, sdt) if sdt == "bf16" else ctx.put(scales)

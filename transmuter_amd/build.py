@@ -44,11 +44,12 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-# Per-file flags. The decode GEMV's kernels take their leading arguments preloaded into SGPRs at
-# wave launch (gfx950 kernarg preloading), so a wavefront's first loads do not wait on a
-# kernel-argument fetch (0.38 us of a 2.8 us launch at the Qwen3-0.6B projection shapes).
-EXTRA = {"tmh_gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
-         "tmh_bench.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"]}
+# Per-file flags. The decode GEMV's kernels (and the gather, DequantizeLinear and MatMulInteger
+# kernels) take their leading arguments preloaded into SGPRs at wave launch (gfx950 kernarg
+# preloading), so a wavefront's first loads do not wait on a kernel-argument fetch (0.38 us of a
+# 2.8 us launch at the Qwen3-0.6B projection shapes).
+PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=8"]
+EXTRA = {"tmh_gemv.hip": PRELOAD, "tmh_bench.hip": PRELOAD, "tmh_quant_ops.hip": PRELOAD}
 
 
 def _compile(src: str) -> str:

@@ -137,6 +137,135 @@ void launch_gather_ub(const uint8_t* data, bool sgn, int64_t rows, int64_t row_b
                                                                    blocks, bs, zp, zp_dt, zrow, out, un);
 }
 
+// Rows of whole 256-byte slices (row_bytes % 256 == 0), 4 bytes per lane in one quantization
+// block, 16-byte-aligned output: each wavefront takes S consecutive (id, slice) pairs. Its ids
+// are wavefront-uniform (scalar loads, one cache line for all of them), and the data, scale and
+// zero point loads of all S slices issue before the first value is computed, so a wavefront pays
+// the id latency and the row latency once for S slices instead of once per half row. Each
+// slice's values leave as one 16-byte store per lane (1 KiB contiguous per instruction). A
+// slice past the end (the last wavefront's) stores to an offset beyond the output buffer's
+// range, which the hardware drops: no branch, so no slice's loads wait behind another's stores.
+template <int DT, int BITS, int S, bool IDS64, bool HAS_ZP>
+__global__ __launch_bounds__(256) void k_gather_bq_rows(
+    const uint8_t* __restrict__ data, bool data_signed, uint32_t rows, uint32_t row_bytes,
+    const void* __restrict__ ids, uint32_t n_slices, uint32_t slices_per_row, const void* __restrict__ scales,
+    uint32_t blocks, uint32_t bs_shift, const uint8_t* __restrict__ zp, bool zp_signed, uint32_t zrow,
+    void* __restrict__ out) {
+  constexpr int PER = 8 / BITS;
+  constexpr int V = 4 * PER;  // values per lane and slice
+  constexpr int ES = DT == DT_F32 ? 4 : 2;
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const uint32_t s0 = wave * S;
+  if (s0 >= n_slices) return;
+  const uint32_t D = row_bytes * PER;
+  const auto d_rsrc = buffer_rsrc(data, rows * row_bytes);
+  const auto s_rsrc = buffer_rsrc(scales, rows * blocks * ES);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? rows * zrow : 0u);
+  const auto o_rsrc = buffer_rsrc(out, (n_slices / slices_per_row) * D * ES);
+  // The rows of the S slices first (lane j loads slice j's id, one vector load, then each row
+  // is broadcast from its lane), then every data, scale and zero point load, then the values.
+  const uint32_t my_sl = s0 + (lane < S ? lane : S - 1) < n_slices ? s0 + (lane < S ? lane : S - 1) : n_slices - 1;
+  int64_t my_id;
+  if constexpr (IDS64) my_id = static_cast<const int64_t*>(ids)[my_sl / slices_per_row];
+  else my_id = static_cast<const int32_t*>(ids)[my_sl / slices_per_row];
+  my_id = my_id < 0 ? my_id + rows : my_id;  // ONNX: a negative index counts from the end
+  const uint32_t my_row = static_cast<uint32_t>(my_id < 0 ? 0 : (my_id >= rows ? rows - 1 : my_id));
+  uint32_t row[S];
+#pragma unroll
+  for (int j = 0; j < S; ++j) row[j] = __builtin_amdgcn_readlane(my_row, j);
+  uint32_t x[S], sv[S], zv[S];
+  uint32_t bit[S];
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const uint32_t sl = s0 + j < n_slices ? s0 + j : n_slices - 1;
+    const uint32_t i = sl / slices_per_row;
+    const uint32_t r = row[j];
+    const uint32_t byte = (sl - i * slices_per_row) * 256 + lane * 4;
+    const uint32_t blk = (byte * PER) >> bs_shift;
+    x[j] = __builtin_amdgcn_raw_buffer_load_b32(d_rsrc, r * row_bytes + byte, 0, 0);
+    if constexpr (ES == 4) sv[j] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, (r * blocks + blk) * 4, 0, 0);
+    else sv[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, (r * blocks + blk) * 2, 0, 0);
+    bit[j] = blk * BITS;
+    if constexpr (HAS_ZP) zv[j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, r * zrow + bit[j] / 8, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const uint32_t sl = s0 + j;
+    const uint32_t i = sl / slices_per_row;
+    float z;
+    if constexpr (HAS_ZP) {
+      int zq;
+      if constexpr (BITS == 8) {
+        zq = zp_signed ? static_cast<int>(static_cast<int8_t>(zv[j])) : static_cast<int>(zv[j] & 0xFFu);
+      } else {
+        zq = (zv[j] >> (bit[j] % 8)) & ((1 << BITS) - 1);
+        if (zp_signed && zq >= (1 << (BITS - 1))) zq -= (1 << BITS);
+      }
+      z = static_cast<float>(zq);
+    } else {
+      z = data_signed ? 0.f : static_cast<float>(1 << (BITS - 1));
+    }
+    float sc;
+    if constexpr (DT == DT_F32) sc = __builtin_bit_cast(float, sv[j]);
+    else if constexpr (DT == DT_F16) sc = f16_bits_to_f32(static_cast<uint16_t>(sv[j]));
+    else sc = bf16_bits_to_f32(static_cast<uint16_t>(sv[j]));
+    float vals[V];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t byte = (x[j] >> (8 * b)) & 0xFFu;
+#pragma unroll
+      for (int v = 0; v < PER; ++v) {
+        int q;
+        if constexpr (BITS == 8) {
+          q = data_signed ? static_cast<int>(static_cast<int8_t>(byte)) : static_cast<int>(byte);
+        } else {
+          q = (byte >> (v * BITS)) & ((1 << BITS) - 1);
+          if (data_signed && q >= (1 << (BITS - 1))) q -= (1 << BITS);
+        }
+        vals[b * PER + v] = dequant_value<DT>(static_cast<float>(q), z, sc);
+      }
+    }
+    uint32_t words[V * ES / 4];
+#pragma unroll
+    for (int k = 0; k < V * ES / 4; ++k) {
+      if constexpr (DT == DT_F32) {
+        words[k] = __builtin_bit_cast(uint32_t, vals[k]);
+      } else if constexpr (DT == DT_F16) {
+        words[k] = f32_to_f16_bits(vals[2 * k]) | (static_cast<uint32_t>(f32_to_f16_bits(vals[2 * k + 1])) << 16);
+      } else {
+        words[k] = f32_to_bf16_bits(vals[2 * k]) | (static_cast<uint32_t>(f32_to_bf16_bits(vals[2 * k + 1])) << 16);
+      }
+    }
+    const uint32_t o = (i * D + ((sl - i * slices_per_row) * 256 + lane * 4) * PER) * ES;
+    const uint32_t off = sl < n_slices ? o : 0xFFFFFF00u;  // past the range: dropped
+    if constexpr (V * ES == 8) {  // 8-bit values in a 2-byte type: 8 bytes per lane
+      typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+      __builtin_amdgcn_raw_buffer_store_b64(uint2_t{words[0], words[1]}, o_rsrc, off, 0, 0);
+    } else {
+#pragma unroll
+      for (int k = 0; k < V * ES / 16; ++k)
+        __builtin_amdgcn_raw_buffer_store_b128(uint4_t{words[4 * k], words[4 * k + 1], words[4 * k + 2], words[4 * k + 3]},
+                                               o_rsrc, off + 16 * k, 0, 0);
+    }
+  }
+}
+
+template <int DT, int BITS, bool IDS64, bool HAS_ZP>
+void launch_gather_rows(const uint8_t* data, bool sgn, int64_t rows, int64_t row_bytes, const void* ids,
+                        int64_t n_ids, const void* scales, int64_t blocks, int64_t bs, const void* zp,
+                        bool zp_signed, int64_t zrow, void* out, hipStream_t s) {
+  constexpr int S = 4;
+  const int64_t spr = row_bytes / 256, n_slices = n_ids * spr;
+  int shift = 0;
+  while ((int64_t(1) << shift) < bs) ++shift;
+  const int64_t waves = (n_slices + S - 1) / S;
+  k_gather_bq_rows<DT, BITS, S, IDS64, HAS_ZP><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, s>>>(
+      data, sgn, static_cast<uint32_t>(rows), static_cast<uint32_t>(row_bytes), ids, static_cast<uint32_t>(n_slices),
+      static_cast<uint32_t>(spr), scales, static_cast<uint32_t>(blocks), static_cast<uint32_t>(shift),
+      static_cast<const uint8_t*>(zp), zp_signed, static_cast<uint32_t>(zrow), out);
+}
+
 template <int DT, int BITS>
 void launch_gather(const uint8_t* data, bool sgn, int64_t rows, int64_t row_bytes, const void* ids,
                    bool ids64, int64_t n_ids, const void* scales, int64_t blocks, int64_t bs,
@@ -149,6 +278,21 @@ void launch_gather(const uint8_t* data, bool sgn, int64_t rows, int64_t row_byte
   if (vec) {
     const bool one = bs % (4 * PER) == 0;
     const bool vec_out = reinterpret_cast<uintptr_t>(out) % 16 == 0 && (D * ES) % 16 == 0;
+    // Whole 256-byte slices, power-of-two blocks, no or packed zero points and 32-bit offsets:
+    // several slices per wavefront.
+    const bool packed_zp = zp && (zp_dt == TMH_U8 || zp_dt == TMH_S8);
+    if constexpr (BITS != 2) {
+      if (one && vec_out && row_bytes % 256 == 0 && (bs & (bs - 1)) == 0 && (!zp || packed_zp) &&
+          rows * row_bytes < (int64_t(1) << 32) && rows * blocks * ES < (int64_t(1) << 32) &&
+          rows * zrow < (int64_t(1) << 32) && n_ids * D * ES < (int64_t(1) << 32) - 256) {
+        const bool zs = zp_dt == TMH_S8;
+        if (ids64 && zp) launch_gather_rows<DT, BITS, true, true>(data, sgn, rows, row_bytes, ids, n_ids, scales, blocks, bs, zp, zs, zrow, out, s);
+        else if (ids64) launch_gather_rows<DT, BITS, true, false>(data, sgn, rows, row_bytes, ids, n_ids, scales, blocks, bs, zp, zs, zrow, out, s);
+        else if (zp) launch_gather_rows<DT, BITS, false, true>(data, sgn, rows, row_bytes, ids, n_ids, scales, blocks, bs, zp, zs, zrow, out, s);
+        else launch_gather_rows<DT, BITS, false, false>(data, sgn, rows, row_bytes, ids, n_ids, scales, blocks, bs, zp, zs, zrow, out, s);
+        return;
+      }
+    }
     if (one)
       launch_gather_ub<DT, BITS, 4, true>(data, sgn, rows, row_bytes, ids, ids64, n_ids, scales, blocks, bs, zp, zp_dt,
                                           zrow, out, units, vec_out, s);
