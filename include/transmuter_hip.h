@@ -168,6 +168,19 @@ int tmh_pack_nbits_host(const uint8_t* h_b, size_t b_bytes, const void* h_scales
                         size_t* scale_bytes, void* h_zero, size_t* zero_bytes);
 
 /*
+ * tmh_weight_upload_nbits from device buffers: B, the scales and the zero points already on the
+ * device (the inputs of a MatMulNBits node that move/2 did not rewrite, whose weights the
+ * reference dequantizes on the device at every call, quantized.ex:39-42 and :234-240). The same
+ * arguments and checks (d_* are device pointers of the sizes given), the same device bytes as
+ * the host packing; the repacking runs on `stream` (NULL: the context's) and the weight may be
+ * used by later work on that stream at once. Free with tmh_weight_free after that work is done.
+ */
+int tmh_weight_pack_nbits(tmh_ctx* ctx, const void* d_b, size_t b_bytes, const void* d_scales, int scales_dtype,
+                          size_t scales_count, const void* d_zero_points, int zp_kind, int zp_dtype, size_t zp_count,
+                          int64_t K, int64_t N, int bits, int block_size, int weight_dtype, void* stream,
+                          tmh_weight** out);
+
+/*
  * One weight whose rows are the rows of parts[0], then parts[1], ...: the packed form of the
  * weight concatenation of Fusion.matmuls/2 (lib/transmuter/fusion.ex:430-539), which merges
  * the MatMulNBits that read one input (q/k/v, gate/up) into one matmul over [sum N, K]. The

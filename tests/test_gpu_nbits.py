@@ -64,6 +64,48 @@ def test_dequantize_bit_exact(ctx, case):
     w.free()
 
 
+@pytest.mark.parametrize("case", DEQUANT_CASES, ids=lambda c: "b{}_bs{}_{}_K{}_N{}_{}_{}".format(*c))
+def test_device_packing_equals_host_packing(ctx, case):
+    """tmh_weight_pack_nbits repacks B, scales and zero points that are already on the device;
+    the weight must be the host packing's, bit for bit: the same dequantized values and the same
+    products."""
+    bits, bs, zp, k, n, sdt, wdt = case
+    print(f"device packing {case}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()) + 1)
+    b, s32, z = nbits_weight(rng, k, n, bits, bs, zp=zp, scale_dtype=np.float32)
+    scales = host_float(s32, sdt)
+    host = PackedWeight.upload(ctx, b, scales, z, k=k, n=n, bits=bits, block_size=bs, weight_dtype=wdt,
+                               scales_dtype=sdt)
+    dev = PackedWeight.pack_device(ctx, ctx.put(b), ctx.put(scales, sdt), None if z is None else ctx.put(z), k=k, n=n,
+                                   bits=bits, block_size=bs, weight_dtype=wdt)
+    assert np.array_equal(dev.dequantize().numpy().view(np.uint8), host.dequantize().numpy().view(np.uint8))
+    adt = "f16" if wdt == "f16" else "f32"
+    a = ctx.put(rng.standard_normal((3, k)).astype(NP[adt]))
+    assert np.array_equal(matmul_nbits(a, dev).numpy().view(np.uint8), matmul_nbits(a, host).numpy().view(np.uint8))
+    host.free()
+    dev.free()
+
+
+def test_in_graph_matmul_nbits_packs_on_the_device(ctx):
+    """A MatMulNBits node that move/2 did not rewrite, with B on the device and small host scales
+    and zero points (static values), runs through the device packing and matches the oracle."""
+    from transmuter_amd import quantized
+    from transmuter_amd.onnx_wire import ATTR_INT, AttributeProto, NodeProto
+
+    print("in-graph MatMulNBits, device B", flush=True)
+    rng = np.random.default_rng(77)
+    k, n, bits, bs = 512, 48, 4, 32
+    b, s, z = nbits_weight(rng, k, n, bits, bs)
+    attrs = [AttributeProto(name=name, type=ATTR_INT, i=v) for name, v in (("K", k), ("N", n), ("bits", bits),
+                                                                              ("block_size", bs))]
+    node = NodeProto(op_type="MatMulNBits", input=["a", "b", "s", "z"], output=["y"], attribute=attrs)
+    a = rng.standard_normal((2, 3, k)).astype(np.float16)
+    (y,) = quantized.apply(node, [ctx.put(a), ctx.put(b), s, z])
+    ref = o.matmul_nbits(a, b, s, z, k=k, n=n, bits=bits, block_size=bs).astype(np.float64)
+    assert y.shape == (2, 3, n) and y.dtype == "f16"
+    assert rel_err(y.numpy().astype(np.float64), ref) <= TOL["f16"]
+
+
 MATMUL_CASES = [
     # bits, block, zp, K, N, M list, A type, scale type, bias
     (4, 32, "packed", 1024, 96, [1, 2, 5, 16, 17, 31, 33, 64, 65, 130], "f16", "f16", None),

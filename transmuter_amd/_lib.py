@@ -56,6 +56,8 @@ SIGNATURES = {
     "tmh_weight_upload_nbits": (_i, [_vp, _vp, _sz, _vp, _i, _sz, _vp, _i, _i, _sz, _i64, _i64, _i, _i, _i,
                                      ctypes.POINTER(_vp)]),
     "tmh_weight_free": (None, [_vp]),
+    "tmh_weight_pack_nbits": (_i, [_vp, _vp, _sz, _vp, _i, _sz, _vp, _i, _i, _sz, _i64, _i64, _i, _i, _i, _vp,
+                                   ctypes.POINTER(_vp)]),
     "tmh_pack_nbits_host": (_i, [_vp, _sz, _vp, _i, _sz, _vp, _i, _i, _sz, _i64, _i64, _i, _i, _i,
                                  _vp, ctypes.POINTER(_sz), _vp, ctypes.POINTER(_sz), _vp, ctypes.POINTER(_sz)]),
     "tmh_weight_info": (_i, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i),

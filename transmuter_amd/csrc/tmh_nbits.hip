@@ -1219,6 +1219,73 @@ __global__ __launch_bounds__(256) void k_concat_tiles(ConcatParts parts, uint8_t
   }
 }
 
+// The tiled layout of a weight from its ONNX layout on the device (the same bytes fill_nbits
+// writes on the host). k_pack_tiles: lane-slot (t, c, l) takes row 16t + l%16, bytes
+// 64c + 16(l/16) .. +15 of B (zeros past the row or past N), each 32-bit word reordered so that
+// value 2j sits at bits j*bits and value 2j+1 at 16 + j*bits.
+__global__ __launch_bounds__(256) void k_pack_tiles(const uint8_t* __restrict__ b, int64_t N, int64_t row_bytes,
+                                                    int64_t nchunks, int bits, uint4_t* __restrict__ q,
+                                                    int64_t lanes_total) {
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= lanes_total) return;
+  const int l = static_cast<int>(id & 63);
+  const int64_t tc = id >> 6;
+  const int64_t t = tc / nchunks, c = tc - t * nchunks;
+  const int64_t n = t * 16 + (l & 15);
+  const int64_t off = c * kChunkBytes + (l >> 4) * 16;
+  uint4_t v = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int wd = 0; wd < 4; ++wd) {
+    uint32_t x = 0;
+    if (n < N && off + 4 * wd < row_bytes)  // rows are whole words: block bytes are multiples of 4
+      x = *reinterpret_cast<const uint32_t*>(b + n * row_bytes + off + 4 * wd);
+    if (bits != 8) {
+      const int count = 32 / bits;
+      const uint32_t mask = (1u << bits) - 1u;
+      uint32_t out = 0;
+      for (int i = 0; i < count; ++i) out |= ((x >> (i * bits)) & mask) << ((i & 1) * 16 + (i >> 1) * bits);
+      x = out;
+    }
+    v[wd] = x;
+  }
+  q[id] = v;
+}
+
+// k_pack_params: entry (t, c, j, r) holds block (c*CW + j*bsc) / block_size of row 16t + r: the
+// scale rounded to the weight type, the packed zero point as one byte, or a float zero point
+// rounded to the weight type (kept as f32); entries past N or past the blocks hold scale 0 and
+// zero point 2^(bits-1) (0 for float zero points).
+template <int WDT>
+__global__ __launch_bounds__(256) void k_pack_params(const void* __restrict__ scales, int scales_dt,
+                                                     const void* __restrict__ zp, int zp_kind, int zp_dt, int64_t N,
+                                                     int64_t blocks, int64_t zrow, int bits, int block_size,
+                                                     int64_t nchunks, int nbc, int cw, int bsc, void* __restrict__ scale,
+                                                     void* __restrict__ zero, int64_t entries) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= entries) return;
+  const int r = static_cast<int>(e & 15);
+  const int64_t tcj = e >> 4;
+  const int j = static_cast<int>(tcj % nbc);
+  const int64_t tc = tcj / nbc;
+  const int64_t t = tc / nchunks, c = tc - t * nchunks;
+  const int64_t n = t * 16 + r;
+  const int64_t blk = (c * cw + static_cast<int64_t>(j) * bsc) / block_size;
+  const bool valid = n < N && blk < blocks;
+  const float sv = valid ? round_to<WDT>(load_float_rt(scales, scales_dt, n * blocks + blk)) : 0.0f;
+  store_as<WDT>(scale, e, sv);
+  if (zp_kind == TMH_ZP_PACKED) {
+    uint8_t z = static_cast<uint8_t>(1 << (bits - 1));
+    if (valid) {
+      const int64_t bit = blk * bits;
+      const uint8_t byte = static_cast<const uint8_t*>(zp)[n * zrow + bit / 8];
+      z = bits == 8 ? byte : static_cast<uint8_t>((byte >> (bit % 8)) & ((1 << bits) - 1));
+    }
+    static_cast<uint8_t*>(zero)[e] = z;
+  } else if (zp_kind == TMH_ZP_FLOAT) {
+    static_cast<float*>(zero)[e] = valid ? round_to<WDT>(load_float_rt(zp, zp_dt, n * blocks + blk)) : 0.0f;
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -1289,6 +1356,63 @@ int tmh_weight_upload_nbits(tmh_ctx* ctx, const uint8_t* h_b, size_t b_bytes, co
     return st;
   }
   w->device_bytes = q.size() + scale.size() + zero.size();
+  *out = w;
+  return TMH_OK;
+}
+
+int tmh_weight_pack_nbits(tmh_ctx* ctx, const void* d_b, size_t b_bytes, const void* d_scales, int scales_dtype,
+                          size_t scales_count, const void* d_zero_points, int zp_kind, int zp_dtype, size_t zp_count,
+                          int64_t K, int64_t N, int bits, int block_size, int weight_dtype, void* stream,
+                          tmh_weight** out) {
+  if (!ctx) return fail(nullptr, TMH_ERR_INVALID, "the context is NULL");
+  if (!out) return fail(ctx, TMH_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  PackPlan p;
+  TMH_TRY(plan_nbits(ctx, static_cast<const uint8_t*>(d_b), b_bytes, d_scales, scales_dtype, scales_count,
+                     d_zero_points, zp_kind, zp_dtype, zp_count, K, N, bits, block_size, weight_dtype, &p));
+  TMH_TRY(use_device(ctx));
+  hipStream_t s = pick_stream(ctx, stream);
+  tmh_weight* w = new tmh_weight();
+  w->device = ctx->device;
+  w->K = p.K;
+  w->N = p.N;
+  w->bits = p.bits;
+  w->block_size = p.block_size;
+  w->blocks = p.blocks;
+  w->row_bytes = p.row_bytes;
+  w->nchunks = p.nchunks;
+  w->ntiles = p.ntiles;
+  w->nbc = p.nbc;
+  w->wdtype = p.wdtype;
+  w->zp_kind = p.zp_kind;
+  int st = check_hip(ctx, hipMalloc(reinterpret_cast<void**>(&w->d_q), p.q_bytes), "hipMalloc (weight)");
+  if (st == TMH_OK) st = check_hip(ctx, hipMalloc(&w->d_scale, p.scale_bytes), "hipMalloc (weight)");
+  if (st == TMH_OK && p.zero_bytes) st = check_hip(ctx, hipMalloc(&w->d_zero, p.zero_bytes), "hipMalloc (weight)");
+  if (st != TMH_OK) {
+    tmh_weight_free(w);
+    return st;
+  }
+  const int64_t lanes = p.ntiles * p.nchunks * 64;
+  k_pack_tiles<<<static_cast<unsigned>((lanes + 255) / 256), 256, 0, s>>>(
+      static_cast<const uint8_t*>(d_b), p.N, p.row_bytes, p.nchunks, p.bits, reinterpret_cast<uint4_t*>(w->d_q), lanes);
+  const int64_t entries = p.ntiles * p.nchunks * p.nbc * 16;
+  const unsigned pgrid = static_cast<unsigned>((entries + 255) / 256);
+#define TMH_PACK_PARAMS(WDT)                                                                                        \
+  k_pack_params<WDT><<<pgrid, 256, 0, s>>>(d_scales, scales_dtype, d_zero_points, p.zp_kind, zp_dtype, p.N, p.blocks, \
+                                           p.zrow, p.bits, p.block_size, p.nchunks, p.nbc, p.cw, p.bsc, w->d_scale,  \
+                                           w->d_zero, entries)
+  switch (p.wdtype) {
+    case TMH_F16: TMH_PACK_PARAMS(DT_F16); break;
+    case TMH_BF16: TMH_PACK_PARAMS(DT_BF16); break;
+    default: TMH_PACK_PARAMS(DT_F32);
+  }
+#undef TMH_PACK_PARAMS
+  st = check_launch(ctx, "k_pack_tiles/k_pack_params");
+  if (st != TMH_OK) {
+    tmh_weight_free(w);
+    return st;
+  }
+  w->device_bytes = p.q_bytes + p.scale_bytes + p.zero_bytes;
   *out = w;
   return TMH_OK;
 }

@@ -76,6 +76,26 @@ class PackedWeight:
         return cls(ctx, handle, k, n, bits, block_size, weight_dtype, zp_kind)
 
     @classmethod
+    def pack_device(cls, ctx: Context, b: DeviceTensor, scales: DeviceTensor, zero_points: DeviceTensor | None, *,
+                    k: int, n: int, bits: int, block_size: int, weight_dtype: str, stream=None) -> "PackedWeight":
+        """The weight of `upload` from buffers already on the device (tmh_weight_pack_nbits): B,
+        scales and zero points in their ONNX layouts, repacked by a device kernel on `stream`."""
+        if weight_dtype not in FLOAT_TYPES:
+            raise ValueError(f"weight type must be one of {FLOAT_TYPES}, got {weight_dtype}")
+        if b.dtype != "u8":
+            raise _lib.TmhArgumentError(_lib.ERR_INVALID, f"MatMulNBits B must be u8 bytes, got {b.dtype}")
+        if zero_points is None:
+            zp_kind, zp_code, zp_ptr, zp_count = _lib.ZP_NONE, _lib.U8, None, 0
+        else:
+            zp_kind = _lib.ZP_FLOAT if zero_points.dtype in FLOAT_TYPES else _lib.ZP_PACKED
+            zp_code, zp_ptr, zp_count = zero_points.tmh_dtype, zero_points.ptr, zero_points.size
+        handle = ctypes.c_void_p()
+        ctx.check(lib().tmh_weight_pack_nbits(ctx.handle, b.ptr, b.nbytes, scales.ptr, scales.tmh_dtype, scales.size,
+                                              zp_ptr, zp_kind, zp_code, zp_count, k, n, bits, block_size,
+                                              NX_TO_TMH[weight_dtype], stream, ctypes.byref(handle)))
+        return cls(ctx, handle, k, n, bits, block_size, weight_dtype, zp_kind)
+
+    @classmethod
     def concat(cls, parts: list["PackedWeight"]) -> "PackedWeight":
         """One weight with the rows of every part in order (tmh_weight_concat_nbits): the
         concatenation of Fusion.matmuls/2 (lib/transmuter/fusion.ex:430-539), kept packed."""

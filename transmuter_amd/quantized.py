@@ -104,7 +104,7 @@ def _device(ctx: Context, x, dtype: str | None = None) -> tuple[DeviceTensor | N
         return None, False
     if isinstance(x, DeviceTensor):
         return x, False
-    return ctx.put(np.asarray(x), dtype), True
+    return ctx.put(x if isinstance(x, np.ndarray) else np.asarray(x), dtype), True
 
 
 def _ptr_offset(t: DeviceTensor, elements: int) -> ctypes.c_void_p:
@@ -156,14 +156,30 @@ def _op_matmul_nbits(node, inputs):
     # B given as an {N, K} weight (a moved model) needs no unpacking (quantized.ex:38-42).
     if isinstance(b, PackedWeight) and b.shape == (n, k):
         return matmul_nbits(a, b, bias)
-    # In the graph, the weights dequantize in A's type (quantized.ex:42).
-    w = PackedWeight.upload(a.ctx, b, scales, zero_points, k=k, n=n, bits=bits, block_size=block_size,
-                            weight_dtype=a.dtype)
+    # In the graph, the weights dequantize in A's type (quantized.ex:42), at every call and on the
+    # device: a B that lives there is repacked by a device kernel (small host-side scales and zero
+    # points, static values in the reference, are copied up first); a host B is packed on the host.
+    ctx = a.ctx
+    temps = []
+    if isinstance(b, DeviceTensor):
+        parts = []
+        for x in (scales, zero_points):
+            t, own = _device(ctx, x)
+            parts.append(t)
+            if own:
+                temps.append(t)
+        w = PackedWeight.pack_device(ctx, b, parts[0], parts[1], k=k, n=n, bits=bits, block_size=block_size,
+                                     weight_dtype=a.dtype)
+    else:
+        w = PackedWeight.upload(ctx, b, scales, zero_points, k=k, n=n, bits=bits, block_size=block_size,
+                                weight_dtype=a.dtype)
     try:
         return matmul_nbits(a, w, bias)
     finally:
-        a.ctx.synchronize()
+        ctx.synchronize()
         w.free()
+        for t in temps:
+            t.free()
 
 
 # ---------------------------------------------------------------- GatherBlockQuantized
