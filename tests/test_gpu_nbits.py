@@ -126,6 +126,13 @@ MATMUL_CASES = [
     (4, 128, "packed", 2048, 2048, [256, 300], "f16", "f16", None),
     (4, 128, "packed", 2048, 1000, [260], "f16", "f16", "f16"),
     (8, 64, "none", 1024, 520, [100], "f16", "f16", "f32"),
+    # decode GEMVs with K not a multiple of a chunk (128 q4 / 64 q8 values): the last chunk's A
+    # reads must stop at K, also for rows of A followed by other rows
+    (4, 32, "packed", 200, 40, [1, 5, 16], "f16", "f16", None),
+    (8, 32, "packed", 72, 24, [2, 9], "f16", "f16", None),
+    (4, 16, "none", 1000, 56, [3, 12], "f16", "f16", None),
+    (4, 32, "packed", 200, 40, [1, 3, 4], "f32", "f32", None),
+    (8, 32, "none", 1000, 24, [2, 4], "f32", "f32", None),
     # K beyond one round of wavefronts: 86 and 128 chunks per row
     (4, 128, "packed", 11008, 64, [1, 20, 70], "f16", "f16", None),
     (8, 32, "packed", 8192, 24, [1, 33], "f16", "f16", "f16"),
@@ -198,7 +205,7 @@ def test_lda_ldy_strides(ctx):
     from transmuter_amd._lib import F16, lib
 
     rng = np.random.default_rng(13)
-    k, n, m, lda, ldy = 256, 32, 5, 264, 40
+    k, n, m, lda, ldy = 200, 32, 5, 264, 40  # K past the last full chunk: A's padding must not count
     b, s, z = nbits_weight(rng, k, n, 4, 32)
     w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=4, block_size=32, weight_dtype="f16")
     a_full = rng.standard_normal((m, lda)).astype(np.float16)

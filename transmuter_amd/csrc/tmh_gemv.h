@@ -18,7 +18,10 @@
 // the fragments back (XOR-swizzled by row, no barrier: a wavefront's LDS accesses stay in order).
 // At M = 16 that takes a 1024 -> 3072 launch from 3.63 to 3.25 us; at M <= 4 it costs 0.03-0.16 us.
 //
-// The arguments the first loads need come first (12 dwords): the library compiles this kernel
+// A reads stop at K (a multiple of 8): values past K in a row of A (the next row, or padding
+// when lda > K) read as zeros, since the weights' padding past K is not zero.
+//
+// The arguments the first loads need come first (13 dwords): the library compiles this kernel
 // with its leading arguments preloaded into SGPRs at wave launch, so a wavefront issues its
 // weight loads without first waiting for a kernel-argument load. Addressing is 32-bit through
 // buffer resources: rows of A past M and tiles past the weight read zeros.
@@ -33,7 +36,7 @@ namespace tmh {
 template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS>
 __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
-    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape, uint32_t K,
     _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
   constexpr int CW = 512 / BITS;   // weights per chunk row
   constexpr int GW = CW / 4;       // weights per lane per chunk
@@ -82,7 +85,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
 #pragma unroll
         for (int j = 0; j < 16 / RPI; ++j) {
           const uint32_t row = RPI * j + lane / RB, p = lane % RB;
-          const uint32_t off = (base + u < nch && row < M) ? row * lda * 2 + ((base + u) * CW + 8 * p) * 2 : 0x80000000u;
+          const uint32_t k = (base + u) * CW + 8 * p;  // K is a multiple of 8: a piece is in or past K
+          const uint32_t off = (base + u < nch && row < M && k < K) ? row * lda * 2 + k * 2 : 0x80000000u;
           rows[j] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0);
         }
         uint4_t* mine = a_lds + (wave * U + u) * 16 * RB;
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
 #pragma unroll
         for (int i = 0; i < STEPS; ++i) {
           const uint32_t k = (base + u) * CW + g * GW + 8 * i;
-          const uint32_t off = base + u < nch ? a_row + k * 2 : 0x80000000u;
+          const uint32_t off = base + u < nch && k < K ? a_row + k * 2 : 0x80000000u;
           af[u][i] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
         }
       }
@@ -150,6 +154,85 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
     } else {
       for (uint32_t e = 0; e < 4 && n + e < N; ++e) dst[e] = static_cast<_Float16>(v[e]);
     }
+  }
+}
+
+// The same GEMV over f32 A and f32 weights (the reference's CPU configuration after move/2: f32
+// scales, so W = (q - zero) * scale in f32, one rounding) for M <= MM rows, f32 Y, no bias.
+// Lane (g, r) dequantizes its 16 bytes (row r, GW consecutive k) to f32 and accumulates
+// A[m][k] * W[r][k] with f32 FMAs; the four lanes of a row add by shuffles, the wavefronts of
+// the workgroup through LDS, in a fixed order.
+template <int BITS, bool HAS_ZP, bool SPLIT, int NW, int MM>
+__global__ __launch_bounds__(64 * NW) void k_gemv_f32(
+    const uint4_t* __restrict__ qt, const float* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const float* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape, uint32_t K,
+    float* __restrict__ Y, uint32_t ldy, uint32_t N) {
+  constexpr int CW = 512 / BITS;
+  constexpr int GW = CW / 4;
+  constexpr int STEPS = GW / 8;
+  constexpr int NJ = SPLIT ? STEPS : 1;
+  __shared__ float red[NW][MM][16];
+  const uint32_t M = shape & 0xFFu, nbc = (shape >> 8) & 0xFFu, bsc_shift = shape >> 16;
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t t = blockIdx.x;
+  const uint32_t n_params = ntiles * nch * nbc * 16;
+  const auto q_rsrc = buffer_rsrc(qt, ntiles * nch * 1024);
+  const auto s_rsrc = buffer_rsrc(sc, n_params * 4);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+  const auto a_rsrc = buffer_rsrc(A, M * lda * 4);
+  float acc[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) acc[m] = 0.f;
+  for (uint32_t c = wave; c < nch; c += NW) {
+    const uint4_t w = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, (t * nch * 64 + lane) * 16, c * 1024, 0);
+    float sv[NJ], zv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t e = ((t * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
+      sv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, e * 4, 0, 0));
+      zv[j] = HAS_ZP ? static_cast<float>(__builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0))
+                     : static_cast<float>(1 << (BITS - 1));
+    }
+    // A[m][k0 .. k0 + GW) as 16-byte pieces (zeros past M or K), held as floats: with hipcc 7.2
+    // a __builtin_bit_cast of one element of an integer vector read element 0 for every index.
+    float4_t av[MM][GW / 4];
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+      for (int i = 0; i < GW / 4; ++i) {
+        const uint32_t k = c * CW + g * GW + 4 * i;
+        const uint32_t off = static_cast<uint32_t>(m) < M && k < K ? m * lda * 4 + k * 4 : 0x80000000u;
+        av[m][i] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
+      }
+    constexpr int PER_WORD = 32 / BITS;
+#pragma unroll
+    for (int e = 0; e < GW; ++e) {
+      const int j = SPLIT ? e / 8 : 0;
+      const float q = static_cast<float>(word_value<BITS>(w[e / PER_WORD], e % PER_WORD));
+      const float wv = (q - zv[j]) * sv[j];
+#pragma unroll
+      for (int m = 0; m < MM; ++m) acc[m] = fmaf(av[m][e / 4][e % 4], wv, acc[m]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    acc[m] += __shfl_xor(acc[m], 16);
+    acc[m] += __shfl_xor(acc[m], 32);
+    if (g == 0) red[wave][m][r] = acc[m];
+  }
+  __syncthreads();
+  if (wave != 0 || g != 0) return;
+  const uint32_t n = t * 16 + r;
+  if (n >= N) return;
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    if (static_cast<uint32_t>(m) >= M) break;
+    float v = red[0][m][r];
+#pragma unroll
+    for (int w2 = 1; w2 < NW; ++w2) v += red[w2][m][r];
+    Y[m * ldy + n] = v;
   }
 }
 

@@ -29,7 +29,7 @@ struct DecArgs {
   const uint16_t* sc;
   const uint8_t* zp;
   const _Float16* a;
-  uint32_t nch, ntiles, lda, shape;
+  uint32_t nch, ntiles, lda, shape, k;
   _Float16* y;
   uint32_t ldy, n;
 };
@@ -44,7 +44,7 @@ void go(const DecArgs& d, hipStream_t s) {
   static_assert(red <= kStaticLds, "partial sums exceed the static LDS");
   const unsigned grid = (d.ntiles + TN - 1) / TN;
   k_gemv_dec<BITS, HAS_ZP, SPLIT, 1, NW, TN, A_LDS><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles,
-                                                                              d.lda, d.shape, d.y, d.ldy, d.n);
+                                                                              d.lda, d.shape, d.k, d.y, d.ldy, d.n);
 }
 
 // Wavefront counts the one-shot kernels are built for: the chunk count rounded up to one of
@@ -97,7 +97,65 @@ void launch_bits(const DecArgs& d, int64_t M, int num_cus, hipStream_t s) {
     streaming<BITS, HAS_ZP, SPLIT, 2>(d, nw, s);
 }
 
+template <int BITS, bool HAS_ZP, bool SPLIT, int NW>
+void go_f32(const DecArgs& d, const float* a, float* y, hipStream_t s) {
+  k_gemv_f32<BITS, HAS_ZP, SPLIT, NW, 4><<<d.ntiles, 64 * NW, 0, s>>>(
+      d.qt, reinterpret_cast<const float*>(d.sc), d.zp, a, d.nch, d.ntiles, d.lda, d.shape, d.k, y, d.ldy, d.n);
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT>
+void launch_f32_bits(const DecArgs& d, const float* a, float* y, hipStream_t s) {
+  switch (round_waves(d.nch)) {
+    case 1: go_f32<BITS, HAS_ZP, SPLIT, 1>(d, a, y, s); break;
+    case 2: go_f32<BITS, HAS_ZP, SPLIT, 2>(d, a, y, s); break;
+    case 4: go_f32<BITS, HAS_ZP, SPLIT, 4>(d, a, y, s); break;
+    case 8: go_f32<BITS, HAS_ZP, SPLIT, 8>(d, a, y, s); break;
+    case 12: go_f32<BITS, HAS_ZP, SPLIT, 12>(d, a, y, s); break;
+    default: go_f32<BITS, HAS_ZP, SPLIT, 16>(d, a, y, s);
+  }
+}
+
+DecArgs dec_args(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy) {
+  const int cw = chunk_weights(w->bits);
+  const int bsc = std::min(w->block_size, cw);
+  int shift = 0;
+  while ((1 << shift) < bsc) ++shift;
+  return DecArgs{reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+                 static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a),
+                 static_cast<uint32_t>(w->nchunks), static_cast<uint32_t>(w->ntiles), static_cast<uint32_t>(lda),
+                 static_cast<uint32_t>(M) | (static_cast<uint32_t>(w->nbc) << 8) | (static_cast<uint32_t>(shift) << 16),
+                 static_cast<uint32_t>(w->K), static_cast<_Float16*>(y), static_cast<uint32_t>(ldy),
+                 static_cast<uint32_t>(w->N)};
+}
+
 }  // namespace
+
+bool decode_gemv_f32_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, const void* a) {
+  return M >= 1 && M <= 4 && reinterpret_cast<uintptr_t>(a) % 16 == 0 && lda % 4 == 0 && w->K % 4 == 0 &&
+         M * lda * 4 < (int64_t(1) << 31) && w->ntiles * w->nchunks * 1024 < (int64_t(1) << 31) &&
+         w->ntiles * w->nchunks * w->nbc * 16 * 4 < (int64_t(1) << 31) && ldy < (int64_t(1) << 30) &&
+         w->wdtype == TMH_F32 && w->zp_kind != TMH_ZP_FLOAT && w->ntiles < (int64_t(1) << 31);
+}
+
+void launch_decode_gemv_f32(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,
+                            hipStream_t s) {
+  const DecArgs d = dec_args(w, a, M, lda, y, ldy);
+  const bool zp = w->zp_kind == TMH_ZP_PACKED;
+  const bool split = w->block_size < chunk_weights(w->bits) / 4;
+  const auto* af = static_cast<const float*>(a);
+  auto* yf = static_cast<float*>(y);
+#define TMH_DEC32(B)                                                    \
+  if (zp && split) launch_f32_bits<B, true, true>(d, af, yf, s);        \
+  else if (zp) launch_f32_bits<B, true, false>(d, af, yf, s);           \
+  else if (split) launch_f32_bits<B, false, true>(d, af, yf, s);        \
+  else launch_f32_bits<B, false, false>(d, af, yf, s);
+  switch (w->bits) {
+    case 2: { TMH_DEC32(2) } break;
+    case 4: { TMH_DEC32(4) } break;
+    default: { TMH_DEC32(8) }
+  }
+#undef TMH_DEC32
+}
 
 bool decode_gemv_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, const void* a, const void* y) {
   return M >= 1 && M <= 16 && reinterpret_cast<uintptr_t>(a) % 16 == 0 && lda % 8 == 0 && w->K % 8 == 0 &&
@@ -109,14 +167,7 @@ bool decode_gemv_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, co
 void launch_decode_gemv(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,
                         hipStream_t s, int num_cus) {
   const int cw = chunk_weights(w->bits);
-  const int bsc = std::min(w->block_size, cw);
-  int shift = 0;
-  while ((1 << shift) < bsc) ++shift;
-  const DecArgs d{reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
-                  static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a),
-                  static_cast<uint32_t>(w->nchunks), static_cast<uint32_t>(w->ntiles), static_cast<uint32_t>(lda),
-                  static_cast<uint32_t>(M) | (static_cast<uint32_t>(w->nbc) << 8) | (static_cast<uint32_t>(shift) << 16),
-                  static_cast<_Float16*>(y), static_cast<uint32_t>(ldy), static_cast<uint32_t>(w->N)};
+  const DecArgs d = dec_args(w, a, M, lda, y, ldy);
   const bool zp = w->zp_kind == TMH_ZP_PACKED;
   const bool split = w->block_size < cw / 4;  // a lane's k-group spans several blocks
 #define TMH_DEC(B)                                                   \

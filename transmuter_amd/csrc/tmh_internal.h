@@ -98,6 +98,10 @@ float load_float(const void* p, int dt, size_t i);  // host read of a float arra
 bool decode_gemv_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, const void* a, const void* y);
 void launch_decode_gemv(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,
                         hipStream_t s, int num_cus);
+// The f32 decode GEMV (k_gemv_f32): f32 A and weights, f32 Y without bias, M <= 4.
+bool decode_gemv_f32_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, const void* a);
+void launch_decode_gemv_f32(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,
+                            hipStream_t s);
 
 // Looks up, once per device and with that device current, the device address of the scratch
 // memory tmh_matmul_nbits_noalloc uses (a failure is reported by that call).

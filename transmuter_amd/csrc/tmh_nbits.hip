@@ -1569,6 +1569,10 @@ int launch_matmul(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream
     }
     return check_launch(ctx, "k_gemv_f16/k_gemm_f16");
   }
+  if (a.a_dt == TMH_F32 && a.y_dt == TMH_F32 && !a.bias && decode_gemv_f32_ok(w, a.M, a.lda, a.ldy, a.a)) {
+    launch_decode_gemv_f32(w, a.a, a.M, a.lda, a.y, a.ldy, s);
+    return check_launch(ctx, "k_gemv_f32");
+  }
   switch (w->bits) {
     case 2: launch_general_bits<2>(w, a, s); break;
     case 4: launch_general_bits<4>(w, a, s); break;
