@@ -115,10 +115,14 @@ int tmh_copy_2d(tmh_ctx* ctx, void* d_dst, size_t dst_pitch, const void* d_src, 
 /* Blocks until the stream (NULL: the context's) has finished its work. */
 int tmh_synchronize(tmh_ctx* ctx, void* stream);
 
-/* HIP events for timing on a stream. tmh_event_elapsed waits for `end`. */
+/* HIP events on a stream: completion fences of asynchronous calls and timing. tmh_event_query
+ * sets *done to 1 when the work recorded before the event has finished, 0 otherwise, without
+ * blocking; tmh_event_synchronize blocks until it has; tmh_event_elapsed waits for `end`. */
 int tmh_event_create(tmh_ctx* ctx, void** event_out);
 int tmh_event_destroy(tmh_ctx* ctx, void* event);
 int tmh_event_record(tmh_ctx* ctx, void* event, void* stream);
+int tmh_event_query(tmh_ctx* ctx, void* event, int* done);
+int tmh_event_synchronize(tmh_ctx* ctx, void* event);
 int tmh_event_elapsed(tmh_ctx* ctx, void* start, void* end, float* ms_out);
 
 /* HIP graphs: capture the calls made on `stream` between begin and end into an executable

@@ -48,6 +48,8 @@ SIGNATURES = {
     "tmh_event_create": (_i, [_vp, ctypes.POINTER(_vp)]),
     "tmh_event_destroy": (_i, [_vp, _vp]),
     "tmh_event_record": (_i, [_vp, _vp, _vp]),
+    "tmh_event_query": (_i, [_vp, _vp, ctypes.POINTER(_i)]),
+    "tmh_event_synchronize": (_i, [_vp, _vp]),
     "tmh_event_elapsed": (_i, [_vp, _vp, _vp, ctypes.POINTER(ctypes.c_float)]),
     "tmh_graph_begin": (_i, [_vp, _vp]),
     "tmh_graph_end": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),

@@ -304,6 +304,25 @@ int tmh_event_record(tmh_ctx* ctx, void* event, void* stream) {
                    "hipEventRecord");
 }
 
+int tmh_event_query(tmh_ctx* ctx, void* event, int* done) {
+  TMH_TRY(use_device(ctx));
+  if (!event || !done) return fail(ctx, TMH_ERR_INVALID, "tmh_event_query: NULL argument");
+  const hipError_t err = hipEventQuery(static_cast<hipEvent_t>(event));
+  if (err == hipErrorNotReady) {
+    (void)hipGetLastError();
+    *done = 0;
+    return TMH_OK;
+  }
+  *done = err == hipSuccess ? 1 : 0;
+  return check_hip(ctx, err, "hipEventQuery");
+}
+
+int tmh_event_synchronize(tmh_ctx* ctx, void* event) {
+  TMH_TRY(use_device(ctx));
+  if (!event) return fail(ctx, TMH_ERR_INVALID, "tmh_event_synchronize: NULL event");
+  return check_hip(ctx, hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
+}
+
 int tmh_event_elapsed(tmh_ctx* ctx, void* start, void* end, float* ms_out) {
   TMH_TRY(use_device(ctx));
   if (!start || !end || !ms_out) return fail(ctx, TMH_ERR_INVALID, "tmh_event_elapsed: NULL");
