@@ -583,8 +583,8 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_gemv_traffic.json")
 COPY_BYTES = 256 << 20
 
 
-def profile_run(ctx, kind, steps):
-    """A short, graph-free run for rocprofv3: `decode` runs the M=1 projection sweep over one
+def profile_run(ctx, kind, steps, m=1):
+    """A short, graph-free run for rocprofv3: `decode` runs the projection sweep at M = m over one
     weight copy plus one 256 MiB device copy (the calibration of the memory counters);
     `prefill` runs the SmolLM3-3B projections at M=2048; `moe` the quantized MoE layer; `vocab`
     the lm_head MatMulNBits and the GatherBlockQuantized lookup at the 151936 x 1024 shape; `int8`
@@ -592,7 +592,7 @@ def profile_run(ctx, kind, steps):
     global USE_GRAPHS
     USE_GRAPHS = False
     if kind == "decode":
-        decode_sweep(ctx, steps, 2, 1, [1])
+        decode_sweep(ctx, steps, 2, 1, [m])
         src, dst = ctx.empty((COPY_BYTES,), "u8"), ctx.empty((COPY_BYTES,), "u8")
         from transmuter_amd._lib import lib
 
@@ -637,6 +637,47 @@ def summarize(kernel_csv, pmc_dirs):
     return "\n".join(out)
 
 
+def write_traffic(fetch_dir, write_dir):
+    """Writes the decode GEMV's HBM traffic per launch (TRAFFIC_FILE) from two rocprofv3 --pmc runs
+    of `--profile decode`, one with FETCH_SIZE and one with WRITE_SIZE. Each counter is scaled by
+    what it reads for the 256 MiB calibration copy of the same run (bytes known), and averaged
+    over every k_gemv_dec dispatch: the 7 projections run equally often."""
+    import csv
+    import glob
+
+    def read(d, counter):
+        gemv, copy = [], []
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                if "k_gemv_dec" in r["Kernel_Name"]:
+                    gemv.append(float(r["Counter_Value"]))
+                elif "copyBufferRect" in r["Kernel_Name"]:
+                    copy.append(float(r["Counter_Value"]))
+        if not gemv or not copy:
+            raise SystemExit(f"{d}: no k_gemv_dec or calibration-copy rows for {counter}")
+        return sum(gemv) / len(gemv), sum(copy) / len(copy), len(gemv)
+
+    fetch, fetch_copy, n_f = read(fetch_dir, "FETCH_SIZE")
+    write, write_copy, n_w = read(write_dir, "WRITE_SIZE")
+    copy_kib = COPY_BYTES / 1024
+    fs, ws = copy_kib / fetch_copy, copy_kib / write_copy
+    hbm = (fetch * fs + write * ws) * 1024
+    algo = sum(nbits_bytes(k, n, 1) for _, k, n in QWEN3_06B) / len(QWEN3_06B)
+    t = {"what": "HBM bytes per k_gemv_dec launch over the 7 Qwen3-0.6B q4 decode projections at M=1 "
+                 "(block 32, f16 scales, packed zero points)",
+         "fetch_scale": fs, "write_scale": ws,
+         "copy_calibration": {"bytes": COPY_BYTES, "fetch_kib": fetch_copy, "write_kib": write_copy},
+         "dispatches": {"fetch_run": n_f, "write_run": n_w},
+         "fetch_kib_per_launch": fetch, "write_kib_per_launch": write,
+         "hbm_bytes_per_launch": hbm, "algorithmic_bytes_per_launch": algo,
+         "traffic_over_algorithmic": hbm / algo}
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(t, f, indent=1)
+    print(json.dumps(t, indent=1))
+
+
 def traffic_per_launch():
     """HBM bytes per decode GEMV launch from the committed counter summary, or None."""
     if not os.path.exists(TRAFFIC_FILE):
@@ -662,9 +703,15 @@ def main():
                    help="comma list of parts to run besides the M=1 decode headline: decode (M=4/8/16 and merged), "
                         "single, prefill, vocab, moe, int8, cpu (default all)")
     p.add_argument("--profile", choices=["decode", "prefill", "moe", "vocab", "int8"], help="a short graph-free run for rocprofv3")
+    p.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="write the decode GEMV's HBM bytes per launch from two --pmc runs of --profile decode")
+    p.add_argument("--profile-m", type=int, default=1, help="rows of A for --profile decode")
     p.add_argument("--summarize", nargs="*", metavar="PATH",
                    help="print a markdown summary of rocprofv3 output: a kernel_stats.csv, then --pmc directories")
     args = p.parse_args()
+    if args.traffic:
+        write_traffic(*args.traffic)
+        return
     if args.summarize is not None:
         paths = args.summarize
         kernel_csv = paths[0] if paths and paths[0].endswith(".csv") else None
@@ -681,7 +728,7 @@ def main():
 
     ctx = Context(0)
     if args.profile:
-        profile_run(ctx, args.profile, args.steps)
+        profile_run(ctx, args.profile, args.steps, args.profile_m)
         ctx.close()
         return
     parts = {"decode", "single", "prefill", "vocab", "moe", "int8", "cpu"} if args.sections == "all" \

@@ -133,6 +133,14 @@ MATMUL_CASES = [
     (4, 16, "none", 1000, 56, [3, 12], "f16", "f16", None),
     (4, 32, "packed", 200, 40, [1, 3, 4], "f32", "f32", None),
     (8, 32, "none", 1000, 24, [2, 4], "f32", "f32", None),
+    # 16 wavefronts with A staged through LDS (M > 4), partial sums in the wavefronts' A areas:
+    # one round (16 chunks) and two rounds (24 chunks), 4- and 8-bit
+    (4, 32, "packed", 2048, 48, [6, 16], "f16", "f16", None),
+    (4, 32, "packed", 3072, 40, [8], "f16", "f16", None),
+    (8, 32, "none", 1024, 40, [12], "f16", "f16", None),
+    # block 256 over K = 104: the second chunk lies wholly past K
+    (4, 256, "packed", 104, 40, [1, 5, 16], "f16", "f16", None),
+    (4, 256, "none", 104, 24, [2], "f32", "f32", None),
     # K beyond one round of wavefronts: 86 and 128 chunks per row
     (4, 128, "packed", 11008, 64, [1, 20, 70], "f16", "f16", None),
     (8, 32, "packed", 8192, 24, [1, 33], "f16", "f16", "f16"),

@@ -49,8 +49,7 @@ def sources() -> list[str]:
 # preloading), so a wavefront's first loads do not wait on a kernel-argument fetch (0.38 us of a
 # 2.8 us launch at the Qwen3-0.6B projection shapes).
 PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=8"]
-EXTRA = {"tmh_gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"], "tmh_bench.hip": PRELOAD,
-         "tmh_quant_ops.hip": PRELOAD}
+EXTRA = {"tmh_gemv.hip": PRELOAD, "tmh_bench.hip": PRELOAD, "tmh_quant_ops.hip": PRELOAD}
 
 
 def _compile(src: str) -> str:

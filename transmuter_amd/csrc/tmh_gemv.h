@@ -15,13 +15,14 @@
 // lane loads its own four 16-byte pieces (16 rows x 4 scattered pieces per instruction, cheap
 // while few rows are real). With ALDS true (M > 4) a wavefront loads its chunk's rows as whole
 // 256-byte rows (4 rows per instruction, contiguous), writes them to its own LDS area and reads
-// the fragments back (XOR-swizzled by row, no barrier: a wavefront's LDS accesses stay in order).
+// the fragments back (XOR-swizzled by row; no barrier, as a wavefront's LDS accesses stay in order,
+// only a wavefront-scope fence against compiler reordering).
 // At M = 16 that takes a 1024 -> 3072 launch from 3.63 to 3.25 us; at M <= 4 it costs 0.03-0.16 us.
 //
 // A reads stop at K (a multiple of 8): values past K in a row of A (the next row, or padding
 // when lda > K) read as zeros, since the weights' padding past K is not zero.
 //
-// The arguments the first loads need come first (13 dwords): the library compiles this kernel
+// The arguments the first loads need come first (12 dwords): the library compiles this kernel
 // with its leading arguments preloaded into SGPRs at wave launch, so a wavefront issues its
 // weight loads without first waiting for a kernel-argument load. Addressing is 32-bit through
 // buffer resources: rows of A past M and tiles past the weight read zeros.
@@ -31,21 +32,30 @@
 
 namespace tmh {
 
-// shape = M | nbc << 8 | bsc_shift << 16: rows of A (1..16), parameter entries per row and
-// chunk, and log2 of the weights one parameter entry covers.
+// shape = M | nbc << 8 | bsc_shift << 16 | pad << 24: rows of A (1..16), parameter entries per
+// row and chunk, log2 of the weights one parameter entry covers, and (nch * CW - K) / 4, the
+// values of the last chunks past K. K travels in shape rather than as an argument of its own:
+// one more argument made a launch 0.09-0.17 us slower.
 template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS>
 __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
-    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape, uint32_t K,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
     _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
   constexpr int CW = 512 / BITS;   // weights per chunk row
   constexpr int GW = CW / 4;       // weights per lane per chunk
   constexpr int STEPS = GW / 8;    // MFMA steps per chunk
   constexpr int NJ = SPLIT ? STEPS : 1;
   constexpr int RB = CW * 2 / 16;  // 16-byte pieces per A row of a chunk
-  __shared__ float4_t red[NW > 1 ? NW * TN * 64 : 1];
-  __shared__ uint4_t a_lds[ALDS ? NW * U * 16 * RB : 1];
-  const uint32_t M = shape & 0xFFu, nbc = (shape >> 8) & 0xFFu, bsc_shift = shape >> 16;
+  // With A staged through LDS, each wavefront's partial sums go to the start of its own A area
+  // (it has read its last fragments by then), so both fit in 64 KiB also at 16 wavefronts.
+  constexpr int A_WAVE = U * 16 * RB;  // 16-byte pieces of A per wavefront
+  constexpr int RED_WAVE = ALDS ? A_WAVE : TN * 64;
+  static_assert(!ALDS || TN * 64 <= A_WAVE, "the partial sums must fit a wavefront's A area");
+  __shared__ uint4_t a_lds[ALDS ? NW * A_WAVE : 1];
+  __shared__ float4_t red_own[NW > 1 && !ALDS ? NW * TN * 64 : 1];
+  float4_t* red = ALDS ? reinterpret_cast<float4_t*>(a_lds) : red_own;
+  const uint32_t M = shape & 0xFFu, nbc = (shape >> 8) & 0xFFu, bsc_shift = (shape >> 16) & 0xFFu;
+  const uint32_t K = nch * CW - (shape >> 24) * 4;
   const int lane = threadIdx.x & 63;
   // Wavefront-uniform through readfirstlane, so chunk offsets go to the loads' scalar offset.
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -89,12 +99,16 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
           const uint32_t off = (base + u < nch && row < M && k < K) ? row * lda * 2 + k * 2 : 0x80000000u;
           rows[j] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0);
         }
-        uint4_t* mine = a_lds + (wave * U + u) * 16 * RB;
+        uint4_t* mine = a_lds + wave * A_WAVE + u * 16 * RB;
 #pragma unroll
         for (int j = 0; j < 16 / RPI; ++j) {
           const uint32_t row = RPI * j + lane / RB, p = lane % RB;
           mine[row * RB + (p ^ (row % RB))] = rows[j];
         }
+        // Lanes read pieces that other lanes of the wavefront wrote: the fence keeps the compiler
+        // from moving those reads above the writes (the LDS itself serves a wavefront in order).
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int i = 0; i < STEPS; ++i) {
           const uint32_t p = g * (GW / 8) + i;
@@ -128,8 +142,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
     }
   }
   if constexpr (NW > 1) {
+    if constexpr (ALDS) {  // the partial sums overwrite A pieces that other lanes read
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) red[(wave * TN + tn) * 64 + lane] = acc[tn];
+    for (int tn = 0; tn < TN; ++tn) red[wave * RED_WAVE + tn * 64 + lane] = acc[tn];
     __syncthreads();
   }
   if (static_cast<uint32_t>(r) >= M) return;
@@ -139,7 +157,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
       if (tn % NW != static_cast<int>(wave)) continue;
       acc[tn] = red[tn * 64 + lane];
 #pragma unroll
-      for (int w2 = 1; w2 < NW; ++w2) acc[tn] += red[(w2 * TN + tn) * 64 + lane];
+      for (int w2 = 1; w2 < NW; ++w2) acc[tn] += red[w2 * RED_WAVE + tn * 64 + lane];
     } else if (wave != 0) {
       continue;
     }
@@ -165,14 +183,15 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
 template <int BITS, bool HAS_ZP, bool SPLIT, int NW, int MM>
 __global__ __launch_bounds__(64 * NW) void k_gemv_f32(
     const uint4_t* __restrict__ qt, const float* __restrict__ sc, const uint8_t* __restrict__ zp,
-    const float* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape, uint32_t K,
+    const float* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
     float* __restrict__ Y, uint32_t ldy, uint32_t N) {
   constexpr int CW = 512 / BITS;
   constexpr int GW = CW / 4;
   constexpr int STEPS = GW / 8;
   constexpr int NJ = SPLIT ? STEPS : 1;
   __shared__ float red[NW][MM][16];
-  const uint32_t M = shape & 0xFFu, nbc = (shape >> 8) & 0xFFu, bsc_shift = shape >> 16;
+  const uint32_t M = shape & 0xFFu, nbc = (shape >> 8) & 0xFFu, bsc_shift = (shape >> 16) & 0xFFu;
+  const uint32_t K = nch * CW - (shape >> 24) * 4;
   const int lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;

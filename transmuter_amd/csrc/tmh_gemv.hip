@@ -10,10 +10,12 @@
 //    wavefront and round (U = 1), as many wavefronts as chunks (NW = nch, up to 16), one tile
 //    per workgroup. Latency-bound: more chunks per wavefront or more tiles per workgroup were
 //    0.07-0.4 us slower per launch. A is staged through LDS for M > 4.
-//  - streaming (lm_head-sized N): U = 1, NW = nch / 2 wavefronts (two rounds each), two tiles per
-//    workgroup for M <= 4 and four for M > 4, so every A fragment serves two or four tiles. On
-//    151936 x 1024 this reached 5.7-5.9 TB/s at M = 1 and 5.5 TB/s at M = 8 (plain reads of the
-//    same bytes: 6.6-6.75 TB/s); grid-stride persistent variants were 10-60% slower.
+//  - streaming (lm_head-sized N): U = 2 chunks per wavefront loaded together, NW = nch / 2
+//    wavefronts, four tiles per workgroup, so every A fragment serves four tiles. On 151936 x 1024
+//    with random weights rotating over three copies (270 MB, more than the last-level cache) this
+//    takes 16.3-16.7 us at M = 1 and 17.0 us at M = 8, 5.4-5.5 TB/s (a plain read of the packed
+//    weights streams 6.7 TB/s); U = 1 with two rounds was 17.5-19.4 us. Persistent wavefronts
+//    that double-buffer whole tiles, and scales staged through LDS with wide loads, were no faster.
 #include <algorithm>
 
 #include "tmh_gemv.h"
@@ -29,22 +31,22 @@ struct DecArgs {
   const uint16_t* sc;
   const uint8_t* zp;
   const _Float16* a;
-  uint32_t nch, ntiles, lda, shape, k;
+  uint32_t nch, ntiles, lda, shape;
   _Float16* y;
   uint32_t ldy, n;
 };
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int NW, int TN, bool ALDS>
+template <int BITS, bool HAS_ZP, bool SPLIT, int NW, int TN, bool ALDS, int U = 1>
 void go(const DecArgs& d, hipStream_t s) {
-  // The LDS-staged A needs NW * 16 rows of a chunk beside the partial sums; shapes where that
-  // exceeds the static LDS of a workgroup load A directly.
+  // The LDS-staged A needs U * 16 rows of a chunk per wavefront (the partial sums reuse that
+  // space); shapes where that exceeds the static LDS of a workgroup load A directly.
   constexpr size_t rb = (512 / BITS) * 2 / 16;
   constexpr size_t red = NW > 1 ? static_cast<size_t>(NW) * TN * 64 * 16 : 0;
-  constexpr bool A_LDS = ALDS && red + static_cast<size_t>(NW) * 16 * rb * 16 <= kStaticLds;
+  constexpr bool A_LDS = ALDS && static_cast<size_t>(NW) * U * 16 * rb * 16 <= kStaticLds;
   static_assert(red <= kStaticLds, "partial sums exceed the static LDS");
   const unsigned grid = (d.ntiles + TN - 1) / TN;
-  k_gemv_dec<BITS, HAS_ZP, SPLIT, 1, NW, TN, A_LDS><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles,
-                                                                              d.lda, d.shape, d.k, d.y, d.ldy, d.n);
+  k_gemv_dec<BITS, HAS_ZP, SPLIT, U, NW, TN, A_LDS><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles,
+                                                                              d.lda, d.shape, d.y, d.ldy, d.n);
 }
 
 // Wavefront counts the one-shot kernels are built for: the chunk count rounded up to one of
@@ -66,13 +68,13 @@ void one_shot(const DecArgs& d, int nw, hipStream_t s) {
   }
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int TN>
+template <int BITS, bool HAS_ZP, bool SPLIT>
 void streaming(const DecArgs& d, int nw, hipStream_t s) {
   switch (nw) {
-    case 1: go<BITS, HAS_ZP, SPLIT, 1, TN, false>(d, s); break;
-    case 2: go<BITS, HAS_ZP, SPLIT, 2, TN, false>(d, s); break;
-    case 4: go<BITS, HAS_ZP, SPLIT, 4, TN, false>(d, s); break;
-    default: go<BITS, HAS_ZP, SPLIT, 8, TN, false>(d, s);
+    case 1: go<BITS, HAS_ZP, SPLIT, 1, 4, false, 2>(d, s); break;
+    case 2: go<BITS, HAS_ZP, SPLIT, 2, 4, false, 2>(d, s); break;
+    case 4: go<BITS, HAS_ZP, SPLIT, 4, 4, false, 2>(d, s); break;
+    default: go<BITS, HAS_ZP, SPLIT, 8, 4, false, 2>(d, s);
   }
 }
 
@@ -88,19 +90,15 @@ void launch_bits(const DecArgs& d, int64_t M, int num_cus, hipStream_t s) {
       one_shot<BITS, HAS_ZP, SPLIT, false>(d, nw, s);
     return;
   }
-  // Streaming: two rounds of one chunk per wavefront (at most 8 wavefronts, more rounds for
-  // larger K), two or four tiles per workgroup.
-  const int nw = std::min(8, round_waves((nch + 1) / 2));
-  if (M > 4)
-    streaming<BITS, HAS_ZP, SPLIT, 4>(d, nw, s);
-  else
-    streaming<BITS, HAS_ZP, SPLIT, 2>(d, nw, s);
+  // Streaming: two chunks per wavefront loaded together (at most 8 wavefronts, more rounds for
+  // larger K), four tiles per workgroup.
+  streaming<BITS, HAS_ZP, SPLIT>(d, std::min(8, round_waves((nch + 1) / 2)), s);
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT, int NW>
 void go_f32(const DecArgs& d, const float* a, float* y, hipStream_t s) {
   k_gemv_f32<BITS, HAS_ZP, SPLIT, NW, 4><<<d.ntiles, 64 * NW, 0, s>>>(
-      d.qt, reinterpret_cast<const float*>(d.sc), d.zp, a, d.nch, d.ntiles, d.lda, d.shape, d.k, y, d.ldy, d.n);
+      d.qt, reinterpret_cast<const float*>(d.sc), d.zp, a, d.nch, d.ntiles, d.lda, d.shape, y, d.ldy, d.n);
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
@@ -115,6 +113,9 @@ void launch_f32_bits(const DecArgs& d, const float* a, float* y, hipStream_t s) 
   }
 }
 
+// (nch * CW - K) / 4: the values of the last chunks past K, in fours (K is a multiple of 4).
+int64_t pad_quads(const tmh_weight* w) { return (w->nchunks * chunk_weights(w->bits) - w->K) / 4; }
+
 DecArgs dec_args(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy) {
   const int cw = chunk_weights(w->bits);
   const int bsc = std::min(w->block_size, cw);
@@ -123,9 +124,9 @@ DecArgs dec_args(const tmh_weight* w, const void* a, int64_t M, int64_t lda, voi
   return DecArgs{reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
                  static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a),
                  static_cast<uint32_t>(w->nchunks), static_cast<uint32_t>(w->ntiles), static_cast<uint32_t>(lda),
-                 static_cast<uint32_t>(M) | (static_cast<uint32_t>(w->nbc) << 8) | (static_cast<uint32_t>(shift) << 16),
-                 static_cast<uint32_t>(w->K), static_cast<_Float16*>(y), static_cast<uint32_t>(ldy),
-                 static_cast<uint32_t>(w->N)};
+                 static_cast<uint32_t>(M) | (static_cast<uint32_t>(w->nbc) << 8) | (static_cast<uint32_t>(shift) << 16) |
+                     (static_cast<uint32_t>(pad_quads(w)) << 24),
+                 static_cast<_Float16*>(y), static_cast<uint32_t>(ldy), static_cast<uint32_t>(w->N)};
 }
 
 }  // namespace
@@ -134,7 +135,7 @@ bool decode_gemv_f32_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy
   return M >= 1 && M <= 4 && reinterpret_cast<uintptr_t>(a) % 16 == 0 && lda % 4 == 0 && w->K % 4 == 0 &&
          M * lda * 4 < (int64_t(1) << 31) && w->ntiles * w->nchunks * 1024 < (int64_t(1) << 31) &&
          w->ntiles * w->nchunks * w->nbc * 16 * 4 < (int64_t(1) << 31) && ldy < (int64_t(1) << 30) &&
-         w->wdtype == TMH_F32 && w->zp_kind != TMH_ZP_FLOAT && w->ntiles < (int64_t(1) << 31);
+         w->wdtype == TMH_F32 && w->zp_kind != TMH_ZP_FLOAT && w->ntiles < (int64_t(1) << 31) && pad_quads(w) < 256;
 }
 
 void launch_decode_gemv_f32(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,
@@ -161,7 +162,8 @@ bool decode_gemv_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, co
   return M >= 1 && M <= 16 && reinterpret_cast<uintptr_t>(a) % 16 == 0 && lda % 8 == 0 && w->K % 8 == 0 &&
          M * lda * 2 < (int64_t(1) << 31) && w->ntiles * w->nchunks * 1024 < (int64_t(1) << 31) &&
          w->ntiles * w->nchunks * w->nbc * 16 * 2 < (int64_t(1) << 31) && ldy < (int64_t(1) << 30) &&
-         (reinterpret_cast<uintptr_t>(y) & 7) == 0 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT;
+         (reinterpret_cast<uintptr_t>(y) & 7) == 0 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT &&
+         pad_quads(w) < 256;
 }
 
 void launch_decode_gemv(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,
