@@ -151,6 +151,18 @@ __device__ __forceinline__ half8_t unpack_step(const uint4_t& w, int i, half2_t 
   return out;
 }
 
+// XOR swizzle of the 16-byte pieces of LDS rows that 16 lanes read as MFMA fragments (lane r of a
+// lane group reads row r, all lanes the same piece): piece p of row r sits in slot
+// p ^ frag_swizzle<PPR>(r). The values were found by timing ds_read_b128 over candidate tables on
+// MI355X: with them a wavefront's read has no bank conflict, while p ^ r (the textbook choice)
+// spends half the LDS's active cycles on conflicts (1.7x slower). PPR = pieces per row: 16
+// (256-byte rows) or 32 use a transposed nibble of r, 8 (128-byte rows) bits 1-3 of r.
+template <int PPR>
+__device__ __forceinline__ int frag_swizzle(int r) {
+  if constexpr (PPR == 8) return (((r >> 1) & 1) << 1) | ((r >> 2) & 1) | (((r >> 3) & 1) << 2);
+  else return ((r & 3) << 2) | ((r >> 2) & 3);
+}
+
 // Raw buffer resource over `bytes` bytes: a load whose VGPR offset is at or beyond `bytes`
 // returns zeros, so tiles past N need no address clamps or selects. Every in-range access of
 // these kernels stays inside its buffer.

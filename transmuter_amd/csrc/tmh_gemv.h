@@ -15,8 +15,8 @@
 // lane loads its own four 16-byte pieces (16 rows x 4 scattered pieces per instruction, cheap
 // while few rows are real). With ALDS true (M > 4) a wavefront loads its chunk's rows as whole
 // 256-byte rows (4 rows per instruction, contiguous), writes them to its own LDS area and reads
-// the fragments back (XOR-swizzled by row; no barrier, as a wavefront's LDS accesses stay in order,
-// only a wavefront-scope fence against compiler reordering).
+// the fragments back (XOR-swizzled by row, frag_swizzle; no barrier, as a wavefront's LDS accesses
+// stay in order, only a wavefront-scope fence against compiler reordering).
 // At M = 16 that takes a 1024 -> 3072 launch from 3.63 to 3.25 us; at M <= 4 it costs 0.03-0.16 us.
 //
 // A reads stop at K (a multiple of 8): values past K in a row of A (the next row, or padding
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
 #pragma unroll
         for (int j = 0; j < 16 / RPI; ++j) {
           const uint32_t row = RPI * j + lane / RB, p = lane % RB;
-          mine[row * RB + (p ^ (row % RB))] = rows[j];
+          mine[row * RB + (p ^ frag_swizzle<RB>(row))] = rows[j];
         }
         // Lanes read pieces that other lanes of the wavefront wrote: the fence keeps the compiler
         // from moving those reads above the writes (the LDS itself serves a wavefront in order).
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
 #pragma unroll
         for (int i = 0; i < STEPS; ++i) {
           const uint32_t p = g * (GW / 8) + i;
-          af[u][i] = __builtin_bit_cast(half8_t, mine[r * RB + (p ^ (r % RB))]);
+          af[u][i] = __builtin_bit_cast(half8_t, mine[r * RB + (p ^ frag_swizzle<RB>(r))]);
         }
       } else {
 #pragma unroll

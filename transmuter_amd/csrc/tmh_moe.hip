@@ -210,11 +210,11 @@ __device__ __forceinline__ MoeItem moe_item(const int* items, int item, const in
   return MoeItem{e, offsets[e] + b * rows, min(rows, counts[e] - b * rows)};
 }
 
-// LDS slot of 16-byte piece `piece` of A row `row`: an XOR swizzle that puts the fragment reads
-// of 16 consecutive rows on distinct banks (8-bit weights: 8 pieces per row).
+// LDS slot of 16-byte piece `piece` of A row `row`: the XOR swizzle (frag_swizzle) under which
+// the fragment reads of 16 consecutive rows meet no bank conflict (8-bit weights: 8 pieces per row).
 template <int BITS>
 __device__ __forceinline__ int a_slot_moe(int row, int piece) {
-  return BITS == 8 ? (piece ^ ((row >> 1) & 7)) : (piece ^ (row & 15));
+  return piece ^ frag_swizzle<BITS == 8 ? 8 : 16>(row);
 }
 
 // Epilogue of the fast grouped product: none (the f16 sums), an activation of the sums plus the

@@ -392,10 +392,24 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* 
 #endif
 }
 
-// Slot of 16-byte piece `piece` in LDS row `row` (q4 rows hold 16 pieces, q8 rows 8).
+// Slot of 16-byte piece `piece` in LDS row `row` (q4 rows hold 16 pieces, q8 rows 8); its own
+// inverse, and a function of row % 16 only.
 template <int BITS>
 __device__ __forceinline__ int a_slot(int row, int piece) {
-  return BITS == 8 ? (piece ^ ((row >> 1) & 7)) : (piece ^ (row & 15));
+  return piece ^ frag_swizzle<BITS == 8 ? 8 : 16>(row);
+}
+
+// Four consecutive outputs of row offset `row` (columns n.., those below N) in any float type: the
+// dot type's rounding, then the bias. Kept out of line so that the GEMM epilogue's loops over its
+// accumulator tiles stay small enough to unroll (the tiles then stay in registers).
+__device__ __noinline__ void store_quad_any(float4_t v, void* Y, int y_dt, int dot_dt, const void* bias, int bias_dt,
+                                            int64_t row, int64_t n, int64_t N) {
+  for (int e = 0; e < 4 && n + e < N; ++e) {
+    float x = v[e];
+    if (dot_dt == DT_F16) x = round_to<DT_F16>(x);
+    if (bias) x += load_float_rt(bias, bias_dt, n + e);
+    store_float_rt(Y, y_dt, row + n + e, x);
+  }
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS>
@@ -411,7 +425,8 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
   constexpr int ROWB = CW * 2;           // bytes per LDS row
   constexpr int PPR = CW / 8;            // 16-byte pieces per row
   constexpr int RPI = 64 / PPR;          // rows per wavefront load instruction
-  constexpr int RW = BM / (2 * WN * KS); // A rows each wavefront brings into LDS
+  constexpr int NWAVE = 2 * WN * KS;
+  constexpr int RW = BM / NWAVE;         // A rows each wavefront brings into LDS
   // KS == 2 (BM = 128, WN = 2 only): eight wavefronts, two per SIMD; wavefronts w and w + 4 share
   // an output sub-tile and take the first and second half of each k-block's MFMA steps, and the
   // second half's partial sums add to the first's through LDS after the k-loop.
@@ -422,6 +437,10 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
   // Tall (WN == 4, eight wavefronts, two per SIMD; or BM == 128): each wavefront takes all BM
   // rows and two weight tiles, so every dequantized fragment feeds BM/16 MFMAs. BM == 256 with
   // WN == 2 (four wavefronts): 128 rows and four tiles per wavefront.
+  // Measured alternatives, none faster on the SmolLM3-3B shapes: four wavefronts each taking all
+  // 256 rows of four tiles (one per SIMD; half the LDS reads per MFMA) were 4-15% slower; eight-
+  // wavefront 128-row tiles held to 128 VGPRs (four per SIMD) spilled and were slower; reading A
+  // fragments two or three ahead instead of one changed nothing.
   static_assert(BM == 128 || BM == 256, "tile height");
   constexpr bool TALL = WN == 4 || BM == 128;
   constexpr int MTW = TALL ? BM / 16 : 8;
@@ -668,12 +687,7 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
         *reinterpret_cast<uint2*>(static_cast<_Float16*>(Y) + m * ldy + n) = make_uint2(pair[0], pair[1]);
         continue;
       }
-      for (int e = 0; e < 4 && n + e < N; ++e) {
-        float x = v[e];
-        if (dot_dt == DT_F16) x = round_to<DT_F16>(x);
-        if (bias) x += load_float_rt(bias, bias_dt, n + e);
-        store_float_rt(Y, y_dt, m * ldy + n + e, x);
-      }
+      store_quad_any(v, Y, y_dt, dot_dt, bias, bias_dt, m * ldy, n, N);
     }
   }
 }
