@@ -171,4 +171,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
                                            0x00020000);
 }
 
+// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (buffer_load_dwordx4
+// ... lds: the data never passes through VGPRs). `lds` must be wavefront-uniform. The body
+// exists in the device pass only; the host pass of hipcc does not accept LDS address spaces.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, uint32_t voffset,
+                                          uint32_t soffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds), 16, voffset,
+                                           soffset, 0, 0);
+#endif
+}
+
 }  // namespace tmh
