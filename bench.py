@@ -350,10 +350,10 @@ def prefill(ctx, reps, ms_list, per_graph=8):
 
 
 def large_vocab(ctx, reps, per_graph=21):
-    """lm_head MatMulNBits (M=8) and the tied-embedding GatherBlockQuantized lookup. Each graph
-    holds `per_graph` calls, so one graph launch's own cost spreads over them; the lm_head calls
-    rotate over 3 weight copies (276 MB, more than the 256 MB last-level cache) and every gather
-    call reads its own 4096 ids, from 2 tables."""
+    """lm_head MatMulNBits (M=1 and M=8) and the tied-embedding GatherBlockQuantized lookup. Each
+    graph holds `per_graph` calls, so one graph launch's own cost spreads over them; the lm_head
+    calls rotate over 3 weight copies (276 MB, more than the 256 MB last-level cache) and every
+    gather call reads its own 4096 ids, from 2 tables."""
     from transmuter_amd import PackedWeight
     from transmuter_amd._lib import F16, S64, U8, lib
 
@@ -362,38 +362,43 @@ def large_vocab(ctx, reps, per_graph=21):
     b, sc, zp = make_weight_parts(rng, hidden, vocab)
     ws = [PackedWeight.upload(ctx, b, sc, zp, k=hidden, n=vocab, bits=4, block_size=32, weight_dtype="f16")
           for _ in range(3)]
-    a = ctx.put(rng.standard_normal((8, hidden), dtype=np.float32).astype(np.float16))
-    y = ctx.empty((8, vocab), "f16")
+    out = {}
+    for m in (1, 8):
+        a = ctx.put(rng.standard_normal((m, hidden), dtype=np.float32).astype(np.float16))
+        y = ctx.empty((m, vocab), "f16")
 
-    def lm_heads():
-        for i in range(per_graph):
-            matmul_call(ctx, ws[i % len(ws)], a, y, 8)
+        def lm_heads(a=a, y=y, m=m):
+            for i in range(per_graph):
+                matmul_call(ctx, ws[i % len(ws)], a, y, m)
 
-    g = Graph(ctx, lm_heads)
-    us = time_graphs(ctx, [g], reps, 3) * 1e3 / (reps * per_graph)
-    g.destroy()
+        g = Graph(ctx, lm_heads)
+        us = time_graphs(ctx, [g], reps, 3) * 1e3 / (reps * per_graph)
+        g.destroy()
+        lm_bytes = nbits_bytes(hidden, vocab, m)
+        out[f"lm_head_M{m}"] = {"us": us, "gbs": lm_bytes / (us * 1e-6) / 1e9,
+                                "frac": lm_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+        log(f"lm_head M={m}: {us:.1f} us, {lm_bytes / us / 1e3:.0f} GB/s")
     for w in ws:
         w.free()
-    lm_bytes = nbits_bytes(hidden, vocab, 8)
     tables = [(ctx.put(b.reshape(vocab, -1)), ctx.put(sc.reshape(vocab, -1)), ctx.put(zp.reshape(vocab, -1)))
               for _ in range(2)]
     ids = [ctx.put(rng.integers(0, vocab, (8, 512)).astype(np.int64)) for _ in range(per_graph)]
-    out = ctx.empty((8, 512, hidden), "f16")
+    rows = ctx.empty((8, 512, hidden), "f16")
 
     def gathers():
         for i in range(per_graph):
             table, scales, zps = tables[i % 2]
             ctx.check(lib().tmh_gather_block_quantized(ctx.handle, table.ptr, U8, vocab, hidden // 2, ids[i].ptr, S64,
-                                                       4096, scales.ptr, F16, hidden // 32, zps.ptr, U8, 4, out.ptr,
+                                                       4096, scales.ptr, F16, hidden // 32, zps.ptr, U8, 4, rows.ptr,
                                                        None))
 
     g2 = Graph(ctx, gathers)
     us_g = time_graphs(ctx, [g2], reps, 3) * 1e3 / (reps * per_graph)
     g2.destroy()
     g_bytes = 4096 * (hidden // 2 + hidden // 32 * 2 + hidden // 64 + 8) + 4096 * hidden * 2
-    log(f"lm_head M=8: {us:.1f} us, {lm_bytes / us / 1e3:.0f} GB/s; gather: {us_g:.1f} us, {g_bytes / us_g / 1e3:.0f} GB/s")
-    return {"lm_head_M8": {"us": us, "gbs": lm_bytes / (us * 1e-6) / 1e9},
-            "gather_8x512": {"us": us_g, "gbs": g_bytes / (us_g * 1e-6) / 1e9}}
+    log(f"gather: {us_g:.1f} us, {g_bytes / us_g / 1e3:.0f} GB/s")
+    out["gather_8x512"] = {"us": us_g, "gbs": g_bytes / (us_g * 1e-6) / 1e9}
+    return out
 
 
 # ---------------------------------------------------------------- quantized MoE

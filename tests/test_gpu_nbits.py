@@ -275,3 +275,69 @@ def test_matmul_every_gemm_plan(ctx, monkeypatch, case, plan):
         err = rel_err(got, np.asarray(ref, np.float64))
         assert err <= TOL["f16"], f"M={m}: relative error {err}"
     w.free()
+
+
+# One row of A (decode at M = 1) goes to the dot-product GEMV (4- and 8-bit weights with one
+# parameter entry per lane) or, forced with TMH_GEMV_PLAN=mfma, to the MFMA GEMV: both against
+# the oracle, over resident and streaming grids, ragged K, a chunk wholly past K, many chunk rounds
+# and rows of A with padding (lda > K).
+ONE_ROW_CASES = [
+    # bits, block, zp, K, N, lda
+    (4, 32, "packed", 1024, 96, 1024),
+    (4, 32, "none", 200, 40, 264),
+    (4, 128, "packed", 2048, 64, 2048),
+    (4, 256, "packed", 104, 40, 112),
+    (4, 64, "packed", 11008, 48, 11008),
+    (4, 32, "packed", 1024, 30008, 1024),
+    (8, 32, "packed", 512, 48, 512),
+    (8, 128, "none", 1000, 20, 1000),
+    (8, 32, "none", 72, 24, 80),
+    (8, 128, "none", 256, 50008, 256),
+    (4, 16, "packed", 256, 40, 256),  # a lane's values span two blocks: MFMA kernel either way
+    (2, 16, "packed", 256, 24, 256),
+]
+
+
+@pytest.mark.parametrize("plan", ["dot", "mfma"])
+@pytest.mark.parametrize("case", ONE_ROW_CASES, ids=lambda c: "b{}_bs{}_{}_K{}_N{}_lda{}".format(*c))
+def test_one_row_both_kernels(ctx, monkeypatch, case, plan):
+    import ctypes
+
+    from transmuter_amd._lib import F16, lib
+
+    bits, bs, zp, k, n, lda = case
+    if plan == "mfma":
+        monkeypatch.setenv("TMH_GEMV_PLAN", "mfma")
+    else:
+        monkeypatch.delenv("TMH_GEMV_PLAN", raising=False)
+    print(f"one row {plan} {case}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    b, s, z = nbits_weight(rng, k, n, bits, bs, zp=zp)
+    w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=bits, block_size=bs, weight_dtype="f16")
+    a_full = rng.standard_normal((1, lda)).astype(np.float16)
+    y_d = ctx.empty((1, n), "f16")
+    ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, ctx.put(a_full).ptr, F16, 1, lda, None, 0, y_d.ptr, F16, n,
+                                     None))
+    ref = o.matmul_nbits(a_full[:, :k], b, s, z, k=k, n=n, bits=bits, block_size=bs).astype(np.float64)
+    err = rel_err(y_d.numpy().astype(np.float64), ref)
+    assert err <= TOL["f16"], f"relative error {err}"
+    w.free()
+    del ctypes
+
+
+def test_one_row_dot_kernel_is_near_exact(ctx, monkeypatch):
+    """The dot-product GEMV sums exact products (q + 1024) * a in f32 and removes the offsets per
+    lane: against the f64 sum over the exact weights (q - zero) * scale its error is about one f16
+    output rounding."""
+    monkeypatch.delenv("TMH_GEMV_PLAN", raising=False)
+    rng = np.random.default_rng(15)
+    k, n = 3072, 512
+    b, s, z = nbits_weight(rng, k, n, 4, 32, zp="packed")
+    w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=4, block_size=32, weight_dtype="f16")
+    a = rng.standard_normal((1, k)).astype(np.float16)
+    y = matmul_nbits(ctx.put(a), w).numpy().astype(np.float64)
+    q = o.unpack(b.reshape(n, -1), 4)[:, :k].astype(np.float64)
+    zq = o.unpack(z.reshape(n, -1), 4)[:, : k // 32].astype(np.float64)
+    wx = (q - np.repeat(zq, 32, axis=1)) * np.repeat(s.reshape(n, -1).astype(np.float64), 32, axis=1)
+    ref = a.astype(np.float64) @ wx.T
+    assert np.abs(y - ref).max() <= 2 * np.abs(ref).max() * 2.0 ** -11

@@ -118,16 +118,38 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t o
 }
 
 // Eight exact f16 weights (q - zero) * scale of MFMA step i of a lane, from its 16 bytes.
-// zz holds 1024 + zero (f16, both halves) and ss the scale (both halves); a 16-bit half
-// 0x6400 | q is the f16 number 1024 + q, so (0x6400 | q) - zz is q - zero exactly.
+// zz holds 1024 + zero and ss the scale as f16 (only the low halves are read: the packed
+// operations take them as splats); a 16-bit half 0x6400 | q is the f16 number 1024 + q, so
+// (0x6400 | q) - (1024 + zero) is q - zero exactly.
+// 4 bits: the nibbles at bits 4-7 of each half are masked in place, 0x6400 | q << 4 = 1024 + 16q,
+// and (1024 + 16q) / 16 - (64 + zero) is q - zero exactly in one fused multiply-add (every
+// intermediate is a small integer); four pairs then take 5 bit operations instead of 7.
 template <int BITS>
 __device__ __forceinline__ half8_t unpack_step(const uint4_t& w, int i, half2_t zz, half2_t ss) {
+  const half2_t z2 = {zz[0], zz[0]}, s2 = {ss[0], ss[0]};
   uint32_t pr[4];
   if constexpr (BITS == 4) {
     const uint32_t x = w[i];
     const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
+    pr[0] = and_or(x, 0x000F000Fu, magic);
+    pr[1] = and_or(x, 0x00F000F0u, magic);
+    pr[2] = and_or(x >> 8, 0x000F000Fu, magic);
+    pr[3] = and_or(x >> 8, 0x00F000F0u, magic);
+    // 64 + zero: the zero's 4 bits moved under the f16 exponent of 64 (ulp 1/16).
+    const uint16_t z64 = static_cast<uint16_t>(0x5400u + ((__builtin_bit_cast(uint16_t, zz[0]) & 0xFFu) << 4));
+    const _Float16 z64h = __builtin_bit_cast(_Float16, z64);
+    const half2_t z16 = {z64h, z64h};
+    const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+    half8_t out;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pr[j] = and_or(x >> (4 * j), 0x000F000Fu, magic);
+    for (int j = 0; j < 4; ++j) {
+      const half2_t q = __builtin_bit_cast(half2_t, pr[j]);
+      const half2_t d = (j & 1) ? __builtin_elementwise_fma(q, sixteenth, -z16) : q - z2;
+      const half2_t wv = d * s2;
+      out[2 * j] = wv[0];
+      out[2 * j + 1] = wv[1];
+    }
+    return out;
   } else if constexpr (BITS == 8) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -144,7 +166,7 @@ __device__ __forceinline__ half8_t unpack_step(const uint4_t& w, int i, half2_t 
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const half2_t q = __builtin_bit_cast(half2_t, pr[j]);
-    const half2_t wv = (q - zz) * ss;
+    const half2_t wv = (q - z2) * s2;
     out[2 * j] = wv[0];
     out[2 * j + 1] = wv[1];
   }

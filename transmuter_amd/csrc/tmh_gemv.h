@@ -175,6 +175,141 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
   }
 }
 
+// The decode GEMV for one row of A (M = 1), 4- or 8-bit weights whose parameters are constant
+// over a lane's GW values (block_size >= GW), f16 A / scales / Y, no bias: dot products instead
+// of MFMAs, which at one row leave 15 of 16 MFMA columns empty while the per-weight scaling
+// costs the same VALU work.
+//
+// Lane (g, r) takes the GW values of row r in k-group g of each chunk. The f16 pairs 0x6400 | q
+// (= 1024 + q; 4 bits: also 0x6400 | q << 4 = 1024 + 16q for the nibbles at bits 4-7 of each
+// half) go straight into v_dot2_f32_f16 against the matching pairs of A, with f32 sums De (pairs
+// 1024 + q) and Do (pairs 1024 + 16q). Then
+//   sum (q - zero) * a = De + Do / 16 - (1024 * Se + 64 * So + zero * (Se + So)),
+// Se and So being the sums of the matching A values (shared by all tiles of a chunk), and the
+// lane adds scale * that to its row's sum. Every product (q + 1024) * a is exact in f32; the
+// result differs from the reference's dot over f16-rounded weights (q - zero) * scale only by
+// that rounding and by f32 summation order.
+// The four lanes of a row and the wavefronts of the workgroup add through LDS in a fixed order.
+// Chunk rounds, launch shapes and buffer addressing are those of k_gemv_dec.
+template <int BITS, bool HAS_ZP, int U, int NW, int TN>
+__global__ __launch_bounds__(64 * NW) void k_gemv_dot(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
+  static_assert(BITS == 4 || BITS == 8, "4- or 8-bit weights");
+  constexpr int CW = 512 / BITS;  // weights per chunk row
+  constexpr int GW = CW / 4;      // weights per lane per chunk
+  constexpr int NP = GW / 8;      // 16-byte pieces of A per lane per chunk
+  __shared__ float red[NW * TN * 64];
+  (void)ldy;
+  const uint32_t nbc = (shape >> 8) & 0xFFu, bsc_shift = (shape >> 16) & 0xFFu;
+  const uint32_t K = nch * CW - (shape >> 24) * 4;
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t t0 = blockIdx.x * TN;
+  const uint32_t n_params = ntiles * nch * nbc * 16;
+  const auto q_rsrc = buffer_rsrc(qt, ntiles * nch * 1024);
+  const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+  const auto a_rsrc = buffer_rsrc(A, K * 2);
+  const half2_t one2 = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
+  float acc[TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) acc[tn] = 0.f;
+  for (uint32_t base = wave * U; base < nch; base += NW * U) {
+    uint4_t w[U][TN];
+    uint32_t sv[U][TN], zv[U][TN];
+    half8_t av[U][NP];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t c = base + u < nch ? base + u : nch - 1;
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t t = t0 + tn;  // t >= ntiles reads zeros
+        w[u][tn] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, (t * nch * 64 + lane) * 16, c * 1024, 0);
+        const uint32_t e = ((t * nch + c) * nbc + ((g * GW) >> bsc_shift)) * 16 + r;
+        sv[u][tn] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, 0, 0);
+        if constexpr (HAS_ZP) zv[u][tn] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0);
+      }
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const uint32_t k = (base + u) * CW + g * GW + 8 * p;  // a piece lies wholly in or past K
+        av[u][p] = __builtin_bit_cast(
+            half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, base + u < nch && k < K ? k * 2 : 0x80000000u, 0, 0));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // Sums of this lane's A values, split by the pair form their weights take. (A pieces are
+      // held as f16 vectors: pairs are taken by element, since hipcc 7.2 read element 0 of an
+      // integer vector for every index under __builtin_bit_cast of one element.)
+      float se = 0.f, so = 0.f;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const half2_t ap = {av[u][p][2 * j], av[u][p][2 * j + 1]};
+          if (BITS == 4 && (j & 1)) so = __builtin_amdgcn_fdot2(ap, one2, so, false);
+          else se = __builtin_amdgcn_fdot2(ap, one2, se, false);
+        }
+      }
+      const float base_sum = BITS == 4 ? fmaf(1024.f, se, 64.f * so) : 1024.f * se;
+      const float sa = se + so;
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t magic = __builtin_amdgcn_readfirstlane(0x64006400u);
+        float de = 0.f, dq = 0.f;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          half2_t ap[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ap[j] = half2_t{av[u][p][2 * j], av[u][p][2 * j + 1]};
+          if constexpr (BITS == 4) {
+            // Word p holds values 8p .. 8p+7: pairs (0,1) and (4,5) in low-nibble form, (2,3) and
+            // (6,7) in high-nibble form, against A pairs 0, 2 and 1, 3 of piece p.
+            const uint32_t x = w[u][tn][p];
+            de = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, and_or(x, 0x000F000Fu, magic)), ap[0], de, false);
+            dq = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, and_or(x, 0x00F000F0u, magic)), ap[1], dq, false);
+            de = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, and_or(x >> 8, 0x000F000Fu, magic)), ap[2], de, false);
+            dq = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, and_or(x >> 8, 0x00F000F0u, magic)), ap[3], dq, false);
+          } else {
+            // Words 2p, 2p+1 hold values 8p .. 8p+7 in byte order.
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const uint32_t x = w[u][tn][2 * p + h];
+              const uint32_t lo = (x & 0xFFu) | ((x << 8) & 0x00FF0000u) | 0x64006400u;
+              const uint32_t hi = ((x >> 16) & 0xFFu) | ((x >> 8) & 0x00FF0000u) | 0x64006400u;
+              de = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, lo), ap[2 * h], de, false);
+              de = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, hi), ap[2 * h + 1], de, false);
+            }
+          }
+        }
+        const float z = HAS_ZP ? static_cast<float>(zv[u][tn]) : static_cast<float>(1 << (BITS - 1));
+        const float s = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(sv[u][tn])));
+        const float dot = BITS == 4 ? fmaf(dq, 0.0625f, de) : de;
+        acc[tn] = fmaf(s, dot - fmaf(z, sa, base_sum), acc[tn]);
+      }
+    }
+  }
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) red[(wave * TN + tn) * 64 + lane] = acc[tn];
+  __syncthreads();
+  // Tile tn's 16 sums are added by lanes 0-15 of wavefront tn % NW, each over its row's four
+  // lanes in every wavefront.
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    if (tn % NW != static_cast<int>(wave) || g != 0) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2)
+#pragma unroll
+      for (int g2 = 0; g2 < 4; ++g2) v += red[(w2 * TN + tn) * 64 + g2 * 16 + r];
+    const uint32_t n = (t0 + tn) * 16 + r;
+    if (n < N) Y[n] = static_cast<_Float16>(v);
+  }
+}
+
 // The same GEMV over f32 A and f32 weights (the reference's CPU configuration after move/2: f32
 // scales, so W = (q - zero) * scale in f32, one rounding) for M <= MM rows, f32 Y, no bias.
 // Lane (g, r) dequantizes its 16 bytes (row r, GW consecutive k) to f32 and accumulates

@@ -17,6 +17,8 @@
 //    weights streams 6.7 TB/s); U = 1 with two rounds was 17.5-19.4 us. Persistent wavefronts
 //    that double-buffer whole tiles, and scales staged through LDS with wide loads, were no faster.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 #include "tmh_gemv.h"
 #include "tmh_internal.h"
@@ -78,11 +80,50 @@ void streaming(const DecArgs& d, int nw, hipStream_t s) {
   }
 }
 
+template <int BITS, bool HAS_ZP, int NW, int TN, int U>
+void go_dot(const DecArgs& d, hipStream_t s) {
+  const unsigned grid = (d.ntiles + TN - 1) / TN;
+  k_gemv_dot<BITS, HAS_ZP, U, NW, TN><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles, d.lda, d.shape,
+                                                                d.y, d.ldy, d.n);
+}
+
+// Which kernel serves one row of A: the dot-product kernel unless TMH_GEMV_PLAN=mfma in the
+// environment forces the MFMA kernel (how the tests reach both at M = 1; read at each call).
+bool dot_for_one_row() {
+  const char* v = std::getenv("TMH_GEMV_PLAN");
+  return !(v && std::strcmp(v, "mfma") == 0);
+}
+
 template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_bits(const DecArgs& d, int64_t M, int num_cus, hipStream_t s) {
   const int64_t nch = d.nch;
   const int64_t resident = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * 24;
-  if (static_cast<int64_t>(d.ntiles) * std::min<int64_t>(nch, 16) <= resident) {
+  const bool resident_grid = static_cast<int64_t>(d.ntiles) * std::min<int64_t>(nch, 16) <= resident;
+  if constexpr (BITS != 2 && !SPLIT) {
+    if (M == 1 && dot_for_one_row()) {
+      if (resident_grid) {
+        switch (round_waves(nch)) {
+          case 1: go_dot<BITS, HAS_ZP, 1, 1, 1>(d, s); break;
+          case 2: go_dot<BITS, HAS_ZP, 2, 1, 1>(d, s); break;
+          case 4: go_dot<BITS, HAS_ZP, 4, 1, 1>(d, s); break;
+          case 8: go_dot<BITS, HAS_ZP, 8, 1, 1>(d, s); break;
+          case 12: go_dot<BITS, HAS_ZP, 12, 1, 1>(d, s); break;
+          default: go_dot<BITS, HAS_ZP, 16, 1, 1>(d, s);
+        }
+      } else {
+        // Streaming: two chunks per wavefront loaded together, two tiles per workgroup (151936 x
+        // 1024 q4: 15.7 us against 15.9 with four tiles and 17.0 for the MFMA kernel).
+        switch (std::min(8, round_waves((nch + 1) / 2))) {
+          case 1: go_dot<BITS, HAS_ZP, 1, 2, 2>(d, s); break;
+          case 2: go_dot<BITS, HAS_ZP, 2, 2, 2>(d, s); break;
+          case 4: go_dot<BITS, HAS_ZP, 4, 2, 2>(d, s); break;
+          default: go_dot<BITS, HAS_ZP, 8, 2, 2>(d, s);
+        }
+      }
+      return;
+    }
+  }
+  if (resident_grid) {
     const int nw = round_waves(nch);
     if (M > 4)
       one_shot<BITS, HAS_ZP, SPLIT, true>(d, nw, s);
