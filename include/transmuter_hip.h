@@ -69,6 +69,7 @@ typedef enum { TMH_QPARAM_TENSOR = 0, TMH_QPARAM_AXIS = 1, TMH_QPARAM_BLOCKED = 
 
 typedef struct tmh_ctx tmh_ctx;       /* one device, one stream, the last error */
 typedef struct tmh_weight tmh_weight; /* a device-resident packed MatMulNBits weight */
+typedef struct tmh_int8_weight tmh_int8_weight; /* a MatMulInteger B prepared for the int8 GEMM */
 
 /* ------------------------------------------------------------------ context and memory */
 
@@ -290,6 +291,27 @@ int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d
                        const void* d_a_zero, int64_t a_zero_count, const void* d_b_zero,
                        int64_t b_zero_count, int64_t batch, int64_t M, int64_t K, int64_t N,
                        int b_batched, void* d_y, void* stream);
+
+/*
+ * MatMulInteger with a B prepared once (no reference counterpart: for a B that is an initializer,
+ * prepared at load as move/2 prepares MatMulNBits weights, lib/transmuter.ex:1104-1240).
+ * tmh_int8_weight_prepare transposes B [K, N] (U8 or S8, on the device) into s8 rows of k,
+ * zero-padded to a multiple of 128, and precomputes its column sums and the zero-point terms of
+ * b_zero (NULL, one value or [N] of B's type); asynchronous on `stream`, whose later work may use
+ * the weight at once. K must be a multiple of 16 (TMH_ERR_UNSUPPORTED otherwise; the caller keeps
+ * B and uses tmh_matmul_integer). tmh_matmul_integer_prepared computes what tmh_matmul_integer
+ * computes for the same B and zero points: y[b, m, n] = sum_k (a[b, m, k] - a_zero[m]) *
+ * (B[k, n] - b_zero[n]) as s32 (mod 2^32), A [batch, M, K] U8 or S8, 16-byte aligned, with
+ * (M + 128) * K below 2^31; y [batch, M, N] S32.
+ */
+int tmh_int8_weight_prepare(tmh_ctx* ctx, const void* d_b, int b_dtype, const void* d_b_zero,
+                            int64_t b_zero_count, int64_t K, int64_t N, void* stream,
+                            tmh_int8_weight** out);
+void tmh_int8_weight_free(tmh_int8_weight* w);
+int tmh_int8_weight_info(const tmh_int8_weight* w, int64_t* K, int64_t* N, size_t* device_bytes);
+int tmh_matmul_integer_prepared(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d_a_zero,
+                                int64_t a_zero_count, int64_t batch, int64_t M,
+                                const tmh_int8_weight* w, void* d_y, void* stream);
 
 /* ------------------------------------------------------------------ DynamicQuantizeLinear */
 

@@ -185,3 +185,40 @@ def test_split_k_repeated_calls_and_replays_are_bit_exact(monkeypatch):
     finally:
         ctx.synchronize()
         ctx.close()
+
+
+def test_prepared_matmul_integer_replays_match_eager():
+    """MatMulInteger over a prepared B inside a graph: every replay equals the eager call."""
+    from transmuter_amd._lib import S32
+    from transmuter_amd.packed import Int8Weight
+
+    ctx = Context(0)
+    try:
+        rng = np.random.default_rng(23)
+        m, k, n = 300, 1040, 400
+        b = rng.integers(0, 256, (k, n), dtype=np.uint8)
+        w = Int8Weight.prepare(ctx, b, rng.integers(0, 256, n, dtype=np.uint8))
+        a = ctx.put(rng.integers(0, 256, (m, k), dtype=np.uint8))
+        az = ctx.put(np.array([17], np.uint8))
+        y = ctx.empty((m, n), "s32")
+
+        def call():
+            ctx.check(lib().tmh_matmul_integer_prepared(ctx.handle, a.ptr, U8, az.ptr, 1, 1, m, w.handle, y.ptr, None))
+
+        call()
+        want = y.numpy()
+        graph = ctypes.c_void_p()
+        ctx.check(lib().tmh_graph_begin(ctx.handle, None))
+        call()
+        ctx.check(lib().tmh_graph_end(ctx.handle, None, ctypes.byref(graph)))
+        for _ in range(3):
+            ctx.check(lib().tmh_upload(ctx.handle, y.ptr, np.zeros((m, n), np.int32).ctypes.data_as(ctypes.c_void_p),
+                                       y.nbytes))
+            ctx.check(lib().tmh_graph_launch(ctx.handle, graph, None))
+            ctx.synchronize()
+            assert np.array_equal(y.numpy(), want)
+        ctx.check(lib().tmh_graph_destroy(ctx.handle, graph))
+        del S32
+        w.free()
+    finally:
+        ctx.close()

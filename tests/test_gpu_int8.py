@@ -129,3 +129,108 @@ def test_dynamic_quant_matmul_fixture(ctx):
     expected = f.outputs["y"]
     assert got.shape == expected.shape
     assert np.abs(got - expected).max() <= tolerance(expected)
+
+
+# MatMulInteger over a B prepared once (tmh_int8_weight_prepare: B transposed to s8 rows of k with
+# its column sums and zero points folded in), against the oracle, bit-exactly: u8/s8 on either
+# side, every zero-point form, batched A, ragged M and N (N off the 16-byte stores), K a multiple
+# of 16 but not of a 128-byte k-step, and one prepared B serving calls of different M.
+PREPARED_CASES = [
+    # batch, M, K, N, a type, b type, a_zero, b_zero
+    (1, 1, 64, 16, "u8", "s8", "scalar", None),
+    (1, 130, 272, 70, "u8", "u8", "row", "col"),
+    (1, 128, 256, 128, "s8", "s8", None, None),
+    (1, 33, 4096, 257, "u8", "s8", "scalar", "scalar"),
+    (3, 40, 96, 48, "s8", "u8", "row", "col"),
+    (2, 17, 16, 9, "u8", "u8", "scalar", "col"),
+    (1, 300, 512, 520, "u8", "s8", "scalar", None),
+    (2, 129, 1040, 400, "s8", "u8", "scalar", "col"),
+    (1, 513, 2048, 384, "u8", "s8", "scalar", None),
+    (1, 256, 512, 1024, "u8", "u8", "scalar", "col"),
+]
+
+
+@pytest.mark.parametrize("case", PREPARED_CASES, ids=lambda c: "b{}_M{}_K{}_N{}_{}{}_{}_{}".format(*c))
+def test_matmul_integer_prepared_matches_oracle(ctx, case):
+    from transmuter_amd.packed import Int8Weight
+
+    batch, m, k, n, adt, bdt, az, bz = case
+    print(f"matmul_integer prepared {case}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()) + 7)
+    b = _ints(rng, (k, n), bdt)
+    b_zero = None if bz is None else _ints(rng, (1,) if bz == "scalar" else (n,), bdt)
+    w = Int8Weight.prepare(ctx, b, b_zero)
+    for mm in (m, max(1, m // 2 + 1)):
+        a = _ints(rng, (batch, mm, k) if batch > 1 else (mm, k), adt)
+        a_zero = None if az is None else _ints(rng, (1,) if az == "scalar" else (mm,), adt)
+        node = NodeProto(op_type="MatMulInteger", input=["a", "b", "az" if az else "", ""], output=["y"])
+        got = quantized.apply(node, [ctx.put(a), w, ctx.put(a_zero) if a_zero is not None else None, None])[0].numpy()
+        ref = o.matmul_integer(a, b, a_zero.reshape(-1) if a_zero is not None else None,
+                               b_zero.reshape(-1) if b_zero is not None else None)
+        assert got.dtype == np.int32 and got.shape == ref.shape
+        assert np.array_equal(got, ref), f"M={mm}"
+    w.free()
+
+
+def test_matmul_integer_prepared_extremes_and_full_size(ctx):
+    """Every product at its largest (4096 * 255 * 255, beyond 2^24), and the 2048^3 u8 x u8 product
+    with zero points equal to the plain MatMulInteger kernel's, bit for bit."""
+    from transmuter_amd.packed import Int8Weight
+
+    w = Int8Weight.prepare(ctx, np.full((4096, 5), 255, np.uint8))
+    node = NodeProto(op_type="MatMulInteger", input=["a", "b"], output=["y"])
+    got = quantized.apply(node, [ctx.put(np.full((3, 4096), 255, np.uint8)), w])[0].numpy()
+    assert np.all(got == 4096 * 255 * 255)
+    w.free()
+    rng = np.random.default_rng(2048)
+    a = rng.integers(0, 256, (2048, 2048), dtype=np.uint8)
+    b = rng.integers(0, 256, (2048, 2048), dtype=np.uint8)
+    az, bz = np.array([131], np.uint8), rng.integers(0, 256, 2048, dtype=np.uint8)
+    plain = NodeProto(op_type="MatMulInteger", input=["a", "b", "az", "bz"], output=["y"])
+    want = quantized.apply(plain, [ctx.put(a), ctx.put(b), ctx.put(az), ctx.put(bz)])[0].numpy()
+    w = Int8Weight.prepare(ctx, b, bz)
+    prepared = NodeProto(op_type="MatMulInteger", input=["a", "b", "az", ""], output=["y"])
+    got = quantized.apply(prepared, [ctx.put(a), w, ctx.put(az), None])[0].numpy()
+    assert np.array_equal(got, want)
+    w.free()
+
+
+def test_matmul_integer_prepare_needs_k_in_sixteens(ctx):
+    from transmuter_amd._lib import TmhArgumentError
+    from transmuter_amd.packed import Int8Weight
+
+    assert not Int8Weight.supported(75, 9)
+    with pytest.raises(TmhArgumentError, match="multiple of 16"):
+        Int8Weight.prepare(ctx, np.zeros((75, 9), np.uint8))
+
+
+def test_dynamic_quant_matmul_fixture_with_b_prepared_at_load(ctx):
+    """The MatMulInteger_dynamic_quant graph after the load-time move: its MatMulInteger reads the
+    s8 weight initializer prepared as "<B>:int8", and the graph still matches ONNX Runtime."""
+    from transmuter_amd import hip
+    from transmuter_amd.packed import Int8Weight
+
+    f = Fixture("MatMulInteger_dynamic_quant")
+    model = hip.Model(nodes=list(f.nodes), params={}, static=dict(f.initializers), outputs=["y"])
+    moved = hip.prepare_matmul_integer(model, ctx)
+    mi = [node for node in moved.nodes if node.op_type == "MatMulInteger"]
+    assert mi and all(node.input[1].endswith(":int8") for node in mi)
+    assert all(isinstance(moved.params[node.input[1]], Int8Weight) for node in mi)
+    values = {name: ctx.put(v) for name, v in f.inputs.items()}
+    values.update(moved.static)
+    values.update(moved.params)
+    for node in moved.nodes:
+        args = [values[name] if name else None for name in node.input]
+        if node.op_type in quantized.op_types():
+            outs = quantized.apply(node, args)
+        elif node.op_type == "Cast":
+            outs = [np.asarray(args[0].numpy(), np.float32)]
+        else:  # Mul
+            host = [a.numpy() if hasattr(a, "numpy") else np.asarray(a) for a in args]
+            outs = [(np.asarray(host[0], np.float32) * np.asarray(host[1], np.float32)).astype(np.float32)]
+        for name, v in zip(node.output, outs):
+            values[name] = v
+    got = np.asarray(values["y"])
+    expected = f.outputs["y"]
+    assert got.shape == expected.shape
+    assert np.abs(got - expected).max() <= tolerance(expected)

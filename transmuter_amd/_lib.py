@@ -72,6 +72,10 @@ SIGNATURES = {
     "tmh_dequantize_linear": (_i, [_vp, _vp, _i, _i64, _i64, _i64, _vp, _i, _vp, _i, _i, _i64, _vp, _vp]),
     "tmh_matmul_integer": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i, _vp,
                                 _vp]),
+    "tmh_int8_weight_prepare": (_i, [_vp, _vp, _i, _vp, _i64, _i64, _i64, _vp, ctypes.POINTER(_vp)]),
+    "tmh_int8_weight_free": (None, [_vp]),
+    "tmh_int8_weight_info": (_i, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_sz)]),
+    "tmh_matmul_integer_prepared": (_i, [_vp, _vp, _i, _vp, _i64, _i64, _i64, _vp, _vp, _vp]),
     "tmh_dynamic_quantize_linear": (_i, [_vp, _vp, _i, _i64, _vp, _vp, _vp, _vp]),
     "tmh_upload_file": (_i, [_vp, _vp, ctypes.c_char_p, _i64, _sz]),
     "tmh_floor_empty": (_i, [_vp, _i, _vp]),

@@ -646,15 +646,94 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
         for (int nt = 0; nt < NTW; ++nt) part[((wl * MTW + mt) * NTW + nt) * 64 + lane] = acc[mt][nt];
     }
     __syncthreads();
-    if (kh == 1) return;
+    if (kh == 0) {
 #pragma unroll
-    for (int mt = 0; mt < MTW; ++mt)
+      for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] += part[((wl * MTW + mt) * NTW + nt) * 64 + lane];
+        for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] += part[((wl * MTW + mt) * NTW + nt) * 64 + lane];
+    }
   }
   // Lane (16g + r) holds, for each (mt, nt), row mt*16 + r and the 4 columns nt*16 + 4g ...
   const bool f16_out = y_dt == DT_F16 && dot_dt == DT_F16 && !bias;
   const bool vec_out = (ldy % 4) == 0;
+  // Whole tiles of f32 partial sums, or of f16 outputs with 16-byte aligned rows, go out through
+  // LDS: each wavefront writes its accumulators there in the MFMA layout, then every thread
+  // stores 16 contiguous bytes of a row, so a store instruction writes whole cache lines (from
+  // the MFMA layout a lane holds 4 columns: 16 rows x 8 or 16 bytes per instruction). The tile
+  // goes in passes of as many rows as the LDS holds; 16-byte units are XOR-swizzled by row.
+  // (Stores measured 4-9% of the SmolLM3-3B projections at M = 2048, 25% at M = 256; f32
+  // partial sums that need two passes were slower staged than stored directly, 16 bytes a lane.)
+  constexpr bool kPartialsFit = static_cast<int>(gemm_lds_bytes<BITS, BM, KS>()) >= BM * 64 * WN * 4;
+  const bool staged = ws ? kPartialsFit && (N % 4) == 0
+                         : f16_out && (ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+  if (staged) {
+    auto out_tile = [&](auto esz_c) {
+      constexpr int ESZ = decltype(esz_c)::value;  // bytes per output: 4 (partial sums) or 2 (f16)
+      constexpr int BN = 64 * WN;
+      constexpr int RS = BN * ESZ;  // bytes per staged row
+      constexpr int UPR = RS / 16;  // 16-byte units per row
+      constexpr int CAP = static_cast<int>(gemm_lds_bytes<BITS, BM, KS>());
+      constexpr int RPP = CAP / RS >= BM ? BM : CAP / RS;  // rows per pass
+      static_assert(RPP >= 16 && BM % RPP == 0 && UPR >= 8, "staging shape");
+      constexpr int NTHR = 128 * WN * KS;
+      const int col0 = nb * BN;
+      for (int pass = 0; pass < BM / RPP; ++pass) {
+        __syncthreads();  // the LDS is free: A tiles, partial sums or the previous pass are read
+        if (KS == 1 || kh == 0) {
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt) {
+            const int row = wm * 128 + mt * 16;  // the 16 rows of fragment mt lie in one pass
+            if (row / RPP != pass) continue;
+            const int prow = row % RPP + r;
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) {
+              const int byte = ((t0 + nt) * 16 + 4 * g - col0) * ESZ;
+              uint8_t* p = lds + prow * RS + (((byte >> 4) ^ (prow & 7)) << 4) + (byte & 15);
+              const float4_t v = acc[mt][nt];
+              if constexpr (ESZ == 4) {
+                *reinterpret_cast<float4_t*>(p) = v;
+              } else {
+                const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
+                const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+                *reinterpret_cast<uint2*>(p) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+              }
+            }
+          }
+        }
+        __syncthreads();
+        for (int idx = tid; idx < RPP * UPR; idx += NTHR) {
+          const int prow = idx / UPR, unit = idx % UPR;
+          const int64_t m = m0 + pass * RPP + prow;
+          const int64_t n = col0 + unit * (16 / ESZ);
+          if (m >= M || n >= N) continue;
+          const uint4_t v = *reinterpret_cast<const uint4_t*>(lds + prow * RS + ((unit ^ (prow & 7)) << 4));
+          if constexpr (ESZ == 4) {
+            float* dst = ws + (static_cast<int64_t>(split) * M + m) * N + n;
+            if (n + 4 <= N) {
+              *reinterpret_cast<uint4_t*>(dst) = v;
+            } else {
+              const float4_t f = __builtin_bit_cast(float4_t, v);  // whole vector: hipcc 7.2 miscompiled element casts
+              for (int e = 0; e < 4 && n + e < N; ++e) dst[e] = f[e];
+            }
+          } else {
+            uint16_t* dst = static_cast<uint16_t*>(Y) + m * ldy + n;
+            if (n + 8 <= N) {
+              *reinterpret_cast<uint4_t*>(dst) = v;
+            } else {
+              const uint32_t words[4] = {v[0], v[1], v[2], v[3]};
+              for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = static_cast<uint16_t>(words[e >> 1] >> ((e & 1) * 16));
+            }
+          }
+        }
+      }
+    };
+    if (ws)
+      out_tile(std::integral_constant<int, 4>{});
+    else
+      out_tile(std::integral_constant<int, 2>{});
+    return;
+  }
+  if (KS == 2 && kh == 1) return;
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt) {
     const int64_t m = m0 + wm * 128 + mt * 16 + r;

@@ -21,7 +21,7 @@ from dataclasses import dataclass, field, replace
 import numpy as np
 
 from .device import FLOAT_TYPES, Context, DeviceTensor, cast_float, nx_type
-from .packed import PackedWeight
+from .packed import Int8Weight, PackedWeight
 from .quantized import nbits_sizes
 
 
@@ -159,8 +159,69 @@ def move(model: Model, ctx: Context) -> Model:
               if name not in freed}
     params.update(weights)
     static = {name: value for name, value in model.static.items() if name not in freed}
+    moved = prepare_matmul_integer(replace(model, nodes=nodes, params=params, static=static, backend=ctx), ctx)
     # move/2 ends with Fusion.matmuls/2 (lib/transmuter.ex:1181).
-    return merge_matmuls(replace(model, nodes=nodes, params=params, static=static, backend=ctx))
+    return merge_matmuls(moved)
+
+
+# ---------------------------------------------------------------- MatMulInteger B at load
+
+
+def _int8_name(b: str) -> str:
+    return b + ":int8"
+
+
+def _int8_preparable(node, values: dict) -> bool:
+    """A MatMulInteger whose B is a 2-D u8/s8 initializer (and b_zero_point absent or an
+    initializer) of a shape the prepared GEMM takes."""
+    if node.op_type != "MatMulInteger" or len(node.input) < 2 or not node.input[1]:
+        return False
+    b = values.get(node.input[1])
+    if b is None or isinstance(b, (PackedWeight, Int8Weight)):
+        return False
+    shape = tuple(b.shape)
+    dtype = b.dtype if isinstance(b, DeviceTensor) else getattr(b, "nx_dtype", None) or nx_type(np.asarray(b))
+    bz = node.input[3] if len(node.input) > 3 else ""
+    if bz and bz not in values:
+        return False
+    return len(shape) == 2 and dtype in ("u8", "s8") and Int8Weight.supported(*shape)
+
+
+def prepare_matmul_integer(model: Model, ctx: Context) -> Model:
+    """MatMulInteger nodes whose B is an initializer read "<B>:int8" afterwards: B transposed once
+    into the int8 GEMM's layout with its b_zero_point folded in (no counterpart in move/2, which
+    leaves MatMulInteger to the backend's dot; the outputs are the same s32 sums). The node keeps
+    A and a_zero_point; B and b_zero_point leave the params when nothing else reads them."""
+    values = {**model.static, **model.params}
+    prepared = [node for node in model.nodes if _int8_preparable(node, values)]
+    if not prepared:
+        return model
+    prepared_ids = {id(node) for node in prepared}
+    weights = {}
+    nodes = []
+    for node in model.nodes:
+        if id(node) not in prepared_ids:
+            nodes.append(node)
+            continue
+        b_name = node.input[1]
+        bz_name = node.input[3] if len(node.input) > 3 else ""
+        name = _int8_name(b_name) + (f":{bz_name}" if bz_name else "")
+        if name not in weights:
+            if name in values:
+                raise ValueError(f"the model already has a value named {name}")
+            weights[name] = Int8Weight.prepare(ctx, _host_value(values[b_name]),
+                                               _host_value(values[bz_name]) if bz_name else None)
+        a_zero = node.input[2] if len(node.input) > 2 else ""
+        nodes.append(replace(node, input=[node.input[0], name, a_zero, ""]))
+    used = set(model.outputs)
+    for node in nodes:
+        used.update(node.input)
+    freed = {name for node in prepared for name in (node.input[1], node.input[3] if len(node.input) > 3 else "")
+             if name and name not in used}
+    params = {name: value for name, value in model.params.items() if name not in freed}
+    params.update(weights)
+    static = {name: value for name, value in model.static.items() if name not in freed}
+    return replace(model, nodes=nodes, params=params, static=static)
 
 
 def _to_device(value, ctx: Context, compute_type: str | None):

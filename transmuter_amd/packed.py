@@ -133,3 +133,64 @@ class PackedWeight:
 
     def __repr__(self) -> str:
         return f"PackedWeight(N={self.n}, K={self.k}, bits={self.bits}, block_size={self.block_size}, {self.dtype})"
+
+
+class Int8Weight:
+    """A MatMulInteger B prepared once on the device (tmh_int8_weight): B^T as s8 rows of k, its
+    column sums and its zero-point terms. What the load-time move stores under "<B>:int8" for a
+    MatMulInteger whose B (and b_zero_point) are initializers; the handler then computes what
+    MatMulInteger computes over B and b_zero_point (lib/transmuter/ops/quantized.ex:105-110)."""
+
+    def __init__(self, ctx: Context, handle: ctypes.c_void_p, k: int, n: int, dtype: str):
+        self.ctx, self.handle, self.k, self.n, self.dtype = ctx, handle, k, n, dtype
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self.k, self.n)
+
+    @staticmethod
+    def supported(k: int, n: int) -> bool:
+        """Shapes the prepared GEMM takes: K a multiple of 16 (N * K below 2^31)."""
+        return k > 0 and n > 0 and k % 16 == 0 and (n + 128) * (-(-k // 128) * 128) < 2 ** 31
+
+    @classmethod
+    def prepare(cls, ctx: Context, b, b_zero=None) -> "Int8Weight":
+        """Prepares B [K, N] (u8 or s8, host or device) with b_zero_point (None, one value or
+        [N] of B's type)."""
+        b_t = b if isinstance(b, DeviceTensor) else ctx.put(np.ascontiguousarray(b))
+        z_t = b_zero if (b_zero is None or isinstance(b_zero, DeviceTensor)) else ctx.put(np.ascontiguousarray(b_zero))
+        try:
+            if len(b_t.shape) != 2:
+                raise _lib.TmhArgumentError(_lib.ERR_INVALID, f"a prepared MatMulInteger B is 2-D, got {b_t.shape}")
+            k, n = b_t.shape
+            handle = ctypes.c_void_p()
+            ctx.check(lib().tmh_int8_weight_prepare(ctx.handle, b_t.ptr, b_t.tmh_dtype,
+                                                    z_t.ptr if z_t is not None else None,
+                                                    z_t.size if z_t is not None else 0, k, n, None,
+                                                    ctypes.byref(handle)))
+            ctx.synchronize()
+        finally:
+            if b_t is not b:
+                b_t.free()
+            if z_t is not None and z_t is not b_zero:
+                z_t.free()
+        return cls(ctx, handle, k, n, b_t.dtype)
+
+    def device_bytes(self) -> int:
+        size = ctypes.c_size_t()
+        _lib.check(lib().tmh_int8_weight_info(self.handle, None, None, ctypes.byref(size)))
+        return size.value
+
+    def free(self) -> None:
+        if self.handle:
+            lib().tmh_int8_weight_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def __repr__(self) -> str:
+        return f"Int8Weight(K={self.k}, N={self.n}, {self.dtype})"

@@ -23,7 +23,7 @@ from . import _lib
 from ._lib import TmhArgumentError, lib
 from .device import FLOAT_TYPES, NX_TO_TMH, Context, DeviceTensor, merge_types, nx_type
 from .onnx_wire import ATTR_FLOAT, ATTR_FLOATS, ATTR_INT, ATTR_INTS, ATTR_STRING, ATTR_TENSOR
-from .packed import PackedWeight
+from .packed import Int8Weight, PackedWeight
 
 OP_TYPES = ["MatMulNBits", "GatherBlockQuantized", "DequantizeLinear", "MatMulInteger", "DynamicQuantizeLinear"]
 # The reference's other quantized handlers (quantized.ex:19-21), not on this path.
@@ -299,6 +299,8 @@ def _op_dequantize_linear(node, inputs):
 def _op_matmul_integer(node, inputs):
     a, b, *rest = inputs
     a_zero, b_zero = optional(rest, 2)
+    if isinstance(b, Int8Weight):
+        return _matmul_integer_prepared(a, b, a_zero, b_zero)
     ctx = _ctx_of(a, b, a_zero, b_zero)
     ashape, bshape = _shape_of(a), _shape_of(b)
     if len(ashape) < 1 or len(bshape) < 2:
@@ -344,6 +346,45 @@ def _op_matmul_integer(node, inputs):
                 t.free()
     if squeeze:
         return y.reshape(out_shape[:-2] + (n,))
+    return y
+
+
+def _matmul_integer_prepared(a, w: "Int8Weight", a_zero, b_zero):
+    """MatMulInteger over a B prepared at load (its b_zero_point is part of it): the same s32
+    sums as the plain path, through tmh_matmul_integer_prepared."""
+    if b_zero is not None:
+        raise ArgumentError("a prepared MatMulInteger B carries its own b_zero_point")
+    ctx = w.ctx
+    ashape = _shape_of(a)
+    if len(ashape) < 1:
+        raise ArgumentError(f"MatMulInteger of shape {ashape} is not supported")
+    squeeze = len(ashape) == 1
+    if squeeze:
+        ashape = (1,) + tuple(ashape)
+    m, k = ashape[-2], ashape[-1]
+    if k != w.k:
+        raise ArgumentError(f"MatMulInteger contracts {k} with {w.k}")
+    batch_shape = tuple(ashape[:-2])
+    batch = math.prod(batch_shape) if batch_shape else 1
+    if a_zero is not None and math.prod(_shape_of(a_zero)) not in (1, m):
+        raise ArgumentError(f"MatMulInteger a_zero_point has {math.prod(_shape_of(a_zero))} values")
+    a_t, own_a = _device(ctx, a)
+    az_t, own_az = _device(ctx, a_zero)
+    try:
+        out_shape = batch_shape + (m, w.n)
+        y = ctx.empty(out_shape, "s32")
+        ctx.check(lib().tmh_matmul_integer_prepared(ctx.handle, a_t.ptr, a_t.tmh_dtype,
+                                                    az_t.ptr if az_t is not None else None,
+                                                    az_t.size if az_t is not None else 0, batch, m, w.handle,
+                                                    y.ptr, None))
+    finally:
+        if own_a or own_az:
+            ctx.synchronize()
+        for t, own in ((a_t, own_a), (az_t, own_az)):
+            if own:
+                t.free()
+    if squeeze:
+        return y.reshape(out_shape[:-2] + (w.n,))
     return y
 
 
