@@ -277,10 +277,11 @@ def test_matmul_every_gemm_plan(ctx, monkeypatch, case, plan):
     w.free()
 
 
-# One row of A (decode at M = 1) goes to the dot-product GEMV (4- and 8-bit weights with one
-# parameter entry per lane) or, forced with TMH_GEMV_PLAN=mfma, to the MFMA GEMV: both against
-# the oracle, over resident and streaming grids, ragged K, a chunk wholly past K, many chunk rounds
-# and rows of A with padding (lda > K).
+# One row of A (decode at M = 1) over a streaming grid goes to the dot-product GEMV (4- and 8-bit
+# weights with one parameter entry per lane) or, forced with TMH_GEMV_PLAN=mfma, to the MFMA GEMV;
+# resident grids take the MFMA GEMV either way. Both against the oracle, over resident and
+# streaming grids, ragged K, a chunk wholly past K, many chunk rounds and rows of A with padding
+# (lda > K).
 ONE_ROW_CASES = [
     # bits, block, zp, K, N, lda
     (4, 32, "packed", 1024, 96, 1024),
@@ -289,6 +290,8 @@ ONE_ROW_CASES = [
     (4, 256, "packed", 104, 40, 112),
     (4, 64, "packed", 11008, 48, 11008),
     (4, 32, "packed", 1024, 30008, 1024),
+    (4, 32, "none", 2000, 16000, 2008),
+    (4, 128, "packed", 4096, 12000, 4096),
     (8, 32, "packed", 512, 48, 512),
     (8, 128, "none", 1000, 20, 1000),
     (8, 32, "none", 72, 24, 80),
@@ -326,12 +329,12 @@ def test_one_row_both_kernels(ctx, monkeypatch, case, plan):
 
 
 def test_one_row_dot_kernel_is_near_exact(ctx, monkeypatch):
-    """The dot-product GEMV sums exact products (q + 1024) * a in f32 and removes the offsets per
-    lane: against the f64 sum over the exact weights (q - zero) * scale its error is about one f16
-    output rounding."""
+    """The dot-product GEMV (one row of A over more tiles than the GPU holds at once) sums exact
+    products (q + 1024) * a in f32 and removes the offsets per lane: against the f64 sum over the
+    exact weights (q - zero) * scale its error is about one f16 output rounding."""
     monkeypatch.delenv("TMH_GEMV_PLAN", raising=False)
     rng = np.random.default_rng(15)
-    k, n = 3072, 512
+    k, n = 1024, 12800
     b, s, z = nbits_weight(rng, k, n, 4, 32, zp="packed")
     w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=4, block_size=32, weight_dtype="f16")
     a = rng.standard_normal((1, k)).astype(np.float16)

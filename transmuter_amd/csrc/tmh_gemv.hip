@@ -9,13 +9,18 @@
 //  - one-shot (the whole grid resident at once: the Qwen3-0.6B projections): one chunk per
 //    wavefront and round (U = 1), as many wavefronts as chunks (NW = nch, up to 16), one tile
 //    per workgroup. Latency-bound: more chunks per wavefront or more tiles per workgroup were
-//    0.07-0.4 us slower per launch. A is staged through LDS for M > 4.
+//    0.07-0.4 us slower per launch. A is staged through LDS for M > 4. Ablations at M = 1 (2.66
+//    us per launch): without the final store 2.40, without the cross-wavefront sum 2.47, without
+//    the unpack and MFMAs 2.41; an empty kernel costs 1.57 and a plain read of the weights 1.82.
 //  - streaming (lm_head-sized N): U = 2 chunks per wavefront loaded together, NW = nch / 2
-//    wavefronts, four tiles per workgroup, so every A fragment serves four tiles. On 151936 x 1024
-//    with random weights rotating over three copies (270 MB, more than the last-level cache) this
-//    takes 16.3-16.7 us at M = 1 and 17.0 us at M = 8, 5.4-5.5 TB/s (a plain read of the packed
-//    weights streams 6.7 TB/s); U = 1 with two rounds was 17.5-19.4 us. Persistent wavefronts
-//    that double-buffer whole tiles, and scales staged through LDS with wide loads, were no faster.
+//    wavefronts, four tiles per workgroup, so every A fragment serves four tiles (two tiles for
+//    one row of A, through k_gemv_dot). On 151936 x 1024 with random weights rotating over three
+//    copies (270 MB, more than the last-level cache): 17.0-17.4 us at M = 8 (5.3-5.4 TB/s) and
+//    15.7-16.2 us at M = 1 with k_gemv_dot (5.6-5.7 TB/s); a plain read of the same bytes takes
+//    14.2 us (6.5 TB/s). U = 1 with two rounds was 17.5-19.4 us. Persistent wavefronts that
+//    double-buffer whole tiles, one wavefront walking all of K for a group of tiles with loads
+//    three chunks ahead (19.5-23 us), A staged whole in LDS per workgroup (24-28 us), scales
+//    staged through LDS with wide loads, and non-temporal weight loads were no faster.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -100,25 +105,16 @@ void launch_bits(const DecArgs& d, int64_t M, int num_cus, hipStream_t s) {
   const int64_t resident = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * 24;
   const bool resident_grid = static_cast<int64_t>(d.ntiles) * std::min<int64_t>(nch, 16) <= resident;
   if constexpr (BITS != 2 && !SPLIT) {
-    if (M == 1 && dot_for_one_row()) {
-      if (resident_grid) {
-        switch (round_waves(nch)) {
-          case 1: go_dot<BITS, HAS_ZP, 1, 1, 1>(d, s); break;
-          case 2: go_dot<BITS, HAS_ZP, 2, 1, 1>(d, s); break;
-          case 4: go_dot<BITS, HAS_ZP, 4, 1, 1>(d, s); break;
-          case 8: go_dot<BITS, HAS_ZP, 8, 1, 1>(d, s); break;
-          case 12: go_dot<BITS, HAS_ZP, 12, 1, 1>(d, s); break;
-          default: go_dot<BITS, HAS_ZP, 16, 1, 1>(d, s);
-        }
-      } else {
-        // Streaming: two chunks per wavefront loaded together, two tiles per workgroup (151936 x
-        // 1024 q4: 15.7 us against 15.9 with four tiles and 17.0 for the MFMA kernel).
-        switch (std::min(8, round_waves((nch + 1) / 2))) {
-          case 1: go_dot<BITS, HAS_ZP, 1, 2, 2>(d, s); break;
-          case 2: go_dot<BITS, HAS_ZP, 2, 2, 2>(d, s); break;
-          case 4: go_dot<BITS, HAS_ZP, 4, 2, 2>(d, s); break;
-          default: go_dot<BITS, HAS_ZP, 8, 2, 2>(d, s);
-        }
+    // One row of A over a streaming grid: the dot-product kernel, two chunks per wavefront loaded
+    // together, two tiles per workgroup (151936 x 1024 q4: 15.7-16.2 us against 15.9 with four
+    // tiles and 17.0 for the MFMA kernel). Where the whole grid is resident the launch is latency-
+    // bound and the MFMA kernel is as fast (Qwen3-0.6B projections: 2.71 against 2.75 us).
+    if (M == 1 && !resident_grid && dot_for_one_row()) {
+      switch (std::min(8, round_waves((nch + 1) / 2))) {
+        case 1: go_dot<BITS, HAS_ZP, 1, 2, 2>(d, s); break;
+        case 2: go_dot<BITS, HAS_ZP, 2, 2, 2>(d, s); break;
+        case 4: go_dot<BITS, HAS_ZP, 4, 2, 2>(d, s); break;
+        default: go_dot<BITS, HAS_ZP, 8, 2, 2>(d, s);
       }
       return;
     }
