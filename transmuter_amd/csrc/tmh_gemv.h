@@ -155,9 +155,15 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
   for (int tn = 0; tn < TN; ++tn) {
     if constexpr (NW > 1) {
       if (tn % NW != static_cast<int>(wave)) continue;
-      acc[tn] = red[tn * 64 + lane];
+      // Every partial sum is read before the first is added (one LDS latency, not NW of them:
+      // left alone the compiler reads two at a time into reused registers).
+      float4_t part[NW];
 #pragma unroll
-      for (int w2 = 1; w2 < NW; ++w2) acc[tn] += red[w2 * RED_WAVE + tn * 64 + lane];
+      for (int w2 = 0; w2 < NW; ++w2) part[w2] = red[w2 * RED_WAVE + tn * 64 + lane];
+      __builtin_amdgcn_sched_barrier(0);
+      acc[tn] = part[0];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) acc[tn] += part[w2];
     } else if (wave != 0) {
       continue;
     }
@@ -200,7 +206,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dot(
   constexpr int CW = 512 / BITS;  // weights per chunk row
   constexpr int GW = CW / 4;      // weights per lane per chunk
   constexpr int NP = GW / 8;      // 16-byte pieces of A per lane per chunk
-  __shared__ float red[NW * TN * 64];
+  __shared__ __align__(16) float red[NW * TN * 64];
   (void)ldy;
   const uint32_t nbc = (shape >> 8) & 0xFFu, bsc_shift = (shape >> 16) & 0xFFu;
   const uint32_t K = nch * CW - (shape >> 24) * 4;
@@ -292,19 +298,25 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dot(
       }
     }
   }
+  // Row r's four lane sums of a wavefront sit together (one 16-byte read each).
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn) red[(wave * TN + tn) * 64 + lane] = acc[tn];
+  for (int tn = 0; tn < TN; ++tn) red[(wave * TN + tn) * 64 + r * 4 + g] = acc[tn];
   __syncthreads();
   // Tile tn's 16 sums are added by lanes 0-15 of wavefront tn % NW, each over its row's four
-  // lanes in every wavefront.
+  // lanes in every wavefront, in a fixed order; all the partial sums are read before the first
+  // is added.
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
     if (tn % NW != static_cast<int>(wave) || g != 0) continue;
+    float4_t part[NW];
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) part[w2] = reinterpret_cast<const float4_t*>(red)[(w2 * TN + tn) * 16 + r];
+    __builtin_amdgcn_sched_barrier(0);
     float v = 0.f;
 #pragma unroll
     for (int w2 = 0; w2 < NW; ++w2)
 #pragma unroll
-      for (int g2 = 0; g2 < 4; ++g2) v += red[(w2 * TN + tn) * 64 + g2 * 16 + r];
+      for (int g2 = 0; g2 < 4; ++g2) v += part[w2][g2];
     const uint32_t n = (t0 + tn) * 16 + r;
     if (n < N) Y[n] = static_cast<_Float16>(v);
   }
