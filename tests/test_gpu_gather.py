@@ -32,6 +32,13 @@ CASES = [
     (4, 100, 768, 48, "s8", "s8", "f32", (7, 3), np.int32),  # 3 slices per row, signed data and zero points
     (8, 64, 512, 16, "s8", None, "f16", (5,)),               # q8 signed, no zero points
     (4, 500, 256, 16, "u8", None, "bf16", (1,)),             # one id, one slice
+    # the same kernel's packed-f16 arithmetic: every signedness of data and zero points
+    (4, 100, 512, 32, "s8", "s8", "f16", (9, 3), np.int32),  # signed nibbles and zero points
+    (4, 100, 256, 16, "s8", None, "f16", (7,)),              # signed nibbles, zero point 0
+    (4, 100, 256, 8, "u8", "s8", "f16", (5,)),               # unsigned nibbles, signed zero points
+    (8, 100, 512, 16, "u8", "u8", "f16", (6,)),              # q8 with zero points
+    (8, 100, 256, 4, "s8", "u8", "f16", (5,)),               # signed bytes, unsigned zero points
+    (8, 100, 256, 8, "u8", None, "f16", (3, 3)),             # q8, default zero point 128
 ]
 
 
@@ -88,4 +95,29 @@ def test_gather_vocab_table(ctx, zp):
     got = quantized.apply(node, args)[0].numpy()
     ref = o.gather_block_quantized(data, ids, scales, zero, bits=4)
     assert got.shape == (8, 512, d)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_f16_extreme_scales(ctx, bits):
+    """f16 scales at the edges of the format (zero, both signs, subnormals, the largest finite
+    value, whose products overflow to infinity) through the multi-slice kernel's packed-f16
+    arithmetic: the one rounding of (q - zero) * scale matches the oracle's bit for bit."""
+    print(f"gather f16 extreme scales bits={bits}", flush=True)
+    rng = np.random.default_rng(31 + bits)
+    rows, row_bytes = 64, 512
+    d = row_bytes * 8 // bits
+    blocks = d // 32
+    special = np.array([0.0, -0.0, 6e-8, -6e-8, 3e-5, 6.1e-5, 1.0, -0.5, 65504.0, -65504.0, 0.33325, 1e-3],
+                       np.float16)
+    scales = rng.choice(special, (rows, blocks)).astype(np.float16)
+    data = rng.integers(0, 256, (rows, row_bytes), dtype=np.uint8)
+    zero = rng.integers(0, 256, (rows, -(-blocks * bits // 8)), dtype=np.uint8)
+    ids = rng.integers(0, rows, (40,), dtype=np.int64)
+    node = NodeProto(op_type="GatherBlockQuantized", input=["data", "ids", "scales", "zp"], output=["out"],
+                     attribute=[AttributeProto(name="bits", type=ATTR_INT, i=bits)])
+    got = quantized.apply(node, [ctx.put(data), ctx.put(ids), ctx.put(scales), ctx.put(zero)])[0].numpy()
+    ref = o.gather_block_quantized(data, ids, scales, zero, bits=bits)
+    bits16 = ref.view(np.uint16)
+    assert np.isinf(ref.astype(np.float32)).any() and (((bits16 & 0x7C00) == 0) & ((bits16 & 0x3FF) != 0)).any()
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))

@@ -188,6 +188,10 @@ __device__ __forceinline__ int frag_swizzle(int r) {
 // Raw buffer resource over `bytes` bytes: a load whose VGPR offset is at or beyond `bytes`
 // returns zeros, so tiles past N need no address clamps or selects. Every in-range access of
 // these kernels stays inside its buffer.
+// Cache policy of a buffer store whose data no later instruction of the kernel reads: the nt
+// bit (streaming), so an output written once does not displace the inputs still being read.
+constexpr int kNonTemporal = 2;
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
                                            0x00020000);

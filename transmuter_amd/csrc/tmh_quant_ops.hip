@@ -138,19 +138,23 @@ void launch_gather_ub(const uint8_t* data, bool sgn, int64_t rows, int64_t row_b
 }
 
 // Rows of whole 256-byte slices (row_bytes % 256 == 0), 4 bytes per lane in one quantization
-// block, 16-byte-aligned output: each wavefront takes S consecutive (id, slice) pairs. Its ids
-// are wavefront-uniform (scalar loads, one cache line for all of them), and the data, scale and
-// zero point loads of all S slices issue before the first value is computed, so a wavefront pays
-// the id latency and the row latency once for S slices instead of once per half row. Each
-// slice's values leave as one 16-byte store per lane (1 KiB contiguous per instruction). A
-// slice past the end (the last wavefront's) stores to an offset beyond the output buffer's
-// range, which the hardware drops: no branch, so no slice's loads wait behind another's stores.
+// block, 16-byte-aligned output: each wavefront takes S consecutive (id, slice) pairs. Lane j
+// loads slice j's id (one vector load for the wavefront) and each row is broadcast from its lane;
+// the data, scale and zero point loads of all S slices then issue before the first value is
+// computed, so a wavefront pays the id latency and the row latency once for S slices instead of
+// once per half row. Each slice's values leave as one 16-byte non-temporal store per lane (1 KiB
+// contiguous per instruction): at the [8, 512] x 1024 f16 lookup the 8 MiB of output cost 1.4 us
+// over an empty launch with ordinary stores and 0.9 us with non-temporal ones. A slice past the
+// end (the last wavefront's) stores to an offset beyond the output buffer's range, which the
+// hardware drops: no branch, so no slice's loads wait behind another's stores. `spr_magic` is
+// floor(2^32 / slices_per_row) + 1 (slices_per_row > 1): umulhi(sl, spr_magic) equals
+// sl / slices_per_row for every sl < 2^32 / slices_per_row, which the launcher checks.
 template <int DT, int BITS, int S, bool IDS64, bool HAS_ZP>
 __global__ __launch_bounds__(256) void k_gather_bq_rows(
     const uint8_t* __restrict__ data, bool data_signed, uint32_t rows, uint32_t row_bytes,
-    const void* __restrict__ ids, uint32_t n_slices, uint32_t slices_per_row, const void* __restrict__ scales,
-    uint32_t blocks, uint32_t bs_shift, const uint8_t* __restrict__ zp, bool zp_signed, uint32_t zrow,
-    void* __restrict__ out) {
+    const void* __restrict__ ids, uint32_t n_slices, uint32_t slices_per_row, uint32_t spr_magic,
+    const void* __restrict__ scales, uint32_t blocks, uint32_t bs_shift, const uint8_t* __restrict__ zp,
+    bool zp_signed, uint32_t zrow, void* __restrict__ out) {
   constexpr int PER = 8 / BITS;
   constexpr int V = 4 * PER;  // values per lane and slice
   constexpr int ES = DT == DT_F32 ? 4 : 2;
@@ -167,8 +171,9 @@ __global__ __launch_bounds__(256) void k_gather_bq_rows(
   // is broadcast from its lane), then every data, scale and zero point load, then the values.
   const uint32_t my_sl = s0 + (lane < S ? lane : S - 1) < n_slices ? s0 + (lane < S ? lane : S - 1) : n_slices - 1;
   int64_t my_id;
-  if constexpr (IDS64) my_id = static_cast<const int64_t*>(ids)[my_sl / slices_per_row];
-  else my_id = static_cast<const int32_t*>(ids)[my_sl / slices_per_row];
+  const uint32_t my_i = slices_per_row == 1 ? my_sl : __umulhi(my_sl, spr_magic);
+  if constexpr (IDS64) my_id = static_cast<const int64_t*>(ids)[my_i];
+  else my_id = static_cast<const int32_t*>(ids)[my_i];
   my_id = my_id < 0 ? my_id + rows : my_id;  // ONNX: a negative index counts from the end
   const uint32_t my_row = static_cast<uint32_t>(my_id < 0 ? 0 : (my_id >= rows ? rows - 1 : my_id));
   uint32_t row[S];
@@ -179,7 +184,7 @@ __global__ __launch_bounds__(256) void k_gather_bq_rows(
 #pragma unroll
   for (int j = 0; j < S; ++j) {
     const uint32_t sl = s0 + j < n_slices ? s0 + j : n_slices - 1;
-    const uint32_t i = sl / slices_per_row;
+    const uint32_t i = slices_per_row == 1 ? sl : __umulhi(sl, spr_magic);
     const uint32_t r = row[j];
     const uint32_t byte = (sl - i * slices_per_row) * 256 + lane * 4;
     const uint32_t blk = (byte * PER) >> bs_shift;
@@ -192,61 +197,100 @@ __global__ __launch_bounds__(256) void k_gather_bq_rows(
 #pragma unroll
   for (int j = 0; j < S; ++j) {
     const uint32_t sl = s0 + j;
-    const uint32_t i = sl / slices_per_row;
-    float z;
-    if constexpr (HAS_ZP) {
-      int zq;
-      if constexpr (BITS == 8) {
-        zq = zp_signed ? static_cast<int>(static_cast<int8_t>(zv[j])) : static_cast<int>(zv[j] & 0xFFu);
-      } else {
-        zq = (zv[j] >> (bit[j] % 8)) & ((1 << BITS) - 1);
-        if (zp_signed && zq >= (1 << (BITS - 1))) zq -= (1 << BITS);
-      }
-      z = static_cast<float>(zq);
-    } else {
-      z = data_signed ? 0.f : static_cast<float>(1 << (BITS - 1));
-    }
-    float sc;
-    if constexpr (DT == DT_F32) sc = __builtin_bit_cast(float, sv[j]);
-    else if constexpr (DT == DT_F16) sc = f16_bits_to_f32(static_cast<uint16_t>(sv[j]));
-    else sc = bf16_bits_to_f32(static_cast<uint16_t>(sv[j]));
-    float vals[V];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const uint32_t byte = (x[j] >> (8 * b)) & 0xFFu;
-#pragma unroll
-      for (int v = 0; v < PER; ++v) {
-        int q;
-        if constexpr (BITS == 8) {
-          q = data_signed ? static_cast<int>(static_cast<int8_t>(byte)) : static_cast<int>(byte);
-        } else {
-          q = (byte >> (v * BITS)) & ((1 << BITS) - 1);
-          if (data_signed && q >= (1 << (BITS - 1))) q -= (1 << BITS);
-        }
-        vals[b * PER + v] = dequant_value<DT>(static_cast<float>(q), z, sc);
-      }
-    }
+    const uint32_t i = slices_per_row == 1 ? sl : __umulhi(sl, spr_magic);
     uint32_t words[V * ES / 4];
-#pragma unroll
-    for (int k = 0; k < V * ES / 4; ++k) {
-      if constexpr (DT == DT_F32) {
-        words[k] = __builtin_bit_cast(uint32_t, vals[k]);
-      } else if constexpr (DT == DT_F16) {
-        words[k] = f32_to_f16_bits(vals[2 * k]) | (static_cast<uint32_t>(f32_to_f16_bits(vals[2 * k + 1])) << 16);
+    if constexpr (DT == DT_F16) {
+      // Packed f16: each 32-bit word holds the values 2k, 2k+1 as 1024 + q (0x6400 | q), the
+      // nibbles' high one at bits 20-23 (1024 + 16 q), so one fma per pair gives q - zero
+      // exactly and one multiply by the scale rounds once, as the f32 product rounded to f16
+      // does (the product of two f16 values is exact in f32). Signed values are offset by
+      // 2^(BITS-1) (their top bit flipped), and the zero point with them.
+      constexpr int HALF = 1 << (BITS - 1);
+      int zq;
+      if constexpr (HAS_ZP) {
+        if constexpr (BITS == 8) {
+          zq = zp_signed ? static_cast<int>(static_cast<int8_t>(zv[j])) : static_cast<int>(zv[j] & 0xFFu);
+        } else {
+          zq = (zv[j] >> (bit[j] % 8)) & ((1 << BITS) - 1);
+          if (zp_signed && zq >= HALF) zq -= (1 << BITS);
+        }
       } else {
-        words[k] = f32_to_bf16_bits(vals[2 * k]) | (static_cast<uint32_t>(f32_to_bf16_bits(vals[2 * k + 1])) << 16);
+        zq = data_signed ? 0 : HALF;
+      }
+      const int zz = zq + (data_signed ? HALF : 0);
+      const uint32_t xs = data_signed ? x[j] ^ (BITS == 4 ? 0x88888888u : 0x80808080u) : x[j];
+      const _Float16 s16 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sv[j]));
+      const half2_t s2 = {s16, s16};
+      if constexpr (BITS == 4) {
+        const half2_t mul = {static_cast<_Float16>(1.0f), static_cast<_Float16>(0.0625f)};
+        const half2_t add = {static_cast<_Float16>(-(1024 + zz)), static_cast<_Float16>(-(64 + zz))};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t p = (__builtin_amdgcn_perm(xs, xs, 0x01010101u * k) & 0x00F0000Fu) | 0x64006400u;
+          const half2_t d = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, p), mul, add);
+          words[k] = __builtin_bit_cast(uint32_t, d * s2);
+        }
+      } else {
+        const _Float16 a = static_cast<_Float16>(-(1024 + zz));
+        const half2_t add = {a, a};
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const uint32_t sel = (2 * k) * 0x00000101u + (2 * k + 1) * 0x01010000u;  // bytes 2k, 2k+1 to 0, 2
+          const uint32_t p = (__builtin_amdgcn_perm(xs, xs, sel) & 0x00FF00FFu) | 0x64006400u;
+          const half2_t d = __builtin_bit_cast(half2_t, p) + add;
+          words[k] = __builtin_bit_cast(uint32_t, d * s2);
+        }
+      }
+    } else {
+      float z;
+      if constexpr (HAS_ZP) {
+        int zq;
+        if constexpr (BITS == 8) {
+          zq = zp_signed ? static_cast<int>(static_cast<int8_t>(zv[j])) : static_cast<int>(zv[j] & 0xFFu);
+        } else {
+          zq = (zv[j] >> (bit[j] % 8)) & ((1 << BITS) - 1);
+          if (zp_signed && zq >= (1 << (BITS - 1))) zq -= (1 << BITS);
+        }
+        z = static_cast<float>(zq);
+      } else {
+        z = data_signed ? 0.f : static_cast<float>(1 << (BITS - 1));
+      }
+      float sc;
+      if constexpr (DT == DT_F32) sc = __builtin_bit_cast(float, sv[j]);
+      else if constexpr (DT == DT_F16) sc = f16_bits_to_f32(static_cast<uint16_t>(sv[j]));
+      else sc = bf16_bits_to_f32(static_cast<uint16_t>(sv[j]));
+      float vals[V];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = (x[j] >> (8 * b)) & 0xFFu;
+#pragma unroll
+        for (int v = 0; v < PER; ++v) {
+          int q;
+          if constexpr (BITS == 8) {
+            q = data_signed ? static_cast<int>(static_cast<int8_t>(byte)) : static_cast<int>(byte);
+          } else {
+            q = (byte >> (v * BITS)) & ((1 << BITS) - 1);
+            if (data_signed && q >= (1 << (BITS - 1))) q -= (1 << BITS);
+          }
+          vals[b * PER + v] = dequant_value<DT>(static_cast<float>(q), z, sc);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < V * ES / 4; ++k) {
+        if constexpr (DT == DT_F32) words[k] = __builtin_bit_cast(uint32_t, vals[k]);
+        else words[k] = f32_to_bf16_bits(vals[2 * k]) | (static_cast<uint32_t>(f32_to_bf16_bits(vals[2 * k + 1])) << 16);
       }
     }
     const uint32_t o = (i * D + ((sl - i * slices_per_row) * 256 + lane * 4) * PER) * ES;
     const uint32_t off = sl < n_slices ? o : 0xFFFFFF00u;  // past the range: dropped
     if constexpr (V * ES == 8) {  // 8-bit values in a 2-byte type: 8 bytes per lane
       typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
-      __builtin_amdgcn_raw_buffer_store_b64(uint2_t{words[0], words[1]}, o_rsrc, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(uint2_t{words[0], words[1]}, o_rsrc, off, 0, kNonTemporal);
     } else {
 #pragma unroll
       for (int k = 0; k < V * ES / 16; ++k)
         __builtin_amdgcn_raw_buffer_store_b128(uint4_t{words[4 * k], words[4 * k + 1], words[4 * k + 2], words[4 * k + 3]},
-                                               o_rsrc, off + 16 * k, 0, 0);
+                                               o_rsrc, off + 16 * k, 0, kNonTemporal);
     }
   }
 }
@@ -260,9 +304,10 @@ void launch_gather_rows(const uint8_t* data, bool sgn, int64_t rows, int64_t row
   int shift = 0;
   while ((int64_t(1) << shift) < bs) ++shift;
   const int64_t waves = (n_slices + S - 1) / S;
+  const auto magic = static_cast<uint32_t>((uint64_t(1) << 32) / static_cast<uint64_t>(spr) + 1);
   k_gather_bq_rows<DT, BITS, S, IDS64, HAS_ZP><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, s>>>(
       data, sgn, static_cast<uint32_t>(rows), static_cast<uint32_t>(row_bytes), ids, static_cast<uint32_t>(n_slices),
-      static_cast<uint32_t>(spr), scales, static_cast<uint32_t>(blocks), static_cast<uint32_t>(shift),
+      static_cast<uint32_t>(spr), magic, scales, static_cast<uint32_t>(blocks), static_cast<uint32_t>(shift),
       static_cast<const uint8_t*>(zp), zp_signed, static_cast<uint32_t>(zrow), out);
 }
 
@@ -284,7 +329,8 @@ void launch_gather(const uint8_t* data, bool sgn, int64_t rows, int64_t row_byte
     if constexpr (BITS != 2) {
       if (one && vec_out && row_bytes % 256 == 0 && (bs & (bs - 1)) == 0 && (!zp || packed_zp) &&
           rows * row_bytes < (int64_t(1) << 32) && rows * blocks * ES < (int64_t(1) << 32) &&
-          rows * zrow < (int64_t(1) << 32) && n_ids * D * ES < (int64_t(1) << 32) - 256) {
+          rows * zrow < (int64_t(1) << 32) && n_ids * D * ES < (int64_t(1) << 32) - 256 &&
+          n_ids * (row_bytes / 256) * (row_bytes / 256) < (int64_t(1) << 32)) {
         const bool zs = zp_dt == TMH_S8;
         if (ids64 && zp) launch_gather_rows<DT, BITS, true, true>(data, sgn, rows, row_bytes, ids, n_ids, scales, blocks, bs, zp, zs, zrow, out, s);
         else if (ids64) launch_gather_rows<DT, BITS, true, false>(data, sgn, rows, row_bytes, ids, n_ids, scales, blocks, bs, zp, zs, zrow, out, s);
@@ -463,14 +509,16 @@ __global__ __launch_bounds__(256) void k_dequantize_linear_b4(const uint32_t* __
     const int z = SIGNED ? static_cast<int>(static_cast<int8_t>(zb)) : static_cast<int>(zb);
     out[j] = static_cast<float>(q - z) * sc[j];
   }
+  // Non-temporal stores: the output (four times the input's bytes in f32) is not read again here.
   if constexpr (OUT == DT_F32) {
-    reinterpret_cast<float4_t*>(y)[t] = float4_t{out[0], out[1], out[2], out[3]};
+    __builtin_nontemporal_store(float4_t{out[0], out[1], out[2], out[3]}, reinterpret_cast<float4_t*>(y) + t);
   } else {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
     uint16_t h[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) h[j] = OUT == DT_F16 ? f32_to_f16_bits(out[j]) : f32_to_bf16_bits(out[j]);
-    reinterpret_cast<uint2*>(y)[t] =
-        make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+    __builtin_nontemporal_store(u32x2_t{h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16)},
+                                reinterpret_cast<u32x2_t*>(y) + t);
   }
 }
 
