@@ -270,7 +270,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmi_bt(const uint8_t* __restrict__ 
         out[e] = static_cast<int32_t>(static_cast<uint32_t>(v[e]) + cbn * rs + ca * csn + K * ca * cbn);
       }
       if (y_vec) {
-        *reinterpret_cast<int4_t*>(yrow + n) = out;
+        __builtin_nontemporal_store(out, reinterpret_cast<int4_t*>(yrow + n));
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
