@@ -533,17 +533,15 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
                                  __builtin_bit_cast(half2_t, sv | (sv << 16)));
     }
   };
-  // The next k-block's loads, spread over the steps of this one so that the eight wavefronts
-  // do not queue all of them on the CU's memory path at once after each barrier: A in the first
-  // half of the steps, then the weights, so the A loads still precede the weight loads (WAIT_A).
-  constexpr int HA = LSTEPS > 1 ? LSTEPS / 2 : 1;
-  constexpr int HB = LSTEPS > 1 ? LSTEPS - HA : 1;
+  // The next k-block's loads: the weights, scales and zero points (from HBM, the longest
+  // latency) at the first step, the A tile (L2) spread over the steps so that the eight
+  // wavefronts do not queue all of it on the CU's memory path at once after each barrier. The
+  // barrier at the end of the k-block waits for all of them. (Weights issued after the A tile,
+  // in the second half of the steps: 357 against 371 TFLOP/s over the SmolLM3-3B projections at
+  // M = 256, the same at M = 2048.)
   auto issue = [&](int i, uint32_t kb, int buf, BStage& st) {
-    if (i < HA) load_a(kb, buf, i * LOADS / HA, (i + 1) * LOADS / HA);
-    if (LSTEPS == 1 || i >= HA) {
-      const int ib = LSTEPS == 1 ? 0 : i - HA;
-      load_b(kb, st, ib * NTW / HB, (ib + 1) * NTW / HB);
-    }
+    if (i == 0) load_b(kb, st);
+    load_a(kb, buf, i * LOADS / LSTEPS, (i + 1) * LOADS / LSTEPS);
   };
   // Software pipeline over the k-block's steps: once fragment mt of step i has fed its four
   // MFMAs, the same registers take fragment mt of step i+1 from LDS; step i+1's weights are
@@ -611,11 +609,6 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
       }
     }
   };
-  // Loads issued after the A tile of a k-block: its weights, scales and zero points. Waiting
-  // until only these are outstanding means the A tile has landed in LDS.
-  constexpr int B_LOADS = NTW + NTW * NJ + (HAS_ZP ? NTW * NJ : 0);
-  constexpr int WAIT_A = (B_LOADS & 15) | (7 << 4) | (15 << 8) | ((B_LOADS >> 4) << 14);
-
   BStage cur, next;
   load_a(kb0, 0);
   load_b(kb0, cur);
@@ -630,7 +623,7 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
     const bool more = kb + 1 < kb1;
     compute(buf, cur, more, kb + 1, next);
     if (more) {
-      __builtin_amdgcn_s_waitcnt(WAIT_A);
+      __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
     if (more) cur = next;
@@ -662,7 +655,9 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
   // the MFMA layout a lane holds 4 columns: 16 rows x 8 or 16 bytes per instruction). The tile
   // goes in passes of as many rows as the LDS holds; 16-byte units are XOR-swizzled by row.
   // (Stores measured 4-9% of the SmolLM3-3B projections at M = 2048, 25% at M = 256; f32
-  // partial sums that need two passes were slower staged than stored directly, 16 bytes a lane.)
+  // partial sums that need two passes were slower staged than stored directly, 16 bytes a lane.
+  // The f16 rows store non-temporally: 2048 -> 11008 at M = 2048, 45 MB out, 109.8 -> 107.9 us;
+  // the partial sums, read back by the reduction, gain nothing from it.)
   constexpr bool kPartialsFit = static_cast<int>(gemm_lds_bytes<BITS, BM, KS>()) >= BM * 64 * WN * 4;
   const bool staged = ws ? kPartialsFit && (N % 4) == 0
                          : f16_out && (ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
@@ -718,7 +713,7 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
           } else {
             uint16_t* dst = static_cast<uint16_t*>(Y) + m * ldy + n;
             if (n + 8 <= N) {
-              *reinterpret_cast<uint4_t*>(dst) = v;
+              __builtin_nontemporal_store(v, reinterpret_cast<uint4_t*>(dst));
             } else {
               const uint32_t words[4] = {v[0], v[1], v[2], v[3]};
               for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = static_cast<uint16_t>(words[e >> 1] >> ((e & 1) * 16));
