@@ -314,11 +314,14 @@ def single_op(ctx, reps, copies=160):
 # ---------------------------------------------------------------- prefill GEMM
 
 
-def prefill(ctx, reps, ms_list, per_graph=8, rotate_bytes=320 << 20):
+ROTATE_BYTES = 1 << 30  # weight copies a workload's calls rotate over: 4x the 256 MB last-level cache
+
+
+def prefill(ctx, reps, ms_list, per_graph=8, rotate_bytes=ROTATE_BYTES):
     """SmolLM3-3B projections, q4 block 128, at each M: `per_graph` calls per graph. Each
-    projection's calls rotate over device copies of its weight totalling more than the 256 MB
-    last-level cache (`rotate_bytes`), so the weights stream from HBM as a model's would; the
-    graphs are replayed round robin."""
+    projection's calls rotate over device copies of its weight totalling `rotate_bytes` (four
+    times the 256 MB last-level cache), so the weights stream from HBM as a model's would; the
+    graphs are replayed round robin, each at least once per timed run."""
     from transmuter_amd import PackedWeight
 
     rng = np.random.default_rng(3)
@@ -339,10 +342,11 @@ def prefill(ctx, reps, ms_list, per_graph=8, rotate_bytes=320 << 20):
             ctx.synchronize()
             graphs = [Graph(ctx, lambda i=i, a=a, y=y: [matmul_call(ctx, copies[i + j], a, y, m) for j in range(per_graph)])
                       for i in range(0, len(copies), per_graph)]
-            ms_total = time_graphs(ctx, graphs, reps, 3)
+            steps = max(reps, len(graphs))
+            ms_total = time_graphs(ctx, graphs, steps, 3)
             for g in graphs:
                 g.destroy()
-            us = ms_total * 1e3 / (reps * per_graph)
+            us = ms_total * 1e3 / (steps * per_graph)
             flops = 2 * m * k * n
             per.append({"proj": name, "M": m, "us": us, "tflops": flops / (us * 1e-6) / 1e12,
                         "weight_copies": len(copies)})
@@ -362,16 +366,16 @@ def prefill(ctx, reps, ms_list, per_graph=8, rotate_bytes=320 << 20):
 def large_vocab(ctx, reps, per_graph=21):
     """lm_head MatMulNBits (M=1 and M=8) and the tied-embedding GatherBlockQuantized lookup. Each
     graph holds `per_graph` calls, so one graph launch's own cost spreads over them; the lm_head
-    calls rotate over 3 weight copies (276 MB, more than the 256 MB last-level cache) and every
-    gather call reads its own 4096 ids, from 2 tables."""
+    calls rotate over 12 weight copies (1.1 GB, four times the 256 MB last-level cache) and
+    every gather call reads its own 4096 ids, from 2 tables."""
     from transmuter_amd import PackedWeight
     from transmuter_amd._lib import F16, S64, U8, lib
 
     rng = np.random.default_rng(4)
     vocab, hidden = 151936, 1024
     b, sc, zp = make_weight_parts(rng, hidden, vocab)
-    ws = [PackedWeight.upload(ctx, b, sc, zp, k=hidden, n=vocab, bits=4, block_size=32, weight_dtype="f16")
-          for _ in range(3)]
+    ws = [PackedWeight.upload(ctx, b, sc, zp, k=hidden, n=vocab, bits=4, block_size=32, weight_dtype="f16")]
+    ws += [PackedWeight.concat([ws[0]]) for _ in range(-(-ROTATE_BYTES // ws[0].device_bytes()) - 1)]
     out = {}
     for m in (1, 8):
         a = ctx.put(rng.standard_normal((m, hidden), dtype=np.float32).astype(np.float16))
@@ -388,6 +392,17 @@ def large_vocab(ctx, reps, per_graph=21):
         out[f"lm_head_M{m}"] = {"us": us, "gbs": lm_bytes / (us * 1e-6) / 1e9,
                                 "frac": lm_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
         log(f"lm_head M={m}: {us:.1f} us, {lm_bytes / us / 1e3:.0f} GB/s")
+    # The read floor at this shape: a plain read of each copy's packed weights (the GEMV's load
+    # pattern, not its scales and zero points) over the same rotation.
+    sink = ctx.empty((16,), "u8")
+    g = Graph(ctx, lambda: [ctx.check(lib().tmh_floor_read(ctx.handle, ws[i % len(ws)].handle, sink.ptr, None))
+                            for i in range(per_graph)])
+    us = time_graphs(ctx, [g], reps, 3) * 1e3 / (reps * per_graph)
+    g.destroy()
+    q_bytes = vocab * hidden // 2
+    out["lm_head_read_floor"] = {"us": us, "gbs": q_bytes / (us * 1e-6) / 1e9, "weight_copies": len(ws)}
+    log(f"lm_head read floor: {us:.1f} us for the {q_bytes / 1e6:.1f} MB of packed weights, "
+        f"{q_bytes / us / 1e3:.0f} GB/s ({len(ws)} copies)")
     for w in ws:
         w.free()
     tables = [(ctx.put(b.reshape(vocab, -1)), ctx.put(sc.reshape(vocab, -1)), ctx.put(zp.reshape(vocab, -1)))
@@ -414,11 +429,15 @@ def large_vocab(ctx, reps, per_graph=21):
 # ---------------------------------------------------------------- quantized MoE
 
 
-def moe_ffn(ctx, reps, per_graph=4):
+def moe_ffn(ctx, reps, per_graph=6, sets=3):
     """QMoE at the Qwen3-30B-A3B expert shape: 128 experts, top-8 routing, hidden 2048,
     intermediate 768, SwiGLU (gate fc1, linear fc3, down fc2), q4 block 32 with f16 scales (no
     zero points), 512 tokens of f16 activations and N(0,1) router logits; routing, grouping, the
-    three grouped expert products, activation and the weighted sum in each call."""
+    three grouped expert products, activation and the weighted sum in each call. The calls
+    rotate over `sets` device copies of the layer's expert weights (3: 1.05 GB, four times the
+    256 MB last-level cache)."""
+    import ctypes
+
     from transmuter_amd._lib import F16, F32, lib
     from transmuter_amd.moe import ExpertWeight
 
@@ -430,22 +449,31 @@ def moe_ffn(ctx, reps, per_graph=4):
         scales = (np.abs(rng.standard_normal((experts, n, kk // 32), dtype=np.float32)) * 0.01 + 1e-4).astype(np.float16)
         return ExpertWeight.upload(ctx, packed, scales, None, bits=4, block_size=32, dtype="f16")
 
-    fc1, fc3, fc2 = expert_weight(inter, hidden), expert_weight(inter, hidden), expert_weight(hidden, inter)
+    def device_copy(w):
+        handle = ctypes.c_void_p()
+        ctx.check(lib().tmh_weight_concat_nbits(ctx.handle, (ctypes.c_void_p * 1)(w.handle.value), 1,
+                                                ctypes.byref(handle)))
+        return ExpertWeight(ctx, handle, w.experts, w.n, w.k, w.bits, w.dtype)
+
+    first = (expert_weight(inter, hidden), expert_weight(inter, hidden), expert_weight(hidden, inter))
+    layers = [first] + [tuple(device_copy(w) for w in first) for _ in range(sets - 1)]
     x = ctx.put(rng.standard_normal((tokens, hidden), dtype=np.float32).astype(np.float16))
     router = ctx.put(rng.standard_normal((tokens, experts), dtype=np.float32))
     y = ctx.empty((tokens, hidden), "f16")
 
-    def call():
+    def call(i):
+        fc1, fc3, fc2 = layers[i % len(layers)]
         ctx.check(lib().tmh_qmoe(ctx.handle, x.ptr, F16, tokens, hidden, router.ptr, F32, experts, k, fc1.handle, None,
                                  fc2.handle, None, fc3.handle, None, F16, 4, 0, 1.0, 0.0, 0.0, y.ptr, None))
 
-    call()  # eager first: sizes the workspace before capture
+    call(0)  # eager first: sizes the workspace before capture
     ctx.synchronize()
-    g = Graph(ctx, lambda: [call() for _ in range(per_graph)])
+    g = Graph(ctx, lambda: [call(i) for i in range(per_graph)])
     us = time_graphs(ctx, [g], reps, 2) * 1e3 / (reps * per_graph)
     g.destroy()
-    for w in (fc1, fc2, fc3):
-        w.free()
+    for layer in layers:
+        for w in layer:
+            w.free()
     flops = tokens * k * 2 * 3 * hidden * inter
     weight_bytes = experts * 3 * hidden * inter * (0.5 + 2 / 32)
     log(f"moe 128x top-8 2048/768 T={tokens}: {us:.1f} us, {flops / us / 1e6:.1f} TFLOP/s, "
@@ -626,7 +654,7 @@ def profile_run(ctx, kind, steps, m=1):
             ctx.check(lib().tmh_copy_2d(ctx.handle, dst.ptr, COPY_BYTES, src.ptr, COPY_BYTES, COPY_BYTES, 1, None))
         ctx.synchronize()
     elif kind == "moe":
-        moe_ffn(ctx, steps, per_graph=1)
+        moe_ffn(ctx, steps, per_graph=3)
     elif kind == "vocab":
         large_vocab(ctx, steps, per_graph=3)
     elif kind == "int8":
