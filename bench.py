@@ -695,7 +695,8 @@ def write_traffic(fetch_dir, write_dir):
     """Writes the decode GEMV's HBM traffic per launch (TRAFFIC_FILE) from two rocprofv3 --pmc runs
     of `--profile decode`, one with FETCH_SIZE and one with WRITE_SIZE. Each counter is scaled by
     what it reads for the 256 MiB calibration copy of the same run (bytes known), and averaged
-    over every k_gemv_dec dispatch: the 7 projections run equally often."""
+    over every dispatch of the decode GEMV (k_gemv_dot at M = 1, k_gemv_dec above): the 7
+    projections run equally often."""
     import csv
     import glob
 
@@ -705,12 +706,12 @@ def write_traffic(fetch_dir, write_dir):
             for r in csv.DictReader(open(f)):
                 if r["Counter_Name"] != counter:
                     continue
-                if "k_gemv_dec" in r["Kernel_Name"]:
+                if "k_gemv_dec" in r["Kernel_Name"] or "k_gemv_dot" in r["Kernel_Name"]:
                     gemv.append(float(r["Counter_Value"]))
                 elif "copyBufferRect" in r["Kernel_Name"]:
                     copy.append(float(r["Counter_Value"]))
         if not gemv or not copy:
-            raise SystemExit(f"{d}: no k_gemv_dec or calibration-copy rows for {counter}")
+            raise SystemExit(f"{d}: no decode GEMV or calibration-copy rows for {counter}")
         return sum(gemv) / len(gemv), sum(copy) / len(copy), len(gemv)
 
     fetch, fetch_copy, n_f = read(fetch_dir, "FETCH_SIZE")
@@ -719,7 +720,7 @@ def write_traffic(fetch_dir, write_dir):
     fs, ws = copy_kib / fetch_copy, copy_kib / write_copy
     hbm = (fetch * fs + write * ws) * 1024
     algo = sum(nbits_bytes(k, n, 1) for _, k, n in QWEN3_06B) / len(QWEN3_06B)
-    t = {"what": "HBM bytes per k_gemv_dec launch over the 7 Qwen3-0.6B q4 decode projections at M=1 "
+    t = {"what": "HBM bytes per k_gemv_dot launch over the 7 Qwen3-0.6B q4 decode projections at M=1 "
                  "(block 32, f16 scales, packed zero points)",
          "fetch_scale": fs, "write_scale": ws,
          "copy_calibration": {"bytes": COPY_BYTES, "fetch_kib": fetch_copy, "write_kib": write_copy},
@@ -805,7 +806,7 @@ def main():
         extra["int8"] = int8_ops(ctx, 20)
     head = dec[1]
     roofline = {
-        "bound": "hbm", "kernel": "k_gemv_dec<4,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
+        "bound": "hbm", "kernel": "k_gemv_dot<4,zp>", "achieved": head["bytes_per_launch"] / (head["us_per_launch"] * 1e-6) / 1e9,
         "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "traffic": traffic_per_launch(),
     }

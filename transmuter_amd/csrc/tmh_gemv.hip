@@ -105,16 +105,29 @@ void launch_bits(const DecArgs& d, int64_t M, int num_cus, hipStream_t s) {
   const int64_t resident = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * 24;
   const bool resident_grid = static_cast<int64_t>(d.ntiles) * std::min<int64_t>(nch, 16) <= resident;
   if constexpr (BITS != 2 && !SPLIT) {
-    // One row of A over a streaming grid: the dot-product kernel, two chunks per wavefront loaded
-    // together, two tiles per workgroup (151936 x 1024 q4: 15.7-16.2 us against 15.9 with four
-    // tiles and 17.0 for the MFMA kernel). Where the whole grid is resident the launch is latency-
-    // bound and the MFMA kernel is as fast (Qwen3-0.6B projections: 2.71 against 2.75 us).
+    // One row of A: the dot-product kernel. Over a streaming grid two chunks per wavefront load
+    // together and two tiles share a workgroup (151936 x 1024 q4: 15.7-16.2 us against 15.9 with
+    // four tiles and 17.0 for the MFMA kernel); where the whole grid is resident, one chunk per
+    // wavefront and one tile per workgroup, as the MFMA kernel's one-shot shape (Qwen3-0.6B
+    // projections: 2.64 against 2.67 us per launch, merged 3.04 against 3.06; the streaming
+    // shape there: 2.97).
     if (M == 1 && !resident_grid && dot_for_one_row()) {
       switch (std::min(8, round_waves((nch + 1) / 2))) {
         case 1: go_dot<BITS, HAS_ZP, 1, 2, 2>(d, s); break;
         case 2: go_dot<BITS, HAS_ZP, 2, 2, 2>(d, s); break;
         case 4: go_dot<BITS, HAS_ZP, 4, 2, 2>(d, s); break;
         default: go_dot<BITS, HAS_ZP, 8, 2, 2>(d, s);
+      }
+      return;
+    }
+    if (M == 1 && dot_for_one_row()) {
+      switch (round_waves(nch)) {
+        case 1: go_dot<BITS, HAS_ZP, 1, 1, 1>(d, s); break;
+        case 2: go_dot<BITS, HAS_ZP, 2, 1, 1>(d, s); break;
+        case 4: go_dot<BITS, HAS_ZP, 4, 1, 1>(d, s); break;
+        case 8: go_dot<BITS, HAS_ZP, 8, 1, 1>(d, s); break;
+        case 12: go_dot<BITS, HAS_ZP, 12, 1, 1>(d, s); break;
+        default: go_dot<BITS, HAS_ZP, 16, 1, 1>(d, s);
       }
       return;
     }
