@@ -1,5 +1,6 @@
-// Launch plan of the decode GEMV (k_gemv_dec, tmh_gemv.h): MatMulNBits with M <= 16 rows of f16
-// A, f16 weights, f16 Y, no bias (lib/transmuter/ops/quantized.ex:30-46 after move/2).
+// Launch plan of the decode GEMVs (k_gemv_dot for one row of A, k_gemv_dec, tmh_gemv.h):
+// MatMulNBits with M <= 16 rows of f16 A, f16 weights, f16 Y, no bias
+// (lib/transmuter/ops/quantized.ex:30-46 after move/2).
 //
 // This file is compiled with the kernels' leading arguments preloaded into SGPRs
 // (-mllvm -amdgpu-kernarg-preload-count): at the Qwen3-0.6B projection shapes that takes a
@@ -9,9 +10,13 @@
 //  - one-shot (the whole grid resident at once: the Qwen3-0.6B projections): one chunk per
 //    wavefront and round (U = 1), as many wavefronts as chunks (NW = nch, up to 16), one tile
 //    per workgroup. Latency-bound: more chunks per wavefront or more tiles per workgroup were
-//    0.07-0.4 us slower per launch. A is staged through LDS for M > 4. Ablations at M = 1 (2.66
-//    us per launch): without the final store 2.40, without the cross-wavefront sum 2.47, without
-//    the unpack and MFMAs 2.41; an empty kernel costs 1.57 and a plain read of the weights 1.82.
+//    0.07-0.4 us slower per launch. A is staged through LDS for M > 4. Ablations of the MFMA
+//    kernel at M = 1 (2.66 us per launch): without the final store 2.40, without the
+//    cross-wavefront sum 2.47, without the unpack and MFMAs 2.41; an empty kernel costs 1.57 and
+//    a plain read of the weights 1.82. One row of A goes to k_gemv_dot in the same shape (2.64).
+//  - the same grids over 1.1 GB of weight copies (twelve lm_head copies) read HBM at 5.5-5.8
+//    TB/s in a plain read; k_gemv_dot at M = 1 takes 17.3-18.7 us there (5.0-5.2 TB/s), this
+//    kernel at M = 8 19.7-20.4 us. The figures below are over three copies.
 //  - streaming (lm_head-sized N): U = 2 chunks per wavefront loaded together, NW = nch / 2
 //    wavefronts, four tiles per workgroup, so every A fragment serves four tiles (two tiles for
 //    one row of A, through k_gemv_dot). On 151936 x 1024 with random weights rotating over three
