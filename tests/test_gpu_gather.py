@@ -3,7 +3,8 @@
 stores; u8 and s8 data; no, packed (u8 / s8) and float zero points; f32, f16 and bf16 scales;
 negative ids (counted from the end); s64 and s32 ids; and the multi-slice kernel of rows of whole
 256-byte slices (4- and 8-bit data, no or packed zero points, slice counts that leave the last
-wavefront partly empty). Seeds and shapes are printed before each case."""
+wavefront partly empty), with 32 seeded random draws over all of these. Seeds and shapes are
+printed before each case."""
 
 import zlib
 
@@ -50,9 +51,13 @@ def _scales(rng, shape, dtype):
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "b{}_r{}_B{}_blk{}_{}_{}_{}".format(*c[:7]) +
                          ("_ids32" if len(c) > 8 else ""))
 def test_gather_matches_oracle(ctx, case):
+    print(f"gather {case}", flush=True)
+    _check_gather(ctx, case)
+
+
+def _check_gather(ctx, case):
     bits, rows, row_bytes, blocks, dtype, zp, sdt, ids_shape = case[:8]
     ids_dtype = case[8] if len(case) > 8 else np.int64
-    print(f"gather {case}", flush=True)
     rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
     data = rng.integers(0, 256, (rows, row_bytes), dtype=np.uint8)
     if dtype == "s8":
@@ -121,3 +126,34 @@ def test_gather_f16_extreme_scales(ctx, bits):
     bits16 = ref.view(np.uint16)
     assert np.isinf(ref.astype(np.float32)).any() and (((bits16 & 0x7C00) == 0) & ((bits16 & 0x3FF) != 0)).any()
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+def _draw_gather(seed):
+    """A seeded random gather: 2-, 4- or 8-bit rows, half of them whole 256-byte slices (the
+    multi-slice kernel), power-of-two blocks of at least 16 values, every zero-point kind and
+    scale type, s32 or s64 ids with negatives."""
+    rng = np.random.default_rng(7000 + seed)
+    bits = int(rng.choice([2, 4, 4, 8, 8]))
+    per = 8 // bits
+    if rng.random() < 0.5:
+        row_bytes = 256 * int(rng.integers(1, 9))
+    else:
+        row_bytes = int(rng.integers(1, 200)) * (4 if rng.random() < 0.7 else 1)
+    d = row_bytes * per
+    sizes = [b for b in (16, 32, 64, 128, 256) if d % b == 0]
+    bs = int(rng.choice(sizes)) if sizes else d
+    blocks = d // bs
+    dtype = str(rng.choice(["u8", "s8"]))
+    zp = rng.choice([None, "u8", "s8", "float"])
+    sdt = str(rng.choice(["f16", "f16", "f32", "bf16"]))
+    rows = int(rng.integers(1, 3000))
+    shape = tuple(int(x) for x in rng.integers(1, 40, size=int(rng.integers(1, 3))))
+    ids_dtype = np.int32 if rng.random() < 0.4 else np.int64
+    return (bits, rows, row_bytes, blocks, dtype, None if zp is None else str(zp), sdt, shape, ids_dtype)
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_gather(ctx, seed):
+    case = _draw_gather(seed)
+    print(f"random gather seed={seed} {case}", flush=True)
+    _check_gather(ctx, case)
