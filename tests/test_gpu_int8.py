@@ -152,10 +152,34 @@ PREPARED_CASES = [
 
 @pytest.mark.parametrize("case", PREPARED_CASES, ids=lambda c: "b{}_M{}_K{}_N{}_{}{}_{}_{}".format(*c))
 def test_matmul_integer_prepared_matches_oracle(ctx, case):
+    print(f"matmul_integer prepared {case}", flush=True)
+    _check_prepared(ctx, case)
+
+
+def _draw_prepared(seed):
+    """A seeded random MatMulInteger over a prepared B: K a multiple of 16 (what preparation
+    takes), M and N ragged against the 128-row tiles, batches, every signedness and zero-point
+    layout."""
+    rng = np.random.default_rng(9000 + seed)
+    batch = int(rng.choice([1, 1, 1, 2, 3]))
+    m = int(rng.integers(1, 400))
+    k = 16 * int(rng.integers(1, 100))
+    n = int(rng.integers(1, 400))
+    return (batch, m, k, n, str(rng.choice(["u8", "s8"])), str(rng.choice(["u8", "s8"])),
+            rng.choice([None, "scalar", "row"]), rng.choice([None, "scalar", "col"]))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_matmul_integer_prepared(ctx, seed):
+    case = _draw_prepared(seed)
+    print(f"random matmul_integer prepared seed={seed} {case}", flush=True)
+    _check_prepared(ctx, case)
+
+
+def _check_prepared(ctx, case):
     from transmuter_amd.packed import Int8Weight
 
     batch, m, k, n, adt, bdt, az, bz = case
-    print(f"matmul_integer prepared {case}", flush=True)
     rng = np.random.default_rng(zlib.crc32(repr(case).encode()) + 7)
     b = _ints(rng, (k, n), bdt)
     b_zero = None if bz is None else _ints(rng, (1,) if bz == "scalar" else (n,), bdt)
