@@ -69,8 +69,41 @@ def _weights(rng, e, n, k, bits, bs, zp, dtype):
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "{}_E{}_k{}_T{}_H{}_N{}_{}{}".format(*c[:8]))
 def test_qmoe_matches_oracle(ctx, case):
-    dtype, e, k, t, h, n1, act, fusion, fc3, bits, bs, zp, bias, limit = case
     print(f"qmoe {case}", flush=True)
+    _check_qmoe(ctx, case)
+
+
+def _draw_qmoe(seed):
+    """A seeded random QMoE layer: f32 or f16, 1-64 experts, top-1..8, up to 80 tokens (experts
+    with no rows among them), 2/4/8-bit weights, per-row or block-wise (16-128) parameters, with
+    and without zero points and biases, every activation and swiglu layout."""
+    rng = np.random.default_rng(5000 + seed)
+    dtype = str(rng.choice(["f32", "f16"]))
+    e = int(rng.integers(1, 65))
+    k = int(rng.integers(1, min(8, e) + 1))
+    t = int(rng.integers(1, 81))
+    h = 16 * int(rng.integers(1, 17))
+    act = str(rng.choice(["relu", "gelu", "silu", "identity", "swiglu", "swiglu"]))
+    fusion, fc3, limit = 0, False, 0.0
+    if act == "swiglu":
+        fusion, fc3 = [(0, True), (1, False), (2, False)][int(rng.integers(0, 3))]
+        limit = float(rng.choice([0.0, 7.0]))
+    n1 = (32 if act == "swiglu" and not fc3 else 16) * int(rng.integers(1, 9))
+    bits = int(rng.choice([2, 4, 4, 8]))
+    bs = int(rng.choice([0, 16, 32, 64, 128]))
+    return (dtype, e, k, t, h, n1, act, fusion, fc3, bits, bs, bool(rng.random() < 0.5), bool(rng.random() < 0.3),
+            limit)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_qmoe(ctx, seed):
+    case = _draw_qmoe(seed)
+    print(f"random qmoe seed={seed} {case}", flush=True)
+    _check_qmoe(ctx, case)
+
+
+def _check_qmoe(ctx, case):
+    dtype, e, k, t, h, n1, act, fusion, fc3, bits, bs, zp, bias, limit = case
     rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
     npdt = np.float16 if dtype == "f16" else np.float32
     inter = n1 if (act != "swiglu" or fc3) else n1 // 2
