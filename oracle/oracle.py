@@ -41,12 +41,13 @@ F32, F16, BF16 = "f32", "f16", "bf16"
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
-    """Rounds f32 values to bf16 (nearest even), returned as uint16 bit patterns."""
-    x = np.ascontiguousarray(x, dtype=np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    nan = np.isnan(x)
+    """Rounds f32 values to bf16 (nearest even), returned as uint16 bit patterns of x's shape
+    (a 0-d input stays 0-d)."""
+    x = np.asarray(x, dtype=np.float32)
+    flat = np.ascontiguousarray(x.reshape(-1))
+    u = flat.view(np.uint32).astype(np.uint64)
     rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-    return np.where(nan, np.uint16(0x7FC0), rounded).astype(np.uint16)
+    return np.where(np.isnan(flat), np.uint16(0x7FC0), rounded).astype(np.uint16).reshape(x.shape)
 
 
 def bf16_to_f32(bits: np.ndarray) -> np.ndarray:

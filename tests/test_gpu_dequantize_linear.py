@@ -2,8 +2,8 @@
 parameter layout of expand_quant_param/3 (one value, one per axis entry, blocks along the axis),
 every integer value type and float values, f32/f16/bf16 scales, with and without zero points,
 shapes whose inner extent is not a multiple of the kernel's four elements per thread, 1-byte
-values with per-tensor or last-axis parameters (the vectorized kernel), and the 2048 x 2048 u8
-tensor of the int8 benchmark."""
+values with per-tensor or last-axis parameters (the vectorized kernel), the 2048 x 2048 u8
+tensor of the int8 benchmark, and 32 seeded random draws over all of these."""
 
 import zlib
 
@@ -61,8 +61,34 @@ def _scales(rng, shape, dtype):
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "{}_{}_{}{}_{}".format("x".join(map(str, c[0])) or "scalar",
                                                                               c[3], c[4], "_zp" if c[6] else "", c[5]))
 def test_dequantize_linear_matches_oracle(ctx, case):
-    shape, axis, bs, layout, xdt, sdt, with_zero = case
     print(f"dequantize_linear {case}", flush=True)
+    _check(ctx, case)
+
+
+def _draw(seed):
+    """A seeded random DequantizeLinear: rank 0-3, every parameter layout, integer and float
+    values, every scale type, with and without zero points."""
+    rng = np.random.default_rng(6000 + seed)
+    rank = int(rng.integers(0, 4))
+    shape = tuple(int(x) for x in rng.integers(1, 300 if rank < 3 else 40, size=rank))
+    layout = str(rng.choice(["tensor", "axis", "blocked"])) if rank else "tensor"
+    axis = int(rng.integers(0, rank)) if rank else 0
+    bs = int(rng.integers(1, 70)) if layout == "blocked" else 0
+    xdt = str(rng.choice(["u8", "u8", "s8", "s8", "u16", "s16", "s32", "f32", "f16"]))
+    sdt = "f16" if xdt == "f16" else ("f32" if xdt == "f32" else str(rng.choice(["f32", "f16", "bf16"])))
+    with_zero = bool(rng.random() < 0.6)
+    return (shape, axis, bs, layout, xdt, sdt, with_zero)
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_dequantize_linear(ctx, seed):
+    case = _draw(seed)
+    print(f"random dequantize_linear seed={seed} {case}", flush=True)
+    _check(ctx, case)
+
+
+def _check(ctx, case):
+    shape, axis, bs, layout, xdt, sdt, with_zero = case
     rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
     x = _values(rng, shape, xdt)
     if layout == "tensor":

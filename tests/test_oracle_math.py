@@ -151,6 +151,16 @@ def test_bf16_rounding_is_nearest_even():
     assert np.isinf(o.bf16_to_f32(bits)[4])
 
 
+def test_bf16_rounding_keeps_the_shape():
+    """A 0-d value stays 0-d (a scalar DequantizeLinear scale), and the dequantized scalar with it;
+    NaN keeps its quiet pattern whatever the shape."""
+    assert o.bf16_round(np.float32(0.5)).shape == ()
+    assert o.bf16_round(np.zeros((3, 0, 2), np.float32)).shape == (3, 0, 2)
+    assert o.bf16_round(np.full((2, 3), np.nan, np.float32)).tolist() == [[0x7FC0] * 3] * 2
+    y = o.dequantize_linear(np.array(7, np.uint16), o.bf16_round(np.float32(0.5)), axis=0)
+    assert y.shape == () and o.bf16_to_f32(y) == 3.5
+
+
 # ---------------------------------------------------------------- other operators
 
 
