@@ -38,8 +38,25 @@ def _ints(rng, shape, dtype):
 
 @pytest.mark.parametrize("case", MI_CASES, ids=lambda c: "b{}_M{}_K{}_N{}_{}{}".format(*c[:6]))
 def test_matmul_integer_matches_oracle(ctx, case):
-    batch, m, k, n, adt, bdt, az, bz, bb = case
     print(f"matmul_integer {case}", flush=True)
+    _check_plain(ctx, case)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_matmul_integer(ctx, seed):
+    """Seeded random MatMulInteger over B as given: any K, ragged M and N, batched A with a shared
+    or batched B, every signedness and zero-point layout."""
+    rng = np.random.default_rng(9500 + seed)
+    batch = int(rng.choice([1, 1, 1, 2, 3]))
+    case = (batch, int(rng.integers(1, 400)), int(rng.integers(1, 1600)), int(rng.integers(1, 400)),
+            str(rng.choice(["u8", "s8"])), str(rng.choice(["u8", "s8"])), rng.choice([None, "scalar", "row"]),
+            rng.choice([None, "scalar", "col"]), bool(batch > 1 and rng.random() < 0.5))
+    print(f"random matmul_integer seed={seed} {case}", flush=True)
+    _check_plain(ctx, case)
+
+
+def _check_plain(ctx, case):
+    batch, m, k, n, adt, bdt, az, bz, bb = case
     rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
     a = _ints(rng, (batch, m, k) if batch > 1 else (m, k), adt)
     b = _ints(rng, (batch, k, n) if bb else (k, n), bdt)
@@ -95,7 +112,26 @@ def test_dynamic_quantize_linear_matches_oracle(ctx, case):
     kind, n = case
     print(f"dynamic_quantize_linear {case}", flush=True)
     rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
-    x = _dql_input(rng, kind, n)
+    _check_dql(ctx, _dql_input(rng, kind, n))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_dynamic_quantize_linear(ctx, seed):
+    """Seeded random DynamicQuantizeLinear: rank 1-3 shapes up to about 3 M values, each input
+    kind, scaled over magnitudes from 2^-20 to 2^20 and shifted off zero."""
+    rng = np.random.default_rng(9700 + seed)
+    kind = str(rng.choice(["normal", "positive", "negative", "constant", "zeros", "ties"]))
+    rank = int(rng.integers(1, 4))
+    shape = tuple(int(x) for x in rng.integers(1, [3_000_000, 2000, 150][rank - 1], size=rank))
+    x = _dql_input(rng, kind, int(np.prod(shape))).reshape(shape)
+    if kind != "ties":
+        x = (x * np.float32(2.0 ** int(rng.integers(-20, 21))) + np.float32(rng.standard_normal())).astype(np.float32)
+    print(f"random dynamic_quantize_linear seed={seed} {kind} {shape}", flush=True)
+    _check_dql(ctx, x)
+
+
+def _check_dql(ctx, x):
+    n = x.size
     node = NodeProto(op_type="DynamicQuantizeLinear", input=["x"], output=["y", "s", "z"])
     y, s, z = (t.numpy() for t in quantized.apply(node, [ctx.put(x)]))
     if n == 0:  # no range: the scale of a constant (1) and zero point 0
