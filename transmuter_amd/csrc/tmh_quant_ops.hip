@@ -764,6 +764,7 @@ __global__ __launch_bounds__(512) void k_matmul_integer_mfma(
         out[e] = static_cast<int32_t>(static_cast<uint32_t>(acc[mt][nt][e]) + cb * rsm + ca * sCs[0][nl + e] + kk * ca * cb);
       }
       if (y_vec) {
+        // Non-temporal: the s32 output (four bytes per product) is not read again here (2048^3: 29.3 -> 27.1 us under the tracer).
         __builtin_nontemporal_store(out, reinterpret_cast<int4_t*>(yrow + n));
       } else {
 #pragma unroll
