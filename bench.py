@@ -544,6 +544,77 @@ def int8_ops(ctx, reps, per_graph=8, m=2048, k=2048, n=2048):
     return out
 
 
+def _torch_graph_us(torch, fn, reps, per_graph):
+    """Microseconds per call of fn, from `reps` replays of a torch CUDA graph of `per_graph` calls."""
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            fn()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+
+
+def vendor_gemms(reps, per_graph=10):
+    """The vendor library's dense GEMMs at the shapes the bench times, for comparison (torch on
+    ROCm calls hipBLASLt), in torch CUDA graphs of `per_graph` calls:
+    - int8 2048 x 2048 x 2048 (torch._int_mm, s8 x s8 -> s32, no zero points) with B as [K, N]
+      rows and with B k-contiguous (the layout a prepared MatMulInteger weight has), checked
+      exactly against an f64 product;
+    - f16 x f16 -> f16 at the SmolLM3-3B prefill projections (M = 256 and 2048), weights [N, K]
+      as nn.Linear holds them, dense: the f16 GEMM with no dequantization at all, checked against
+      an f32 product.
+    Opt-in (`--vendor`): it imports torch, whose first import on a fresh machine takes minutes."""
+    import torch
+
+    gen = torch.Generator().manual_seed(7)
+    out = {"int8": {}, "f16_prefill": {}}
+    n = 2048
+    a = torch.randint(-128, 128, (n, n), dtype=torch.int8, generator=gen).cuda()
+    b = torch.randint(-128, 128, (n, n), dtype=torch.int8, generator=gen).cuda()
+    ref = a.double() @ b.double()
+    for name, bb in (("b_rows", b), ("b_k_contiguous", b.t().contiguous().t())):
+        y = torch._int_mm(a, bb)
+        torch.cuda.synchronize()
+        if not torch.equal(y.double(), ref):
+            raise RuntimeError(f"torch._int_mm ({name}) differs from the exact product")
+        us = _torch_graph_us(torch, lambda bb=bb: torch._int_mm(a, bb), reps, per_graph)
+        out["int8"][name] = {"us": us, "tops": 2 * n ** 3 / (us * 1e-6) / 1e12}
+    log(f"torch._int_mm {n}^3: B rows {out['int8']['b_rows']['us']:.1f} us, "
+        f"B k-contiguous {out['int8']['b_k_contiguous']['us']:.1f} us")
+    for m in (256, 2048):
+        per, flops, total_us = [], 0, 0.0
+        for pname, k, nn in SMOLLM3_3B:
+            x = torch.randn((m, k), generator=gen).half().cuda()
+            w = (torch.randn((nn, k), generator=gen) * 0.02).half().cuda()
+            y = torch.nn.functional.linear(x, w)
+            ref = x.float() @ w.float().t()
+            err = (y.float() - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
+            if not err < 1e-2:
+                raise RuntimeError(f"f16 linear {pname} at M={m} is off by {err:.3g} of max|ref|")
+            us = _torch_graph_us(torch, lambda x=x, w=w: torch.nn.functional.linear(x, w), reps, per_graph)
+            per.append({"projection": pname, "us": us, "tflops": 2 * m * k * nn / (us * 1e-6) / 1e12})
+            flops += 2 * m * k * nn
+            total_us += us
+            del x, w, y, ref
+        out["f16_prefill"][str(m)] = {"per_projection": per, "tflops": flops / (total_us * 1e-6) / 1e12}
+        log(f"f16 linear (dense) M={m}: " + ", ".join(f"{p['us']:.1f}" for p in per)
+            + f" us, {out['f16_prefill'][str(m)]['tflops']:.0f} TFLOP/s")
+    return out
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 
@@ -761,6 +832,8 @@ def main():
     p.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="write the decode GEMV's HBM bytes per launch from two --pmc runs of --profile decode")
     p.add_argument("--profile-m", type=int, default=1, help="rows of A for --profile decode")
+    p.add_argument("--vendor", action="store_true",
+                   help="time the vendor library's dense int8 and f16 GEMMs (torch) at the bench's shapes and exit")
     p.add_argument("--summarize", nargs="*", metavar="PATH",
                    help="print a markdown summary of rocprofv3 output: a kernel_stats.csv, then --pmc directories")
     args = p.parse_args()
@@ -778,6 +851,12 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path runs on one GPU, "
               "and its multi-GPU sharding is a design, not a measured run)", file=sys.stderr)
         sys.exit(2)
+
+    if args.vendor:
+        # In a process of its own: torch brings its own HIP runtime, which finds no GPU once this
+        # library's runtime holds the device (run `--sections int8,prefill` beside it).
+        print(json.dumps({"vendor": vendor_gemms(20)}))
+        return
 
     from transmuter_amd import Context
 
