@@ -29,6 +29,13 @@ MI_CASES = [
     (2, 129, 1040, 400, "s8", "u8", "scalar", "col", True),
     (1, 513, 2048, 384, "u8", "s8", "scalar", None, False),
     (1, 256, 512, 1024, "u8", "u8", "scalar", "col", False),  # 16 tiles: the XCD tile order
+    # 256 rows and more over a shared B with K a multiple of 16: one k-step of 16, N off 16 and
+    # off 4 (scalar output stores), a batch of A over one B
+    (1, 256, 16, 16, "s8", "u8", "row", "col", False),
+    (2, 200, 4096, 257, "u8", "u8", "row", "col", False),
+    (1, 384, 1040, 130, "s8", "s8", "scalar", "scalar", False),
+    (3, 100, 272, 64, "u8", "s8", None, "col", False),
+    (1, 512, 1024, 512, "u8", "u8", "scalar", "col", False),
 ]
 
 
@@ -53,6 +60,35 @@ def test_random_matmul_integer(ctx, seed):
             rng.choice([None, "scalar", "col"]), bool(batch > 1 and rng.random() < 0.5))
     print(f"random matmul_integer seed={seed} {case}", flush=True)
     _check_plain(ctx, case)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_matmul_integer_many_rows(ctx, seed):
+    """Seeded random MatMulInteger over B as given with 256 to 700 rows over a shared B and K a
+    multiple of 16 (the 16-byte load path over several row tiles): ragged M and N, every
+    signedness and zero-point layout."""
+    rng = np.random.default_rng(9700 + seed)
+    batch = int(rng.choice([1, 1, 2]))
+    case = (batch, int(rng.integers(256 // batch, 700 // batch)), 16 * int(rng.integers(1, 100)),
+            int(rng.integers(1, 400)), str(rng.choice(["u8", "s8"])), str(rng.choice(["u8", "s8"])),
+            rng.choice([None, "scalar", "row"]), rng.choice([None, "scalar", "col"]), False)
+    print(f"random matmul_integer (many rows) seed={seed} {case}", flush=True)
+    _check_plain(ctx, case)
+
+
+def test_matmul_integer_extremes_over_row_tiles(ctx):
+    """Every product at its largest magnitude over two row tiles (u8 255 x 255 and s8 -128 x -128
+    over K = 4096: 266 M, past 2^24), with the zero points at their ends."""
+    k, m, n = 4096, 256, 48
+    for adt, bdt, av, bv in (("u8", "u8", 255, 255), ("s8", "s8", -128, -128), ("u8", "s8", 255, -128)):
+        a = np.full((m, k), av, np.uint8 if adt == "u8" else np.int8)
+        b = np.full((k, n), bv, np.uint8 if bdt == "u8" else np.int8)
+        az = np.array([0 if adt == "u8" else 127], a.dtype)
+        bz = np.full(n, 0 if bdt == "u8" else 127, b.dtype)
+        node = NodeProto(op_type="MatMulInteger", input=["a", "b", "az", "bz"], output=["y"])
+        got = quantized.apply(node, [ctx.put(a), ctx.put(b), ctx.put(az), ctx.put(bz)])[0].numpy()
+        want = k * (int(av) - int(az[0])) * (int(bv) - int(bz[0]))
+        assert np.all(got == want), (adt, bdt)
 
 
 def _check_plain(ctx, case):

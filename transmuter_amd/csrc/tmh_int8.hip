@@ -28,22 +28,71 @@ namespace {
 constexpr int kQT = 128;   // output rows and columns per workgroup
 constexpr int kQPad = 256;  // a prepared B's rows of k are padded to whole GEMM steps (of 128 or 256 bytes)
 
-// B [K][N] (u8 or s8) -> Bt [N][Kp] as s8 (u8 flipped by ^ 0x80 = b - 128), zero past K. One
-// thread per 16 output bytes; the reads of a thread are a column of B, shared through L2 by the
-// threads of neighbouring columns (a load-time pass).
-__global__ __launch_bounds__(256) void k_i8_transpose(const uint8_t* __restrict__ b, uint32_t flip, int64_t K, int64_t N,
-                                                      int64_t Kp, uint4_t* __restrict__ bt) {
-  const int64_t units = N * (Kp / 16);
-  const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (u >= units) return;
-  const int64_t n = u % N, k0 = (u / N) * 16;
-  uint32_t w[4] = {0u, 0u, 0u, 0u};
+// B [K][N] (u8 or s8) -> Bt [N][Kp] as s8 (u8 flipped by ^ 0x80 = b - 128), zero past K. A
+// workgroup moves one 128 (k) x 128 (n) tile: 16-byte loads along n (a wavefront reads eight whole
+// 128-byte rows) into LDS rows of 132 bytes (the read-back below then meets at most two-way bank
+// conflicts), the flip applied and rows past K zeroed on the way in; then each thread reads the 4
+// columns x 16 rows it owns as sixteen 4-byte words, transposes them in 4 x 4 byte blocks
+// (v_perm_b32) and stores four 16-byte pieces along k, so the eight threads of one output row
+// write its 128 bytes whole.
+constexpr int kTT = 128;    // tile edge, bytes of k and of n
+constexpr int kTRow = 132;  // LDS bytes per tile row
+
+__global__ __launch_bounds__(256) void k_i8_transpose(const uint8_t* __restrict__ b, uint32_t flip, uint32_t K, uint32_t N,
+                                                      uint32_t Kp, bool vec, uint8_t* __restrict__ bt) {
+  __shared__ __align__(16) uint32_t t[kTT * kTRow / 4];
+  const uint32_t n0 = blockIdx.x * kTT, k0 = blockIdx.y * kTT;
+  const int tid = threadIdx.x;
+  const uint32_t flip4 = flip * 0x01010101u;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int64_t k = k0 + e;
-    if (k < K) w[e >> 2] |= static_cast<uint32_t>(b[k * N + n] ^ flip) << (8 * (e & 3));
+  for (int i = 0; i < 4; ++i) {
+    const int p = tid + 256 * i;
+    const int row = p >> 3, piece = p & 7;
+    const uint32_t k = k0 + row, n = n0 + 16 * piece;
+    uint4_t v = uint4_t{0u, 0u, 0u, 0u};
+    if (k < K) {
+      if (vec) {
+        if (n < N) v = *reinterpret_cast<const uint4_t*>(b + static_cast<size_t>(k) * N + n);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (n + e < N) v[e >> 2] |= static_cast<uint32_t>(b[static_cast<size_t>(k) * N + n + e]) << (8 * (e & 3));
+      }
+      v ^= flip4;  // columns past N are flipped too; no thread stores them
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) t[row * (kTRow / 4) + 4 * piece + w] = v[w];
   }
-  bt[n * (Kp / 16) + k0 / 16] = uint4_t{w[0], w[1], w[2], w[3]};
+  __syncthreads();
+  const int kp = tid & 7, ng = tid >> 3;  // k bytes 16 kp .. +15, columns 4 ng .. +3
+  uint32_t d[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) d[i] = t[(16 * kp + i) * (kTRow / 4) + ng];
+  uint4_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    // Rows 4q .. 4q+3 of the thread's 16: output word q of column j holds byte j of each.
+    const uint32_t lo01 = __builtin_amdgcn_perm(d[4 * q + 1], d[4 * q], 0x05010400u);
+    const uint32_t hi01 = __builtin_amdgcn_perm(d[4 * q + 1], d[4 * q], 0x07030602u);
+    const uint32_t lo23 = __builtin_amdgcn_perm(d[4 * q + 3], d[4 * q + 2], 0x05010400u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(d[4 * q + 3], d[4 * q + 2], 0x07030602u);
+    o[0][q] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+    o[1][q] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+    o[2][q] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+    o[3][q] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t n = n0 + 4 * ng + j;
+    if (n < N) *reinterpret_cast<uint4_t*>(bt + static_cast<size_t>(n) * Kp + k0 + 16 * kp) = o[j];
+  }
+}
+
+void launch_i8_transpose(const uint8_t* b, bool b_signed, int64_t K, int64_t N, int64_t Kp, uint8_t* bt, hipStream_t s) {
+  const bool vec = N % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0;
+  const dim3 grid(static_cast<unsigned>((N + kTT - 1) / kTT), static_cast<unsigned>(Kp / kTT));
+  k_i8_transpose<<<grid, 256, 0, s>>>(b, b_signed ? 0u : 0x80u, static_cast<uint32_t>(K), static_cast<uint32_t>(N),
+                                      static_cast<uint32_t>(Kp), vec, bt);
 }
 
 // cs_n = sum_k sb (over Bt's row n: zeros past K add nothing) and cb_n = ob - bz_n; one
@@ -212,6 +261,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmi_bt(const uint8_t* __restrict__ 
       if (g == 0) rs_part[kh * kQT + 64 * wm + 16 * mt + r] = v;
     }
   }
+  if constexpr (KS == 1) __syncthreads();  // the row sums, read across quadrants below
 #pragma unroll
   for (int half = KS / 2; half >= 1; half /= 2) {
     if (kh >= half && kh < 2 * half) {
@@ -319,9 +369,7 @@ int tmh_int8_weight_prepare(tmh_ctx* ctx, const void* d_b, int b_dtype, const vo
   }
   w->device_bytes = static_cast<size_t>(N * Kp) + 2 * terms;
   hipStream_t s = pick_stream(ctx, stream);
-  const int64_t units = N * (Kp / 16);
-  k_i8_transpose<<<static_cast<unsigned>((units + 255) / 256), 256, 0, s>>>(
-      static_cast<const uint8_t*>(d_b), b_dtype == TMH_S8 ? 0u : 0x80u, K, N, Kp, reinterpret_cast<uint4_t*>(w->d_bt));
+  launch_i8_transpose(static_cast<const uint8_t*>(d_b), b_dtype == TMH_S8, K, N, Kp, reinterpret_cast<uint8_t*>(w->d_bt), s);
   st = check_launch(ctx, "k_i8_transpose");
   if (st == TMH_OK) {
     k_i8_colsum<<<static_cast<unsigned>((N + 3) / 4), 256, 0, s>>>(
