@@ -239,9 +239,9 @@ def test_y_type_must_follow_the_reference(ctx):
         ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, a_d.ptr, 10, 1, 64, None, 0, y_d.ptr, F32, 16, None))
 
 
-# Every prefill tile shape (BM x 64*WN: 256x128, 256x256, 128x128, 128x256, and 128x128 with each
-# k-block's steps split between two wavefronts), with and without K splits, forced through
-# TMH_GEMM_PLAN, over ragged M, N and K (a partial last k-block) and a bias.
+# Every prefill tile shape (BM x 64*WN: 256x128, 256x256, 128x128, 128x256, 64x128, 64x256, and
+# 128x128 and 64x128 with each k-block's steps split between two wavefronts), with and without K
+# splits, forced through TMH_GEMM_PLAN, over ragged M, N and K (a partial last k-block) and a bias.
 PLAN_CASES = [
     # bits, block, zp, K, N, M list, bias
     (4, 32, "packed", 1000, 1000, [200, 300], "f16"),
@@ -251,7 +251,7 @@ PLAN_CASES = [
 ]
 # (bm, wn, splits[, 2]): a fourth field 2 splits each k-block's steps between two wavefronts
 PLANS = [(256, 2, 1), (256, 4, 1), (128, 2, 1), (128, 4, 1), (256, 2, 3), (128, 2, 2), (128, 4, 4), (128, 2, 1, 2),
-         (128, 2, 3, 2)]
+         (128, 2, 3, 2), (64, 2, 1), (64, 4, 1), (64, 2, 3), (64, 4, 2), (64, 2, 1, 2), (64, 2, 2, 2)]
 
 
 @pytest.mark.parametrize("plan", PLANS, ids=lambda p: "bm{}_wn{}_s{}".format(*p) + ("_ks2" if len(p) > 3 else ""))

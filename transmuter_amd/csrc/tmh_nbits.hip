@@ -416,22 +416,22 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
   constexpr int RPI = 64 / PPR;          // rows per wavefront load instruction
   constexpr int NWAVE = 2 * WN * KS;
   constexpr int RW = BM / NWAVE;         // A rows each wavefront brings into LDS
-  // KS == 2 (BM = 128, WN = 2 only): eight wavefronts, two per SIMD; wavefronts w and w + 4 share
+  // KS == 2 (BM = 64 or 128, WN = 2 only): eight wavefronts, two per SIMD; wavefronts w and w + 4 share
   // an output sub-tile and take the first and second half of each k-block's MFMA steps, and the
   // second half's partial sums add to the first's through LDS after the k-loop.
-  static_assert(KS == 1 || (KS == 2 && BM == 128 && WN == 2), "K split inside the workgroup");
+  static_assert(KS == 1 || (KS == 2 && BM <= 128 && WN == 2), "K split inside the workgroup");
   constexpr int LSTEPS = STEPS / KS;     // MFMA steps per k-block of one wavefront
   constexpr int LOADS = RW / RPI;        // load instructions per wavefront per k-block
   constexpr int NJ = SPLIT ? STEPS : 1;  // parameter entries per tile per k-block
-  // Tall (WN == 4, eight wavefronts, two per SIMD; or BM == 128): each wavefront takes all BM
+  // Tall (WN == 4, eight wavefronts, two per SIMD; or BM <= 128): each wavefront takes all BM
   // rows and two weight tiles, so every dequantized fragment feeds BM/16 MFMAs. BM == 256 with
   // WN == 2 (four wavefronts): 128 rows and four tiles per wavefront.
   // Measured alternatives, none faster on the SmolLM3-3B shapes: four wavefronts each taking all
   // 256 rows of four tiles (one per SIMD; half the LDS reads per MFMA) were 4-15% slower; eight-
   // wavefront 128-row tiles held to 128 VGPRs (four per SIMD) spilled and were slower; reading A
   // fragments two or three ahead instead of one changed nothing.
-  static_assert(BM == 128 || BM == 256, "tile height");
-  constexpr bool TALL = WN == 4 || BM == 128;
+  static_assert(BM == 64 || BM == 128 || BM == 256, "tile height");
+  constexpr bool TALL = WN == 4 || BM <= 128;
   constexpr int MTW = TALL ? BM / 16 : 8;
   constexpr int NTW = TALL ? 2 : 4;
   extern __shared__ __align__(16) uint8_t lds[];
@@ -975,7 +975,8 @@ struct GemmShape {
   double rate;  // dense f16 FLOP/s per CU
 };
 constexpr GemmShape kGemmShapes[] = {
-    {256, 2, 1, 2.8e12}, {256, 4, 1, 3.9e12}, {128, 2, 1, 2.4e12}, {128, 4, 1, 3.3e12}, {128, 2, 2, 2.9e12}};
+    {256, 2, 1, 2.8e12}, {256, 4, 1, 3.9e12}, {128, 2, 1, 2.4e12}, {128, 4, 1, 3.3e12}, {128, 2, 2, 2.9e12},
+    {64, 2, 1, 1.6e12},  {64, 4, 1, 2.0e12},  {64, 2, 2, 2.0e12}};
 
 struct GemmPlan {
   int bm, wn, splits, cps, ks = 1;
@@ -1011,8 +1012,8 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
   if (const char* f = getenv("TMH_GEMM_PLAN")) {
     int bm = 0, wn = 0, sp = 0, ks = 1;
     const int got = sscanf(f, "%d,%d,%d,%d", &bm, &wn, &sp, &ks);
-    if ((got == 3 || got == 4) && (bm == 128 || bm == 256) && (wn == 2 || wn == 4) && sp >= 1 && sp <= nchunks &&
-        (ks == 1 || (ks == 2 && bm == 128 && wn == 2))) {
+    if ((got == 3 || got == 4) && (bm == 64 || bm == 128 || bm == 256) && (wn == 2 || wn == 4) && sp >= 1 &&
+        sp <= nchunks && (ks == 1 || (ks == 2 && bm <= 128 && wn == 2))) {
       const int cps = static_cast<int>((nchunks + sp - 1) / sp);
       best = GemmPlan{bm, wn, static_cast<int>((nchunks + cps - 1) / cps), cps, ks};
     }
@@ -1047,7 +1048,14 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
 template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
   const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, cus_of(ctx));
-  if (p.bm == 128 && p.ks == 2) {
+  if (p.bm == 64) {
+    if (p.ks == 2)
+      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 64, 2>(ctx, w, a, s, p.splits, p.cps);
+    else if (p.wn == 4)
+      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 64>(ctx, w, a, s, p.splits, p.cps);
+    else
+      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 64>(ctx, w, a, s, p.splits, p.cps);
+  } else if (p.bm == 128 && p.ks == 2) {
     launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 128, 2>(ctx, w, a, s, p.splits, p.cps);
   } else if (p.bm == 128) {
     if (p.wn == 4)
