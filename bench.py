@@ -711,7 +711,7 @@ COPY_BYTES = 256 << 20
 def profile_run(ctx, kind, steps, m=1):
     """A short, graph-free run for rocprofv3: `decode` runs the projection sweep at M = m over one
     weight copy plus one 256 MiB device copy (the calibration of the memory counters);
-    `prefill` runs the SmolLM3-3B projections at M=2048; `moe` the quantized MoE layer; `vocab`
+    `prefill` runs the SmolLM3-3B projections at M=2048 (or M = m when m > 1); `moe` the quantized MoE layer; `vocab`
     the lm_head MatMulNBits and the GatherBlockQuantized lookup at the 151936 x 1024 shape; `int8`
     DynamicQuantizeLinear, MatMulInteger and DequantizeLinear at 2048 x 2048 x 2048."""
     global USE_GRAPHS
@@ -731,7 +731,7 @@ def profile_run(ctx, kind, steps, m=1):
     elif kind == "int8":
         int8_ops(ctx, steps, per_graph=1)
     else:
-        prefill(ctx, steps, [2048])
+        prefill(ctx, steps, [m if m > 1 else 2048])
 
 
 def summarize(kernel_csv, pmc_dirs):
@@ -831,7 +831,7 @@ def main():
     p.add_argument("--profile", choices=["decode", "prefill", "moe", "vocab", "int8"], help="a short graph-free run for rocprofv3")
     p.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="write the decode GEMV's HBM bytes per launch from two --pmc runs of --profile decode")
-    p.add_argument("--profile-m", type=int, default=1, help="rows of A for --profile decode")
+    p.add_argument("--profile-m", type=int, default=1, help="rows of A for --profile decode (and prefill, when above 1)")
     p.add_argument("--vendor", action="store_true",
                    help="time the vendor library's dense int8 and f16 GEMMs (torch) at the bench's shapes and exit")
     p.add_argument("--summarize", nargs="*", metavar="PATH",
