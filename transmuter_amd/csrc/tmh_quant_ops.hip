@@ -910,11 +910,28 @@ __global__ __launch_bounds__(256) void k_dql_quantize_reduce(const float* __rest
   }
   const float z = static_cast<float>(zq);
   auto q = [&](float f) -> uint32_t { return static_cast<uint32_t>(fminf(fmaxf(rintf(f / sc) + z, 0.f), 255.f)); };
+  // rint(x / sc) without the division, bit for bit: rcp = 1 / sc and q0 = x * rcp are each
+  // rounded once, so q0 lies within |x / sc| 2^-22 of the rounded quotient; where q0 is further
+  // than that from every half-integer (the only points where rint's result changes) both round to
+  // the same integer. Otherwise (or where q0 is not finite) the wavefront takes the division for
+  // its four values, a uniform branch so that the common case skips it (9.6 -> 9.0 us at 2048 x
+  // 2048; computing both and selecting took 10.5).
+  const float rcp = 1.f / sc;
   for (; i < n; i += stride) {
     if (vec && i + 4 <= n) {
       const float4_t w = v;
       if (i + stride + 4 <= n) v = *reinterpret_cast<const float4_t*>(x + i + stride);
-      *reinterpret_cast<uint32_t*>(y + i) = q(w[0]) | (q(w[1]) << 8) | (q(w[2]) << 16) | (q(w[3]) << 24);
+      uint32_t packed = 0u;
+      bool near_half = false;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float q0 = w[e] * rcp;
+        const float frac = q0 - floorf(q0);
+        near_half = near_half || !(fabsf(frac - 0.5f) > fabsf(q0) * 0x1p-21f);
+        packed |= static_cast<uint32_t>(fminf(fmaxf(rintf(q0) + z, 0.f), 255.f)) << (8 * e);
+      }
+      if (__any(near_half)) packed = q(w[0]) | (q(w[1]) << 8) | (q(w[2]) << 16) | (q(w[3]) << 24);
+      *reinterpret_cast<uint32_t*>(y + i) = packed;
     } else {
       for (int e = 0; e < 4 && i + e < n; ++e) y[i + e] = static_cast<uint8_t>(q(x[i + e]));
     }
