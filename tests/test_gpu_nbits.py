@@ -292,6 +292,7 @@ ONE_ROW_CASES = [
     (4, 32, "packed", 1024, 30008, 1024),
     (4, 32, "none", 2000, 16000, 2008),
     (4, 128, "packed", 4096, 12000, 4096),
+    (4, 32, "packed", 1024, 40008, 1024),  # thousands of tiles: four per workgroup, a ragged last one
     (8, 32, "packed", 512, 48, 512),
     (8, 128, "none", 1000, 20, 1000),
     (8, 32, "none", 72, 24, 80),

@@ -115,17 +115,19 @@ void launch_bits(const DecArgs& d, int64_t M, int num_cus, hipStream_t s) {
   const bool resident_grid = static_cast<int64_t>(d.ntiles) * std::min<int64_t>(nch, 16) <= resident;
   if constexpr (BITS != 2 && !SPLIT) {
     // One row of A: the dot-product kernel. Over a streaming grid two chunks per wavefront load
-    // together and two tiles share a workgroup (151936 x 1024 q4: 15.7-16.2 us against 15.9 with
-    // four tiles and 17.0 for the MFMA kernel); where the whole grid is resident, one chunk per
-    // wavefront and one tile per workgroup, as the MFMA kernel's one-shot shape (Qwen3-0.6B
-    // projections: 2.64 against 2.67 us per launch, merged 3.04 against 3.06; the streaming
-    // shape there: 2.97).
+    // together, and four tiles share a workgroup where the grid spans thousands of tiles (151936 x
+    // 1024 q4 over 1.1 GB of rotating copies: 17.5 against 18.2-18.5 us with two tiles; one chunk
+    // per wavefront 18.5-19.3, four 19.0-22.6), two below that; where the whole grid is resident,
+    // one chunk per wavefront and one tile per workgroup, as the MFMA kernel's one-shot shape
+    // (Qwen3-0.6B projections: 2.64 against 2.67 us per launch, merged 3.04 against 3.06; the
+    // streaming shape there: 2.97).
     if (M == 1 && !resident_grid && dot_for_one_row()) {
+      const bool wide = d.ntiles >= 2048;
       switch (std::min(8, round_waves((nch + 1) / 2))) {
-        case 1: go_dot<BITS, HAS_ZP, 1, 2, 2>(d, s); break;
-        case 2: go_dot<BITS, HAS_ZP, 2, 2, 2>(d, s); break;
-        case 4: go_dot<BITS, HAS_ZP, 4, 2, 2>(d, s); break;
-        default: go_dot<BITS, HAS_ZP, 8, 2, 2>(d, s);
+        case 1: wide ? go_dot<BITS, HAS_ZP, 1, 4, 2>(d, s) : go_dot<BITS, HAS_ZP, 1, 2, 2>(d, s); break;
+        case 2: wide ? go_dot<BITS, HAS_ZP, 2, 4, 2>(d, s) : go_dot<BITS, HAS_ZP, 2, 2, 2>(d, s); break;
+        case 4: wide ? go_dot<BITS, HAS_ZP, 4, 4, 2>(d, s) : go_dot<BITS, HAS_ZP, 4, 2, 2>(d, s); break;
+        default: wide ? go_dot<BITS, HAS_ZP, 8, 4, 2>(d, s) : go_dot<BITS, HAS_ZP, 8, 2, 2>(d, s);
       }
       return;
     }
