@@ -119,6 +119,21 @@ class Graph:
 USE_GRAPHS = True
 
 
+def rocprof_domains() -> list[str]:
+    """The rocprofv3 tracing or counter-collection domains switched on in this process's
+    environment (rocprofv3 exports ROCPROF_<DOMAIN>_TRACE=1 and ROCPROF_COUNTER_COLLECTION=1)."""
+    return sorted(k for k, v in os.environ.items()
+                  if k.startswith("ROCPROF_") and (k.endswith("_TRACE") or k == "ROCPROF_COUNTER_COLLECTION")
+                  and v == "1")
+
+
+# Graph replays under rocprofv3 ended twice in a segmentation fault inside hipGraphLaunch, at the
+# same code offset of the runtime, once in a process that never loaded this library: the tracer's
+# own graph-launch path. Runs under the tracer therefore launch every call directly (--profile,
+# --no-graph); a graph run under it is refused.
+GRAPHS_UNDER_TRACER = "graph replays are not run under rocprofv3 (its graph-launch path has crashed)"
+
+
 def matmul_call(ctx, w, a, y, m):
     from transmuter_amd._lib import F16, lib
 
@@ -847,6 +862,10 @@ def main():
         return
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
+    if USE_GRAPHS and not args.profile and not args.vendor and rocprof_domains():
+        print(f"bench.py: {GRAPHS_UNDER_TRACER}; found {', '.join(rocprof_domains())}. Use --profile KIND "
+              "(graph-free launches) or --no-graph under the profiler.", file=sys.stderr)
+        sys.exit(3)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path runs on one GPU, "
               "and its multi-GPU sharding is a design, not a measured run)", file=sys.stderr)

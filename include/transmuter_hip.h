@@ -226,11 +226,14 @@ int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_d
 /*
  * tmh_matmul_nbits for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
- * reference. Same arguments, checks and results (the same kernels and plan, bit for bit), but a
- * prefill GEMM whose plan splits K keeps its f32 partial sums in a fixed 64 MiB scratch area per
- * device (set up by tmh_ctx_create) instead of the context's workspace, and the call neither
- * allocates nor frees. A call whose partial sums exceed 64 MiB fails with TMH_ERR_INVALID (the
- * message gives the size). Every call on one device shares that device's scratch, which keeps
+ * reference. Same arguments and checks, but a prefill GEMM whose plan splits K keeps its f32
+ * partial sums in a fixed 64 MiB scratch area per device (set up by tmh_ctx_create) instead of
+ * the context's workspace, and the call neither allocates nor frees. Where tmh_matmul_nbits's
+ * plan keeps at most 64 MiB of partial sums (every plan up to M * N = 2^22 outputs at 4 splits,
+ * for example), both run the same kernels and plan and give the same bits; beyond that this call
+ * runs the best plan whose partial sums fit (fewer K splits, or none, also when TMH_GEMM_PLAN
+ * forces more), whose sums differ from tmh_matmul_nbits's only in f32 summation order. Every call
+ * on one device shares that device's scratch, which keeps
  * the last call's partial sums: calls on one device that overlap in time (other streams, other
  * contexts, other threads) race and must be serialized by the caller.
  */
@@ -296,10 +299,10 @@ int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d
  * MatMulInteger with a B prepared once (no reference counterpart: for a B that is an initializer,
  * prepared at load as move/2 prepares MatMulNBits weights, lib/transmuter.ex:1104-1240).
  * tmh_int8_weight_prepare transposes B [K, N] (U8 or S8, on the device) into s8 rows of k,
- * zero-padded to a multiple of 128, and precomputes its column sums and the zero-point terms of
+ * zero-padded to a multiple of 256, and precomputes its column sums and the zero-point terms of
  * b_zero (NULL, one value or [N] of B's type); asynchronous on `stream`, whose later work may use
- * the weight at once. K must be a multiple of 16 (TMH_ERR_UNSUPPORTED otherwise; the caller keeps
- * B and uses tmh_matmul_integer). tmh_matmul_integer_prepared computes what tmh_matmul_integer
+ * the weight at once. K must be a multiple of 16 and (N + 128) * (K padded to 256) below 2^31
+ * (TMH_ERR_UNSUPPORTED otherwise; the caller keeps B and uses tmh_matmul_integer). tmh_matmul_integer_prepared computes what tmh_matmul_integer
  * computes for the same B and zero points: y[b, m, n] = sum_k (a[b, m, k] - a_zero[m]) *
  * (B[k, n] - b_zero[n]) as s32 (mod 2^32), A [batch, M, K] U8 or S8, 16-byte aligned, with
  * (M + 128) * K below 2^31; y [batch, M, N] S32.

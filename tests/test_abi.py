@@ -176,3 +176,22 @@ def test_pack_rejects_a_small_buffer():
                                        [bb.ctypes.data_as(ctypes.c_void_p) for bb in bufs],
                                        [ctypes.byref(sz) for sz in sizes]) for x in pair])
     assert st == _lib.ERR_INVALID and b"too small" in lib().tmh_last_error(None)
+
+
+def test_qmoe_refuses_more_tokens_than_its_work_items_number():
+    """Work items carry their index in 16 bits, at least 32 rows each, and an expert gets at most
+    one row per token: more than 2^21 tokens could overflow that field, so the call refuses them
+    before it touches a device (here, with no context at all)."""
+    args = dict(x_dtype=_lib.F16, H=2048, router_dtype=_lib.F32, E=128, k=1)
+    qmoe = lib().tmh_qmoe
+
+    def call(T, k=1):
+        return qmoe(None, None, args["x_dtype"], T, args["H"], None, args["router_dtype"], args["E"], k, None, None,
+                    None, None, None, None, _lib.F16, 4, 0, 1.0, 0.0, 0.0, None, None)
+
+    assert call((32 << 16) + 1) == _lib.ERR_UNSUPPORTED
+    assert b"tokens per call" in lib().tmh_last_error(None)
+    assert call(1 << 24, k=1) == _lib.ERR_UNSUPPORTED  # also past the routed-row limit
+    # At the limit the sizes pass and the missing context is what fails.
+    assert call(32 << 16) == _lib.ERR_INVALID
+    assert b"context is NULL" in lib().tmh_last_error(None)

@@ -3,6 +3,7 @@ row/column-sum corrections) against the oracle, bit-exactly, and the reference's
 MatMulInteger_dynamic_quant graph (DynamicQuantizeLinear -> MatMulInteger on the device, Cast
 and Mul on the host as they stay on the Nx backend) against its ONNX Runtime output."""
 
+import ctypes
 import zlib
 
 import numpy as np
@@ -330,3 +331,51 @@ def test_dynamic_quant_matmul_fixture_with_b_prepared_at_load(ctx):
     expected = f.outputs["y"]
     assert got.shape == expected.shape
     assert np.abs(got - expected).max() <= tolerance(expected)
+
+
+def test_prepared_matmul_integer_offset_view_and_row_blocks(ctx, monkeypatch):
+    """A prepared MatMulInteger whose A is an offset view (not 16-byte aligned) is copied to an
+    aligned buffer first, and an A longer than one launch's 32-bit offsets reach goes in blocks of
+    rows per batch (forced here with a small row limit): both bit-exact against the oracle, with
+    one a_zero_point per row so the blocks must take their own slice of it."""
+    from transmuter_amd import DeviceTensor
+    from transmuter_amd.packed import Int8Weight
+
+    rng = np.random.default_rng(77)
+    batch, m, k, n = 2, 300, 272, 130
+    b = _ints(rng, (k, n), "u8")
+    bz = _ints(rng, (n,), "u8")
+    w = Int8Weight.prepare(ctx, b, bz)
+    a = _ints(rng, (batch, m, k), "u8")
+    az = _ints(rng, (m,), "u8")
+    ref = o.matmul_integer(a, b, az, bz)
+    node = NodeProto(op_type="MatMulInteger", input=["a", "b", "az", ""], output=["y"])
+    # A at byte offset 3 inside a larger buffer.
+    buf = ctx.put(np.concatenate([np.zeros(3, np.uint8), a.ravel(), np.zeros(13, np.uint8)]))
+    view = DeviceTensor(ctx, ctypes.c_void_p(buf.ptr.value + 3), a.shape, "u8", a.nbytes)
+    view._owner = False
+    assert view.ptr.value % 16 != 0
+    for limit in (None, 64):
+        monkeypatch.setattr(quantized, "PREPARED_ROW_LIMIT", limit)
+        print(f"prepared MatMulInteger offset A, row limit {limit}", flush=True)
+        got = quantized.apply(node, [view, w, ctx.put(az), None])[0].numpy()
+        assert np.array_equal(got, ref), limit
+        aligned = quantized.apply(node, [ctx.put(a), w, ctx.put(az), None])[0].numpy()
+        assert np.array_equal(aligned, ref), limit
+    w.free()
+    buf.free()
+
+
+def test_handlers_defer_freeing_their_uploads(ctx):
+    """A handler that uploads host inputs frees them after its work is done, without waiting
+    for it: the temporaries wait on an event until the next synchronize or download."""
+    rng = np.random.default_rng(78)
+    a = _ints(rng, (64, 128), "u8")
+    b = _ints(rng, (128, 48), "s8")
+    node = NodeProto(op_type="MatMulInteger", input=["a", "b"], output=["y"])
+    ctx.synchronize()
+    y = quantized.apply(node, [a, b])[0]
+    assert ctx.pending_frees() == 2
+    got = y.numpy()  # the download drains the stream: the uploads are freed
+    assert ctx.pending_frees() == 0
+    assert np.array_equal(got, o.matmul_integer(a, b, None, None))

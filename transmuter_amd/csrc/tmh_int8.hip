@@ -352,7 +352,8 @@ int tmh_int8_weight_prepare(tmh_ctx* ctx, const void* d_b, int b_dtype, const vo
                 (long long)b_zero_count, (long long)N);
   const int64_t Kp = (K + kQPad - 1) / kQPad * kQPad;
   if ((N + kQT) * Kp >= (int64_t{1} << 31) || K % 16 != 0)
-    return fail(ctx, TMH_ERR_UNSUPPORTED, "a prepared MatMulInteger B needs K a multiple of 16 and N * K below 2^31");
+    return fail(ctx, TMH_ERR_UNSUPPORTED,
+                "a prepared MatMulInteger B needs K a multiple of 16 and (N + 128) * (K padded to 256) below 2^31");
   auto* w = new tmh_int8_weight();
   w->device = ctx->device;
   w->K = K;

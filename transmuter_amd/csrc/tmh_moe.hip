@@ -763,14 +763,22 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
              int64_t E, int k, const tmh_weight* fc1, const void* d_fc1_bias, const tmh_weight* fc2,
              const void* d_fc2_bias, const tmh_weight* fc3, const void* d_fc3_bias, int bias_dtype, int activation,
              int swiglu_fusion, float alpha, float beta, float limit, void* d_y, void* stream) {
-  TMH_TRY(use_device(ctx));
+  // The sizes are checked before the device is touched (a context-free caller gets the same errors).
   if (!is_float_dtype(x_dtype) || !is_float_dtype(router_dtype))
     return fail(ctx, TMH_ERR_INVALID, "QMoE input and router must be float tensors");
-  if (!fc1 || !fc2) return fail(ctx, TMH_ERR_INVALID, "QMoE needs fc1 and fc2 weights");
   if (E <= 0 || E > 1024) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE supports 1 to 1024 experts, got %lld", (long long)E);
   if (k <= 0 || k > 32 || k > E) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE k must be in 1..min(32, experts), got %d", k);
   if (activation < ACT_RELU || activation > ACT_SWIGLU) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE activation %d", activation);
   if (T < 0 || H <= 0) return fail(ctx, TMH_ERR_INVALID, "QMoE sizes must be positive");
+  // Work items are numbered expert << 16 | item, with at least kMoeRows rows per item, and an
+  // expert receives at most one row per token (the k experts of a token are distinct): T tokens
+  // must not give an expert more than 2^16 items.
+  if ((T + kMoeRows - 1) / kMoeRows > (int64_t(1) << 16))
+    return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE supports at most %lld tokens per call, got %lld",
+                (long long)kMoeRows << 16, (long long)T);
+  if (T * k >= (int64_t(1) << 24)) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE supports fewer than 2^24 routed rows");
+  TMH_TRY(use_device(ctx));
+  if (!fc1 || !fc2) return fail(ctx, TMH_ERR_INVALID, "QMoE needs fc1 and fc2 weights");
   if (fc1->N % E || fc2->N % E) return fail(ctx, TMH_ERR_INVALID, "QMoE weights do not hold %lld experts", (long long)E);
   const int64_t n1 = fc1->N / E;
   if (fc1->K != H || fc2->N / E != H)
@@ -793,7 +801,6 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
   if (T == 0) return TMH_OK;
   if (!d_x || !d_router || !d_y) return fail(ctx, TMH_ERR_INVALID, "QMoE: NULL pointer");
   const int64_t tk = T * k;
-  if (tk >= (int64_t(1) << 24)) return fail(ctx, TMH_ERR_UNSUPPORTED, "QMoE supports fewer than 2^24 routed rows");
   hipStream_t s = pick_stream(ctx, stream);
   const size_t es = static_cast<size_t>(dtype_size(x_dtype));
   // Rows per work item: 64 when experts average more than 24 rows and every product takes the

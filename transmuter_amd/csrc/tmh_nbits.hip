@@ -906,6 +906,7 @@ struct MatArgs {
   int y_dt, dot_dt;
   int64_t ldy;
   float* ws = nullptr;  // split-K partial sums (splitk_bytes() of them), resolved by the entry point
+  size_t split_cap = 0;  // most bytes of partial sums the plan may use (0: no limit)
 };
 
 int bsc_shift_of(const tmh_weight* w) {
@@ -959,8 +960,9 @@ void launch_gemm(const tmh_weight* w, const MatArgs& a, hipStream_t s) {
 }
 
 // Split K when the output tiles cannot fill the GPU: partial sums go to the context's
-// workspace and k_splitk_reduce adds them. During stream capture the workspace cannot grow,
-// so a capture that finds it too small runs without splitting.
+// workspace (tmh_matmul_nbits) or the fixed per-device scratch (tmh_matmul_nbits_noalloc) and
+// k_splitk_reduce adds them. During stream capture the workspace cannot grow, so a captured
+// tmh_matmul_nbits that finds it too small fails rather than running a different plan.
 // Tile shape and K split of one prefill GEMM. Each candidate (BM x 64*WN tiles; KS = 2 for the
 // 128x128 tile on eight wavefronts that split each k-block's steps; 1-16 splits of K) is priced
 // as rounds of workgroups over the CUs times the work of one, at the per-CU rate the tile shape
@@ -984,7 +986,13 @@ struct GemmPlan {
 
 int cus_of(const tmh_ctx* ctx) { return ctx->num_cus > 0 ? ctx->num_cus : 256; }
 
-GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bits, int cus) {
+// split_cap > 0 bounds the f32 partial sums a split plan keeps (splits * M * N * 4 bytes): plans
+// beyond it are not considered, a forced one included.
+GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bits, int cus, size_t split_cap = 0) {
+  auto fits = [&](int64_t splits) {
+    return split_cap == 0 || splits == 1 ||
+           static_cast<double>(splits) * static_cast<double>(M) * static_cast<double>(N) * 4.0 <= static_cast<double>(split_cap);
+  };
   const double cw = 512.0 / bits;
   GemmPlan best{256, 2, 1, static_cast<int>(nchunks), 1};
   double best_t = 1e30;
@@ -996,7 +1004,7 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
       if (splits > 1 && 2 * splits > nchunks) break;
       const int64_t cps = (nchunks + splits - 1) / splits;
       const int64_t used = (nchunks + cps - 1) / cps;
-      if (used != splits) continue;
+      if (used != splits || !fits(splits)) continue;
       // A last round that occupies a fraction f of the CUs runs each workgroup faster (less
       // memory contention, a higher clock): priced at 0.6 + 0.4 f of a full round.
       const int64_t wgs = tiles * splits, full = wgs / cus, rem = wgs % cus;
@@ -1015,7 +1023,8 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
     if ((got == 3 || got == 4) && (bm == 64 || bm == 128 || bm == 256) && (wn == 2 || wn == 4) && sp >= 1 &&
         sp <= nchunks && (ks == 1 || (ks == 2 && bm <= 128 && wn == 2))) {
       const int cps = static_cast<int>((nchunks + sp - 1) / sp);
-      best = GemmPlan{bm, wn, static_cast<int>((nchunks + cps - 1) / cps), cps, ks};
+      const int used = static_cast<int>((nchunks + cps - 1) / cps);
+      if (fits(used)) best = GemmPlan{bm, wn, used, cps, ks};
     }
   }
   return best;
@@ -1047,7 +1056,7 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
-  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, cus_of(ctx));
+  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, cus_of(ctx), a.split_cap);
   if (p.bm == 64) {
     if (p.ks == 2)
       launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 64, 2>(ctx, w, a, s, p.splits, p.cps);
@@ -1085,7 +1094,7 @@ bool gemm_lds_ok(const tmh_weight* w, const MatArgs& a) {
 // K, else 0 (the GEMVs and unsplit GEMMs use no scratch memory).
 size_t splitk_bytes(const tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a) {
   if (!fast_path(w, a) || !gemm_lds_ok(w, a)) return 0;
-  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, w->bits, cus_of(ctx));
+  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, w->bits, cus_of(ctx), a.split_cap);
   return p.splits > 1 ? static_cast<size_t>(p.splits) * static_cast<size_t>(a.M) * static_cast<size_t>(w->N) * sizeof(float)
                       : 0;
 }
@@ -1723,12 +1732,13 @@ int tmh_matmul_nbits_noalloc(tmh_ctx* ctx, const tmh_weight* w, const void* d_a,
   bool run = false;
   TMH_TRY(prepare_matmul(ctx, w, d_a, a_dtype, M, lda, d_bias, bias_dtype, d_y, y_dtype, ldy, &a, &run));
   if (!run) return TMH_OK;
+  // The plan keeps its partial sums within the scratch: where tmh_matmul_nbits's plan would need
+  // more, the best plan with fewer splits of K (or none) runs instead.
+  a.split_cap = kNoallocScratchBytes;
   if (const size_t need = splitk_bytes(ctx, w, a)) {
-    if (need > kNoallocScratchBytes)
-      return fail(ctx, TMH_ERR_INVALID,
-                  "MatMulNBits with M=%lld, N=%lld, K=%lld splits K into %zu bytes of partial sums; "
-                  "tmh_matmul_nbits_noalloc holds at most %zu bytes (use tmh_matmul_nbits)",
-                  (long long)M, (long long)w->N, (long long)w->K, need, kNoallocScratchBytes);
+    if (need > kNoallocScratchBytes)  // the plan honours the cap; kept as a guard on the scratch's bounds
+      return fail(ctx, TMH_ERR_INVALID, "MatMulNBits partial sums of %zu bytes exceed the %zu-byte scratch", need,
+                  kNoallocScratchBytes);
     float* p = nullptr;
     hipError_t err = hipErrorInvalidDevice;
     if (ctx->device >= 0 && ctx->device < kMaxDevices) {

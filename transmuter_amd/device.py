@@ -91,14 +91,73 @@ def merge_types(a: str, b: str) -> str:
     return a if a == b else "f32"
 
 
+def _device_nbytes(obj) -> int:
+    """Device bytes a temporary holds (a tensor's buffer, a packed weight's tiles)."""
+    if hasattr(obj, "device_bytes"):
+        try:
+            return obj.device_bytes()
+        except Exception:
+            return 0
+    return getattr(obj, "nbytes", 0)
+
+
 class Context:
-    """One device and its stream (tmh_ctx)."""
+    """One device and its stream (tmh_ctx).
+
+    Temporaries of an asynchronous call (inputs a handler uploaded, a weight it repacked) are
+    handed to `defer_free` instead of being freed after a synchronize: an event recorded behind
+    the call's work fences them, and they are freed once that work is done, at the next point
+    where the host waits anyway (`synchronize`, a download) or when more than DEFER_LIMIT bytes
+    are waiting. hipFree itself waits for the device, so a free right after a launch would cost
+    the round trip the deferral saves."""
+
+    DEFER_LIMIT = 1 << 30
 
     def __init__(self, device: int = 0):
         handle = ctypes.c_void_p()
         check(lib().tmh_ctx_create(device, ctypes.byref(handle)))
         self.handle = handle
         self.device = device
+        self._pending = []  # (event, [objects]) in record order
+        self._pending_bytes = 0
+        self._events = []  # recycled events
+
+    def defer_free(self, *objs, stream=None) -> None:
+        """Frees `objs` (DeviceTensor, PackedWeight or anything with free()) once the work queued
+        on `stream` (None: the context's) so far has finished."""
+        objs = [o for o in objs if o is not None]
+        if not objs:
+            return
+        ev = self._events.pop() if self._events else None
+        if ev is None:
+            ev = ctypes.c_void_p()
+            self.check(lib().tmh_event_create(self.handle, ctypes.byref(ev)))
+        self.check(lib().tmh_event_record(self.handle, ev, stream))
+        self._pending.append((ev, objs))
+        self._pending_bytes += sum(_device_nbytes(o) for o in objs)
+        if self._pending_bytes > self.DEFER_LIMIT:
+            self.synchronize()
+
+    def pending_frees(self) -> int:
+        """Temporaries waiting for their work to finish."""
+        return sum(len(objs) for _ev, objs in self._pending)
+
+    def reap(self) -> None:
+        """Frees the deferred temporaries whose work has finished (it never waits)."""
+        if not self._pending:
+            return
+        keep = []
+        done = ctypes.c_int()
+        for ev, objs in self._pending:
+            self.check(lib().tmh_event_query(self.handle, ev, ctypes.byref(done)))
+            if not done.value:
+                keep.append((ev, objs))
+                continue
+            for o in objs:
+                o.free()
+            self._events.append(ev)
+        self._pending = keep
+        self._pending_bytes = sum(_device_nbytes(o) for _ev, objs in keep for o in objs)
 
     @property
     def stream(self) -> ctypes.c_void_p:
@@ -142,9 +201,23 @@ class Context:
 
     def synchronize(self) -> None:
         self.check(lib().tmh_synchronize(self.handle, None))
+        self.reap()
 
     def close(self) -> None:
         if self.handle:
+            if self._pending:
+                lib().tmh_synchronize(self.handle, None)
+                for _ev, objs in self._pending:
+                    for o in objs:
+                        try:
+                            o.free()
+                        except Exception:
+                            pass
+                self._events.extend(ev for ev, _objs in self._pending)
+                self._pending = []
+            for ev in self._events:
+                lib().tmh_event_destroy(self.handle, ev)
+            self._events = []
             lib().tmh_ctx_destroy(self.handle)
             self.handle = None
 
@@ -173,6 +246,7 @@ class DeviceTensor:
         if self.nbytes:
             self.ctx.check(lib().tmh_download(self.ctx.handle, host.ctypes.data_as(ctypes.c_void_p),
                                               self.ptr, self.nbytes))
+            self.ctx.reap()  # the download drained the context's stream
         return bf16_host(host) if self.dtype == "bf16" else host
 
     def reshape(self, shape) -> "DeviceTensor":

@@ -159,7 +159,10 @@ def move(model: Model, ctx: Context) -> Model:
               if name not in freed}
     params.update(weights)
     static = {name: value for name, value in model.static.items() if name not in freed}
-    moved = prepare_matmul_integer(replace(model, nodes=nodes, params=params, static=static, backend=ctx), ctx)
+    # Device copies this move made itself (not the caller's own device tensors) may be released.
+    made = {name for name, value in params.items() if value is not model.params.get(name)}
+    moved = prepare_matmul_integer(replace(model, nodes=nodes, params=params, static=static, backend=ctx), ctx,
+                                   release=made)
     # move/2 ends with Fusion.matmuls/2 (lib/transmuter.ex:1181).
     return merge_matmuls(moved)
 
@@ -187,11 +190,12 @@ def _int8_preparable(node, values: dict) -> bool:
     return len(shape) == 2 and dtype in ("u8", "s8") and Int8Weight.supported(*shape)
 
 
-def prepare_matmul_integer(model: Model, ctx: Context) -> Model:
+def prepare_matmul_integer(model: Model, ctx: Context, release=frozenset()) -> Model:
     """MatMulInteger nodes whose B is an initializer read "<B>:int8" afterwards: B transposed once
     into the int8 GEMM's layout with its b_zero_point folded in (no counterpart in move/2, which
     leaves MatMulInteger to the backend's dot; the outputs are the same s32 sums). The node keeps
-    A and a_zero_point; B and b_zero_point leave the params when nothing else reads them."""
+    A and a_zero_point; B and b_zero_point leave the params when nothing else reads them; those
+    named in `release` (the device copies move/2 made itself) are freed at once."""
     values = {**model.static, **model.params}
     prepared = [node for node in model.nodes if _int8_preparable(node, values)]
     if not prepared:
@@ -209,8 +213,12 @@ def prepare_matmul_integer(model: Model, ctx: Context) -> Model:
         if name not in weights:
             if name in values:
                 raise ValueError(f"the model already has a value named {name}")
-            weights[name] = Int8Weight.prepare(ctx, _host_value(values[b_name]),
-                                               _host_value(values[bz_name]) if bz_name else None)
+            # A B already on the device (move/2 put the params there) is prepared from there, with
+            # no host round trip; a static (host) B is uploaded by prepare.
+            b_val, bz_val = values[b_name], values[bz_name] if bz_name else None
+            weights[name] = Int8Weight.prepare(
+                ctx, b_val if isinstance(b_val, DeviceTensor) else _host_value(b_val),
+                bz_val if bz_val is None or isinstance(bz_val, DeviceTensor) else _host_value(bz_val))
         a_zero = node.input[2] if len(node.input) > 2 else ""
         nodes.append(replace(node, input=[node.input[0], name, a_zero, ""]))
     used = set(model.outputs)
@@ -218,6 +226,12 @@ def prepare_matmul_integer(model: Model, ctx: Context) -> Model:
         used.update(node.input)
     freed = {name for node in prepared for name in (node.input[1], node.input[3] if len(node.input) > 3 else "")
              if name and name not in used}
+    # The device copies of B and b_zero_point that nothing reads any more are released now rather
+    # than when the old params are dropped, so a load does not hold each int8 weight twice.
+    for name in freed & set(release):
+        value = model.params.get(name)
+        if isinstance(value, DeviceTensor):
+            value.free()
     params = {name: value for name, value in model.params.items() if name not in freed}
     params.update(weights)
     static = {name: value for name, value in model.static.items() if name not in freed}

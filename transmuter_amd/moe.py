@@ -140,12 +140,7 @@ def qmoe(node, inputs: list) -> DeviceTensor:
             biases[2].ptr if biases[2] is not None else None, NX_TO_TMH[bias_dt], _lib.ACTIVATIONS[activation],
             fusion, alpha, beta, limit, y.ptr, None))
     finally:
-        if owned or router_t is not router:
-            ctx.synchronize()
-        for o in owned:
-            o.free()
-        if router_t is not router:
-            router_t.free()
+        ctx.defer_free(*owned, router_t if router_t is not router else None)
     return y
 
 

@@ -148,10 +148,14 @@ class Int8Weight:
     def shape(self) -> tuple[int, int]:
         return (self.k, self.n)
 
+    PAD = 256  # a prepared B's rows of k are zero-padded to a multiple of this (the C library's kQPad)
+
     @staticmethod
     def supported(k: int, n: int) -> bool:
-        """Shapes the prepared GEMM takes: K a multiple of 16 (N * K below 2^31)."""
-        return k > 0 and n > 0 and k % 16 == 0 and (n + 128) * (-(-k // 128) * 128) < 2 ** 31
+        """Shapes tmh_int8_weight_prepare takes: K a multiple of 16, and (N + 128) * K padded to
+        256 below 2^31 (the prepared B's 32-bit offsets; the same test as the C library's)."""
+        kp = -(-k // Int8Weight.PAD) * Int8Weight.PAD
+        return k > 0 and n > 0 and k % 16 == 0 and (n + 128) * kp < 2 ** 31
 
     @classmethod
     def prepare(cls, ctx: Context, b, b_zero=None) -> "Int8Weight":

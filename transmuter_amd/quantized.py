@@ -143,7 +143,7 @@ def matmul_nbits(a: DeviceTensor, w: PackedWeight, bias=None, stream=None) -> De
             bias_t.tmh_dtype if bias_t is not None else 0, y.ptr, NX_TO_TMH[y_type], w.n, stream))
     finally:
         if own_bias:
-            bias_t.free()
+            ctx.defer_free(bias_t)
     return y
 
 
@@ -176,10 +176,8 @@ def _op_matmul_nbits(node, inputs):
     try:
         return matmul_nbits(a, w, bias)
     finally:
-        ctx.synchronize()
-        w.free()
-        for t in temps:
-            t.free()
+        # Freed once the call's work is done, without a wait here.
+        ctx.defer_free(w, *temps)
 
 
 # ---------------------------------------------------------------- GatherBlockQuantized
@@ -231,11 +229,7 @@ def _op_gather_block_quantized(node, inputs):
             sc_t.ptr, sc_t.tmh_dtype, blocks, zp_t.ptr if zp_t is not None else None,
             zp_t.tmh_dtype if zp_t is not None else 0, bits, out.ptr, None))
     finally:
-        if own_d or own_i or own_s or own_z:
-            ctx.synchronize()
-        for t, own in ((data_t, own_d), (ids_t, own_i), (sc_t, own_s), (zp_t, own_z)):
-            if own:
-                t.free()
+        ctx.defer_free(*[t for t, own in ((data_t, own_d), (ids_t, own_i), (sc_t, own_s), (zp_t, own_z)) if own])
     return out
 
 
@@ -285,11 +279,7 @@ def _op_dequantize_linear(node, inputs):
             z_t.ptr if z_t is not None else None, z_t.tmh_dtype if z_t is not None else 0, mode,
             block_size, y.ptr, None))
     finally:
-        if own_x or own_s or own_z:
-            ctx.synchronize()
-        for t, own in ((x_t, own_x), (s_t, own_s), (z_t, own_z)):
-            if own:
-                t.free()
+        ctx.defer_free(*[t for t, own in ((x_t, own_x), (s_t, own_s), (z_t, own_z)) if own])
     return y
 
 
@@ -339,11 +329,7 @@ def _op_matmul_integer(node, inputs):
                                                    b_t.tmh_dtype, *args, 1, m, k, n, 0,
                                                    _ptr_offset(y, i * m * n), None))
     finally:
-        if own_a or own_b or own_az or own_bz:
-            ctx.synchronize()
-        for t, own in ((a_t, own_a), (b_t, own_b), (az_t, own_az), (bz_t, own_bz)):
-            if own:
-                t.free()
+        ctx.defer_free(*[t for t, own in ((a_t, own_a), (b_t, own_b), (az_t, own_az), (bz_t, own_bz)) if own])
     if squeeze:
         return y.reshape(out_shape[:-2] + (n,))
     return y
@@ -370,22 +356,51 @@ def _matmul_integer_prepared(a, w: "Int8Weight", a_zero, b_zero):
         raise ArgumentError(f"MatMulInteger a_zero_point has {math.prod(_shape_of(a_zero))} values")
     a_t, own_a = _device(ctx, a)
     az_t, own_az = _device(ctx, a_zero)
+    temps = [t for t, own in ((a_t, own_a), (az_t, own_az)) if own]
     try:
         out_shape = batch_shape + (m, w.n)
         y = ctx.empty(out_shape, "s32")
-        ctx.check(lib().tmh_matmul_integer_prepared(ctx.handle, a_t.ptr, a_t.tmh_dtype,
-                                                    az_t.ptr if az_t is not None else None,
-                                                    az_t.size if az_t is not None else 0, batch, m, w.handle,
-                                                    y.ptr, None))
+        if a_t.ptr.value % 16:
+            # The prepared GEMM streams A 16 bytes at a time: an A that does not start on a 16-byte
+            # boundary (an offset view) is copied to a fresh buffer first.
+            a_al = ctx.empty(a_t.shape, a_t.dtype)
+            temps.append(a_al)
+            ctx.check(lib().tmh_copy_2d(ctx.handle, a_al.ptr, a_t.nbytes, a_t.ptr, a_t.nbytes, a_t.nbytes, 1, None))
+            a_t = a_al
+        rows = _prepared_rows(k)
+        per_row_zero = az_t is not None and az_t.size == m and m > 1
+        if m <= rows:
+            ctx.check(lib().tmh_matmul_integer_prepared(ctx.handle, a_t.ptr, a_t.tmh_dtype,
+                                                        az_t.ptr if az_t is not None else None,
+                                                        az_t.size if az_t is not None else 0, batch, m, w.handle,
+                                                        y.ptr, None))
+        else:
+            # One launch addresses (rows + 128) * K bytes of A with 32-bit offsets: longer A goes in
+            # blocks of rows, batch by batch (row offsets keep A 16-byte aligned, K being a
+            # multiple of 16).
+            for bi in range(batch):
+                for r0 in range(0, m, rows):
+                    mb = min(rows, m - r0)
+                    zero = _ptr_offset(az_t, r0) if per_row_zero else (az_t.ptr if az_t is not None else None)
+                    zcount = mb if per_row_zero else (az_t.size if az_t is not None else 0)
+                    ctx.check(lib().tmh_matmul_integer_prepared(
+                        ctx.handle, _ptr_offset(a_t, (bi * m + r0) * k), a_t.tmh_dtype, zero, zcount, 1, mb,
+                        w.handle, _ptr_offset(y, (bi * m + r0) * w.n), None))
     finally:
-        if own_a or own_az:
-            ctx.synchronize()
-        for t, own in ((a_t, own_a), (az_t, own_az)):
-            if own:
-                t.free()
+        ctx.defer_free(*temps)
     if squeeze:
         return y.reshape(out_shape[:-2] + (w.n,))
     return y
+
+
+# Rows of A one prepared MatMulInteger launch takes: its 32-bit offsets cover (rows + 128) * K
+# bytes of A. None: the largest count that fits; tests set a small value to reach the row blocks.
+PREPARED_ROW_LIMIT = None
+
+
+def _prepared_rows(k: int) -> int:
+    fit = (2 ** 31 - 1) // k - 128
+    return max(1, min(fit, PREPARED_ROW_LIMIT) if PREPARED_ROW_LIMIT else fit)
 
 
 # ---------------------------------------------------------------- DynamicQuantizeLinear
@@ -407,8 +422,7 @@ def _op_dynamic_quantize_linear(node, inputs):
                                                     zero.ptr, None))
     finally:
         if own:
-            ctx.synchronize()
-            x_t.free()
+            ctx.defer_free(x_t)
     return [y, scale, zero]
 
 
