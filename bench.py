@@ -117,6 +117,7 @@ class Graph:
 
 
 USE_GRAPHS = True
+STAMP_HEADLINE = True  # time the headline's kernels inside the replays too (--no-timeline turns it off)
 
 
 def rocprof_domains() -> list[str]:
@@ -210,6 +211,14 @@ def decode_sweep(ctx, steps, warmup, sets, ms, merged=False, full_step=False):
             f"{results[m]['us_per_launch']:.2f} us/launch")
         for g in graphs:
             g.destroy()
+        if full_step and m == 1 and not merged and STAMP_HEADLINE and USE_GRAPHS:
+            # The same step's kernels timed inside the replays (launch timeline), two rotations.
+            calls = [(f"{name} {k}->{n}", nbits_bytes(k, n, m), 2 * m * k * n) for _layer in range(QWEN3_LAYERS)
+                     for name, k, n in QWEN3_06B]
+            res = timeline_steps(ctx, [lambda s=s: [matmul_call(ctx, w, a[w.k], y[w.n], m)
+                                                    for layer in weights[s % sets] for w in layer]
+                                       for s in range(2 * sets)], calls, reps=steps, warmup=warmup)
+            results[m]["timeline"] = timeline_summary(res)
         if full_step and m == 1:
             results[m].update(decode_floors(ctx, steps, warmup, weights, lambda s: [
                 matmul_call(ctx, w, a[w.k], y[w.n], m) for layer in range(QWEN3_LAYERS) for w in weights[s][layer]]))
@@ -827,6 +836,295 @@ def traffic_per_launch():
     return t.get("hbm_bytes_per_launch")
 
 
+# ---------------------------------------------------------------- launch timelines (in-graph kernel times)
+
+
+def timeline_steps(ctx, records, calls, reps=20, warmup=5, capacity=1 << 22):
+    """Times `records` (callables, one step of calls each) as plain HIP graphs, then captures them
+    again with the launch timeline on (transmuter_amd.timeline) and replays those stamping graphs
+    once each, back to back, after a warm-up. `calls` lists each step's calls as (label, bytes,
+    flops). Returns the event-timed ms per step of both runs and, per launch of the stamping
+    replays, its kernel, call label and in-kernel time (first wavefront's start to last one's
+    end) with the time to the next launch's start."""
+    from transmuter_amd.timeline import Timeline
+
+    plain = [Graph(ctx, r) for r in records]
+    steps = max(reps, len(plain))
+    ms_plain = time_graphs(ctx, plain, steps, warmup) / steps
+    tl = Timeline(ctx, capacity)
+    tl.begin()
+    try:
+        stamped = [Graph(ctx, r) for r in records]
+    finally:
+        log = tl.end()
+    if tl.dropped:
+        raise RuntimeError(f"the timeline dropped {tl.dropped} launches: raise its capacity")
+    for i in range(warmup):
+        plain[i % len(plain)].launch()
+    ctx.synchronize()
+    t = Timer(ctx)
+    t.start()
+    for g in stamped:
+        g.launch()
+    ms_stamped = t.stop_ms() / len(stamped)
+    launches = tl.launches()
+    for g in plain + stamped:
+        g.destroy()
+    tl.free()
+    per_step = len(log) // len(records)
+    if per_step * len(records) != len(log):
+        raise RuntimeError("the steps launched different numbers of kernels")
+    rows = []
+    for s in range(len(records)):
+        step = launches[s * per_step:(s + 1) * per_step]
+        call = -1
+        for j, ln in enumerate(step):
+            if len(calls) == per_step:  # one entry per stamped launch
+                call = j
+            elif ln["kernel"] != "k_splitk_reduce":  # one per call; a split-K sum belongs to its GEMM
+                call += 1
+            label, nbytes, flops = calls[call]
+            nxt = step[j + 1]["start_us"] if j + 1 < len(step) else ln["end_us"]
+            rows.append({**ln, "step": s, "label": label, "bytes": nbytes, "flops": flops,
+                         "to_next_us": nxt - ln["start_us"]})
+    return {"ms_per_step": ms_plain, "ms_per_step_stamped": ms_stamped, "steps_stamped": len(records),
+            "launches_per_step": per_step, "rows": rows}
+
+
+def timeline_summary(res):
+    """Per (call label, kernel): launches per step, mean in-kernel us, mean launch-to-next-launch
+    us, shader clock, and the algorithmic rate over the in-kernel time; per step: the event time
+    of plain and stamping replays, the summed in-kernel time and the span from the first start
+    to the last end."""
+    groups = {}
+    for r in res["rows"]:
+        groups.setdefault((r["label"], r["kernel"]), []).append(r)
+    steps = res["steps_stamped"]
+    out = []
+    for (label, kernel), rs in groups.items():
+        us = float(np.mean([r["us"] for r in rs]))
+        nxt = float(np.mean([r["to_next_us"] for r in rs]))
+        ghz = [r["ghz"] for r in rs if r.get("ghz")]
+        nbytes, flops = rs[0]["bytes"], rs[0]["flops"]
+        out.append({"label": label, "kernel": kernel, "per_step": len(rs) / steps, "kernel_us": us,
+                    "kernel_us_min": float(min(r["us"] for r in rs)), "kernel_us_max": float(max(r["us"] for r in rs)),
+                    "to_next_us": nxt, "ghz": float(np.mean(ghz)) if ghz else None,
+                    "gbs_in_kernel": nbytes / (us * 1e-6) / 1e9 if nbytes and kernel != "k_splitk_reduce" else None,
+                    "tflops_in_kernel": flops / (us * 1e-6) / 1e12 if flops and kernel != "k_splitk_reduce" else None})
+    spans, sums = [], []
+    for s in range(steps):
+        rs = [r for r in res["rows"] if r["step"] == s]
+        spans.append(max(r["end_us"] for r in rs) - min(r["start_us"] for r in rs))
+        sums.append(sum(r["us"] for r in rs))
+    return {"ms_per_step": res["ms_per_step"], "ms_per_step_stamped": res["ms_per_step_stamped"],
+            "launches_per_step": res["launches_per_step"], "steps_stamped": steps,
+            "kernel_us_per_step": float(np.mean(sums)), "span_us_per_step": float(np.mean(spans)), "kernels": out}
+
+
+def timeline_markdown(title, command, parts, notes):
+    lines = [f"# {title}", "", "Command (MI355X, one GPU):", "", "```", command, "```", ""]
+    lines += notes + [""]
+    for name, s in parts:
+        lines += [f"## {name}", "",
+                  f"- event-timed step, plain graphs: {s['ms_per_step'] * 1e3:.1f} us; stamping graphs: "
+                  f"{s['ms_per_step_stamped'] * 1e3:.1f} us ({s['steps_stamped']} steps stamped, "
+                  f"{s['launches_per_step']} launches per step)",
+                  f"- per step: in-kernel time summed over the launches {s['kernel_us_per_step']:.1f} us; first "
+                  f"start to last end {s['span_us_per_step']:.1f} us", "",
+                  "| call | kernel | per step | in-kernel us (mean, min-max) | start to next start us | "
+                  "shader GHz | GB/s in-kernel | TFLOP/s in-kernel |",
+                  "|---|---|---|---|---|---|---|---|"]
+        for k in s["kernels"]:
+            gbs = f"{k['gbs_in_kernel']:.0f}" if k["gbs_in_kernel"] else "-"
+            tf = f"{k['tflops_in_kernel']:.1f}" if k["tflops_in_kernel"] else "-"
+            ghz = f"{k['ghz']:.2f}" if k["ghz"] else "-"
+            lines.append(f"| {k['label']} | `{k['kernel']}` | {k['per_step']:g} | {k['kernel_us']:.2f} "
+                         f"({k['kernel_us_min']:.2f}-{k['kernel_us_max']:.2f}) | {k['to_next_us']:.2f} | {ghz} | "
+                         f"{gbs} | {tf} |")
+        lines.append("")
+    lines += ["```json", json.dumps({name: s for name, s in parts}, indent=1), "```", ""]
+    return "\n".join(lines)
+
+
+def decode_weights(ctx, sets, rng):
+    from transmuter_amd import PackedWeight
+
+    weights = []
+    for _s in range(sets):
+        weights.append([[PackedWeight.upload(ctx, *make_weight_parts(rng, k, n), k=k, n=n, bits=4, block_size=32,
+                                             weight_dtype="f16") for _name, k, n in QWEN3_06B]
+                        for _layer in range(QWEN3_LAYERS)])
+    return weights
+
+
+def timeline_decode(ctx, sets=4, steps=8, m=1, floors=True):
+    """The headline decode step (196 GEMVs at M = m over rotating weight copies) with the launch
+    timeline, and the same step's floors: an empty kernel per projection, a plain read of each
+    projection's packed weights, and a plain read of all its bytes (weights, scales, zero points)."""
+    from transmuter_amd._lib import lib
+
+    rng = np.random.default_rng(20260101)
+    weights = decode_weights(ctx, sets, rng)
+    a = {k: ctx.put(rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)) for k in (1024, 2048, 3072)}
+    y = {n: ctx.empty((m, n), "f16") for n in (1024, 2048, 3072)}
+    sink = ctx.empty((16,), "u8")
+    calls = [(f"{name} {k}->{n}", nbits_bytes(k, n, m), 2 * m * k * n) for _layer in range(QWEN3_LAYERS)
+             for name, k, n in QWEN3_06B]
+    parts = []
+    gemv = timeline_steps(ctx, [lambda s=s: [matmul_call(ctx, w, a[w.k], y[w.n], m) for layer in weights[s % sets]
+                                             for w in layer] for s in range(steps)], calls)
+    parts.append((f"decode GEMVs, M={m}", timeline_summary(gemv)))
+    if floors:
+        fl = [("empty kernel", lambda w: lib().tmh_floor_empty(ctx.handle, 256, None)),
+              ("plain read of the packed weights", lambda w: lib().tmh_floor_read(ctx.handle, w.handle, sink.ptr, None)),
+              ("plain read of weights, scales and zero points",
+               lambda w: lib().tmh_floor_read_all(ctx.handle, w.handle, sink.ptr, None))]
+        for name, fn in fl:
+            res = timeline_steps(ctx, [lambda s=s, fn=fn: [ctx.check(fn(w)) for layer in weights[s % sets] for w in layer]
+                                       for s in range(steps)], [(c[0], c[1], 0) for c in calls])
+            parts.append((f"floor: {name}", timeline_summary(res)))
+    for ws in weights:
+        for layer in ws:
+            for w in layer:
+                w.free()
+    return parts
+
+
+def timeline_vocab(ctx, per_graph=12):
+    """lm_head (151936 x 1024, M = 1 and 8) over 12 rotating weight copies, the plain read of all
+    its bytes, the [8, 512] vocabulary gather and the store-only launch of the gather's output."""
+    from transmuter_amd import PackedWeight
+    from transmuter_amd._lib import F16, S64, U8, lib
+
+    rng = np.random.default_rng(4)
+    vocab, hidden = 151936, 1024
+    b, sc, zp = make_weight_parts(rng, hidden, vocab)
+    ws = [PackedWeight.upload(ctx, b, sc, zp, k=hidden, n=vocab, bits=4, block_size=32, weight_dtype="f16")]
+    ws += [PackedWeight.concat([ws[0]]) for _ in range(-(-ROTATE_BYTES // ws[0].device_bytes()) - 1)]
+    parts = []
+    for m in (1, 8):
+        a = ctx.put(rng.standard_normal((m, hidden), dtype=np.float32).astype(np.float16))
+        y = ctx.empty((m, vocab), "f16")
+        res = timeline_steps(ctx, [lambda s=s: [matmul_call(ctx, ws[(s * per_graph + i) % len(ws)], a, y, m)
+                                                for i in range(per_graph)] for s in range(2)],
+                             [(f"lm_head M={m}", nbits_bytes(hidden, vocab, m), 2 * m * hidden * vocab)] * per_graph)
+        parts.append((f"lm_head 151936x1024, M={m}", timeline_summary(res)))
+    sink = ctx.empty((16,), "u8")
+    all_bytes = ws[0].device_bytes()
+    res = timeline_steps(ctx, [lambda s=s: [ctx.check(lib().tmh_floor_read_all(ctx.handle, ws[(s * per_graph + i) % len(ws)]
+                                                                               .handle, sink.ptr, None))
+                                            for i in range(per_graph)] for s in range(2)],
+                         [("plain read of the weight's bytes", all_bytes, 0)] * per_graph)
+    parts.append(("floor: plain read of all lm_head bytes (weights, scales, zero points)", timeline_summary(res)))
+    for w in ws:
+        w.free()
+    tables = [(ctx.put(b.reshape(vocab, -1)), ctx.put(sc.reshape(vocab, -1)), ctx.put(zp.reshape(vocab, -1)))
+              for _ in range(2)]
+    ids = [ctx.put(rng.integers(0, vocab, (8, 512)).astype(np.int64)) for _ in range(per_graph)]
+    rows = ctx.empty((8, 512, hidden), "f16")
+
+    def gathers(s):
+        for i in range(per_graph):
+            table, scales, zps = tables[(s + i) % 2]
+            ctx.check(lib().tmh_gather_block_quantized(ctx.handle, table.ptr, U8, vocab, hidden // 2, ids[i].ptr, S64,
+                                                       4096, scales.ptr, F16, hidden // 32, zps.ptr, U8, 4, rows.ptr,
+                                                       None))
+
+    g_bytes = 4096 * (hidden // 2 + hidden // 32 * 2 + hidden // 64 + 8) + 4096 * hidden * 2
+    res = timeline_steps(ctx, [lambda s=s: gathers(s) for s in range(2)], [("gather [8, 512]", g_bytes, 0)] * per_graph)
+    parts.append(("GatherBlockQuantized [8, 512] ids of 151936 x 1024", timeline_summary(res)))
+    out_bytes = 4096 * hidden * 2
+    res = timeline_steps(ctx, [lambda: [ctx.check(lib().tmh_floor_write(ctx.handle, rows.ptr, out_bytes, None))
+                                        for _ in range(per_graph)]] * 2, [("store-only", out_bytes, 0)] * per_graph)
+    parts.append(("floor: the gather's 8 MiB of output stores alone", timeline_summary(res)))
+    return parts
+
+
+def timeline_prefill(ctx, ms=(256, 2048), per_graph=4):
+    """The SmolLM3-3B prefill projections at each M, each call on its own weight copy."""
+    from transmuter_amd import PackedWeight
+
+    rng = np.random.default_rng(3)
+    parts = []
+    for name, k, n in SMOLLM3_3B:
+        b, sc, zp = make_weight_parts(rng, k, n, bs=128, scale_mul=0.005)
+        w0 = PackedWeight.upload(ctx, b, sc, zp, k=k, n=n, bits=4, block_size=128, weight_dtype="f16")
+        copies = [w0] + [PackedWeight.concat([w0]) for _ in range(max(1, -(-ROTATE_BYTES // w0.device_bytes())) - 1)]
+        for m in ms:
+            a = ctx.put(rng.standard_normal((m, k), dtype=np.float32).astype(np.float16))
+            y = ctx.empty((m, n), "f16")
+            matmul_call(ctx, copies[0], a, y, m)  # sizes the split-K workspace before capture
+            ctx.synchronize()
+            steps = min(4, max(1, len(copies) // per_graph))
+            res = timeline_steps(ctx, [lambda s=s: [matmul_call(ctx, copies[(s * per_graph + i) % len(copies)], a, y, m)
+                                                    for i in range(per_graph)] for s in range(steps)],
+                                 [(f"{name} M={m}", nbits_bytes(k, n, m, bs=128), 2 * m * k * n)] * per_graph)
+            parts.append((f"prefill {name}, M={m}", timeline_summary(res)))
+            a.free()
+            y.free()
+        for w in copies:
+            w.free()
+    return parts
+
+
+def timeline_moe(ctx, sets=3, steps=6):
+    """The QMoE layer of moe_ffn, one call per step over `sets` rotating copies of its experts:
+    the grouped expert products (fc1 and fc3 with the SwiGLU in one launch, then fc2)."""
+    import ctypes
+
+    from transmuter_amd._lib import F16, F32, lib
+    from transmuter_amd.moe import ExpertWeight
+
+    rng = np.random.default_rng(6)
+    experts, k, hidden, inter, tokens = 128, 8, 2048, 768, 512
+
+    def expert_weight(n, kk):
+        packed = rng.integers(0, 256, (experts, n, kk // 2), dtype=np.uint8)
+        scales = (np.abs(rng.standard_normal((experts, n, kk // 32), dtype=np.float32)) * 0.01 + 1e-4).astype(np.float16)
+        return ExpertWeight.upload(ctx, packed, scales, None, bits=4, block_size=32, dtype="f16")
+
+    def device_copy(w):
+        handle = ctypes.c_void_p()
+        ctx.check(lib().tmh_weight_concat_nbits(ctx.handle, (ctypes.c_void_p * 1)(w.handle.value), 1,
+                                                ctypes.byref(handle)))
+        return ExpertWeight(ctx, handle, w.experts, w.n, w.k, w.bits, w.dtype)
+
+    first = (expert_weight(inter, hidden), expert_weight(inter, hidden), expert_weight(hidden, inter))
+    layers = [first] + [tuple(device_copy(w) for w in first) for _ in range(sets - 1)]
+    x = ctx.put(rng.standard_normal((tokens, hidden), dtype=np.float32).astype(np.float16))
+    router = ctx.put(rng.standard_normal((tokens, experts), dtype=np.float32))
+    y = ctx.empty((tokens, hidden), "f16")
+
+    def call(i):
+        fc1, fc3, fc2 = layers[i % len(layers)]
+        ctx.check(lib().tmh_qmoe(ctx.handle, x.ptr, F16, tokens, hidden, router.ptr, F32, experts, k, fc1.handle, None,
+                                 fc2.handle, None, fc3.handle, None, F16, 4, 0, 1.0, 0.0, 0.0, y.ptr, None))
+
+    call(0)  # sizes the workspace before capture
+    ctx.synchronize()
+    wb = experts * hidden * inter * (0.5 + 2 / 32)  # one projection's expert weights and scales
+    rows = tokens * k
+    calls = [("fc1 + fc3 (SwiGLU)", 2 * wb + tokens * hidden * 2 + rows * inter * 2, 2 * 2 * rows * hidden * inter),
+             ("fc2", wb + rows * inter * 2 + rows * hidden * 2, 2 * rows * hidden * inter)]
+    res = timeline_steps(ctx, [lambda s=s: call(s) for s in range(steps)], calls)
+    for layer in layers:
+        for w in layer:
+            w.free()
+    return [("QMoE 128 experts, top-8, 2048/768, 512 tokens", timeline_summary(res))]
+
+
+TIMELINE_NOTES = [
+    "In-kernel times come from the stamping build of each kernel (transmuter_amd.timeline): every",
+    "wavefront writes the 100 MHz real-time counter at its start and, after its memory accesses have",
+    "completed, at its end; a launch's time is its first wavefront's start to its last one's end, read",
+    "from the same HIP graph replays that are timed with events (the stamping graphs replay once each,",
+    "back to back, after a warm-up of the plain graphs). 'start to next start' is the time from a",
+    "launch's first wavefront to the next launch's first wavefront inside the replay. The shader clock",
+    "is the cycle counter over the real-time counter across the launch's wavefronts. Rates count",
+    "algorithmic bytes and FLOPs.",
+]
+
+
 # ---------------------------------------------------------------- main
 
 
@@ -851,6 +1149,10 @@ def main():
                    help="time the vendor library's dense int8 and f16 GEMMs (torch) at the bench's shapes and exit")
     p.add_argument("--summarize", nargs="*", metavar="PATH",
                    help="print a markdown summary of rocprofv3 output: a kernel_stats.csv, then --pmc directories")
+    p.add_argument("--timeline", choices=["decode", "vocab", "prefill", "moe"],
+                   help="time a workload's kernels inside its graph replays (stamping builds) and write markdown")
+    p.add_argument("--out", help="file the --timeline markdown goes to (default: gpurun_out/timeline_KIND.md)")
+    p.add_argument("--no-timeline", action="store_true", help="skip the in-graph kernel times of the headline")
     args = p.parse_args()
     if args.traffic:
         write_traffic(*args.traffic)
@@ -884,6 +1186,22 @@ def main():
         profile_run(ctx, args.profile, args.steps, args.profile_m)
         ctx.close()
         return
+    if args.timeline:
+        parts = {"decode": lambda: timeline_decode(ctx, sets=args.sets), "vocab": lambda: timeline_vocab(ctx),
+                 "prefill": lambda: timeline_prefill(ctx), "moe": lambda: timeline_moe(ctx)}[args.timeline]()
+        title = {"decode": "Qwen3-0.6B q4 decode step (M=1) and its floors, timed inside the graph replays",
+                 "vocab": "151936 x 1024 lm_head and vocabulary gather, timed inside the graph replays",
+                 "prefill": "SmolLM3-3B q4 prefill projections, timed inside the graph replays",
+                 "moe": "Qwen3-30B-A3B QMoE layer (512 tokens), timed inside the graph replays"}[args.timeline]
+        out = args.out or os.path.join(ROOT, "gpurun_out", f"timeline_{args.timeline}.md")
+        os.makedirs(os.path.dirname(out), exist_ok=True)
+        with open(out, "w") as f:
+            f.write(timeline_markdown(title, f"python bench.py --timeline {args.timeline}", parts, TIMELINE_NOTES))
+        log(f"wrote {out}")
+        ctx.close()
+        return
+    global STAMP_HEADLINE
+    STAMP_HEADLINE = not args.no_timeline
     parts = {"decode", "single", "prefill", "vocab", "moe", "int8", "cpu"} if args.sections == "all" \
         else set(args.sections.split(","))
     if args.quick:
@@ -914,6 +1232,21 @@ def main():
     if head.get("read_floor_us"):
         # The GEMV's launch time against a launch that only reads the same packed weights.
         roofline["read_floor_over_launch"] = head["read_floor_us"] / head["us_per_launch"]
+    if head.get("timeline"):
+        # The same kernel inside the replays (launch timeline): first wavefront's start to last
+        # one's end, averaged over its launches; achieved_in_kernel counts the same bytes over it.
+        tls = head["timeline"]
+        gemv = [k for k in tls["kernels"] if k["kernel"] in ("k_gemv_dot", "k_gemv_dec")]
+        n = sum(k["per_step"] for k in gemv)
+        kernel_us = sum(k["kernel_us"] * k["per_step"] for k in gemv) / n
+        roofline.update({
+            "kernel_us_in_graph": kernel_us,
+            "start_to_next_start_us_in_graph": sum(k["to_next_us"] * k["per_step"] for k in gemv) / n,
+            "achieved_in_kernel": head["bytes_per_launch"] / (kernel_us * 1e-6) / 1e9,
+            "shader_ghz": sum((k["ghz"] or 0) * k["per_step"] for k in gemv) / n,
+            "stamped_ms_per_step": tls["ms_per_step_stamped"],
+            "kernel_us_per_step_in_graph": tls["kernel_us_per_step"],
+        })
     cpu = None if args.no_cpu or "cpu" not in parts else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": "MatMulNBits q4: GB/s @M=1 and TFLOP/s @M=2048, % of MI355X roofline",

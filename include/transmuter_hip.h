@@ -378,6 +378,47 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
 int tmh_floor_empty(tmh_ctx* ctx, int workgroups, void* stream);
 int tmh_floor_read(tmh_ctx* ctx, const tmh_weight* w, void* d_sink, void* stream);
 
+/*
+ * More floors (no reference counterpart). tmh_floor_read_all reads every byte the weight holds on
+ * the device once (its packed weights, scales and zero points), 16 bytes per lane: the cost of a
+ * kernel that only reads what a GEMV over it reads. tmh_floor_write writes `bytes` (a multiple of
+ * 16, below 4 GiB) of zeros to d_dst with the vocabulary gather's store pattern (16-byte
+ * non-temporal stores, 4 KiB per wavefront): the cost of a gather's output alone. Asynchronous.
+ */
+int tmh_floor_read_all(tmh_ctx* ctx, const tmh_weight* w, void* d_sink, void* stream);
+int tmh_floor_write(tmh_ctx* ctx, void* d_dst, size_t bytes, void* stream);
+
+/*
+ * Launch timeline (measurement; no reference counterpart). Between tmh_timeline_begin and
+ * tmh_timeline_end, the calls of `ctx` launch a stamping build of their main kernels (the kernel
+ * ids below): every wavefront writes the low 32 bits of the GPU's 100 MHz real-time counter at its
+ * start and, once its memory accesses have completed, at its end, then the low 32 bits of the
+ * shader cycle counter at the same two points, as four u32 into its own 16-byte slot of d_slots
+ * (16-byte aligned, `capacity` slots; wavefront w of a launch in its slot first + w, w counting
+ * workgroups in linear order times their wavefronts), launch after launch in the order the calls
+ * are made. The stamping builds compute what the ordinary ones do. A launch captured into a graph
+ * keeps its slots, so each replay of the graph writes them again; the first wavefront's start to
+ * the last one's end is the kernel's time on the GPU inside the replay. Launches beyond the
+ * capacity run the ordinary build and are counted as dropped. tmh_timeline_end stops recording and
+ * copies the log: for each launch its kernel id, first slot and wavefronts (three int64 each) into
+ * h_log (at most max_launches launches), the launch count into *launches and the dropped count
+ * into *dropped.
+ */
+enum {
+  TMH_TL_GEMV_DOT = 1,      /* k_gemv_dot: decode GEMV for one row of A */
+  TMH_TL_GEMV_DEC = 2,      /* k_gemv_dec: decode GEMV, MFMA, M <= 16 */
+  TMH_TL_GEMM_LDS = 3,      /* k_gemm_lds: prefill GEMM */
+  TMH_TL_SPLITK_REDUCE = 4, /* k_splitk_reduce: the prefill GEMM's split-K sum */
+  TMH_TL_MOE_GEMM = 5,      /* k_moe_gemm_f16: QMoE grouped expert product */
+  TMH_TL_FLOOR_EMPTY = 6,   /* k_floor_empty */
+  TMH_TL_FLOOR_READ = 7,    /* k_floor_read */
+  TMH_TL_GATHER_ROWS = 8,   /* k_gather_bq_rows: GatherBlockQuantized of whole rows */
+  TMH_TL_FLOOR_READ_ALL = 9, /* k_floor_read_all */
+  TMH_TL_FLOOR_WRITE = 10   /* k_floor_write */
+};
+int tmh_timeline_begin(tmh_ctx* ctx, void* d_slots, int64_t capacity);
+int tmh_timeline_end(tmh_ctx* ctx, int64_t* h_log, int64_t max_launches, int64_t* launches, int64_t* dropped);
+
 #ifdef __cplusplus
 }
 #endif

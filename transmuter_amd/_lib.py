@@ -24,6 +24,10 @@ ZP_NONE, ZP_PACKED, ZP_FLOAT = 0, 1, 2
 QPARAM_TENSOR, QPARAM_AXIS, QPARAM_BLOCKED = 0, 1, 2
 # QMoE activation_type
 ACTIVATIONS = {"relu": 0, "gelu": 1, "silu": 2, "identity": 3, "swiglu": 4}
+# Kernel ids of the launch timeline (TMH_TL_*)
+TIMELINE_KERNELS = {1: "k_gemv_dot", 2: "k_gemv_dec", 3: "k_gemm_lds", 4: "k_splitk_reduce", 5: "k_moe_gemm_f16",
+                    6: "k_floor_empty", 7: "k_floor_read", 8: "k_gather_bq_rows", 9: "k_floor_read_all",
+                    10: "k_floor_write"}
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -80,6 +84,10 @@ SIGNATURES = {
     "tmh_upload_file": (_i, [_vp, _vp, ctypes.c_char_p, _i64, _sz]),
     "tmh_floor_empty": (_i, [_vp, _i, _vp]),
     "tmh_floor_read": (_i, [_vp, _vp, _vp, _vp]),
+    "tmh_floor_read_all": (_i, [_vp, _vp, _vp, _vp]),
+    "tmh_floor_write": (_i, [_vp, _vp, _sz, _vp]),
+    "tmh_timeline_begin": (_i, [_vp, _vp, _i64]),
+    "tmh_timeline_end": (_i, [_vp, ctypes.POINTER(_i64), _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "tmh_weight_upload_qmoe": (_i, [_vp, _vp, _sz, _vp, _i, _sz, _vp, _sz, _i64, _i64, _i64, _i, _i64, _i,
                                     ctypes.POINTER(_vp)]),
     "tmh_qmoe": (_i, [_vp, _vp, _i, _i64, _i64, _vp, _i, _i64, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,

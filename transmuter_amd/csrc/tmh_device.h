@@ -208,4 +208,28 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* 
 #endif
 }
 
+// Timeline stamps of the measurement builds of a kernel (tmh_timeline_begin): the low 32 bits of
+// the GPU's constant 100 MHz real-time counter and of the shader clock's cycle counter.
+struct TlStart {
+  uint32_t real, cycles;
+};
+
+__device__ __forceinline__ TlStart tl_clock() {
+  return TlStart{static_cast<uint32_t>(__builtin_amdgcn_s_memrealtime()),
+                 static_cast<uint32_t>(__builtin_amdgcn_s_memtime())};
+}
+
+// Writes this wavefront's stamps into its 16-byte slot (linear workgroup * wavefronts per
+// workgroup + wavefront) of the launch's slots: real-time start and end, cycle counter start
+// and end. The end is read once every memory access the wavefront issued has completed. Lane 0
+// must call it (it stores); other lanes may.
+__device__ __forceinline__ void tl_stamp(uint32_t* tl, TlStart t0) {
+  __builtin_amdgcn_s_waitcnt(0);
+  const TlStart t1 = tl_clock();
+  const uint32_t block = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const uint32_t wave = block * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if ((threadIdx.x & 63) == 0)
+    *reinterpret_cast<uint4*>(tl + 4 * static_cast<size_t>(wave)) = make_uint4(t0.real, t1.real, t0.cycles, t1.cycles);
+}
+
 }  // namespace tmh

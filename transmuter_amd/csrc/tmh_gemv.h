@@ -36,11 +36,13 @@ namespace tmh {
 // row and chunk, log2 of the weights one parameter entry covers, and (nch * CW - K) / 4, the
 // values of the last chunks past K. K travels in shape rather than as an argument of its own:
 // one more argument made a launch 0.09-0.17 us slower.
-template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS>
-__global__ __launch_bounds__(64 * NW) void k_gemv_dec(
+// (The body; k_gemv_dec and its stamping build k_gemv_dec_tl below are the kernels.)
+template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS, bool TL>
+__device__ __forceinline__ void gemv_dec(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
-    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, uint32_t* __restrict__ tl) {
+  const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
   constexpr int CW = 512 / BITS;   // weights per chunk row
   constexpr int GW = CW / 4;       // weights per lane per chunk
   constexpr int STEPS = GW / 8;    // MFMA steps per chunk
@@ -186,6 +188,23 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
       for (uint32_t e = 0; e < 4 && n + e < N; ++e) dst[e] = static_cast<_Float16>(v[e]);
     }
   }
+  if constexpr (TL) tl_stamp(tl, tl0);  // lane 0 (row 0) always gets here
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS>
+__global__ __launch_bounds__(64 * NW) void k_gemv_dec(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
+  gemv_dec<BITS, HAS_ZP, SPLIT, U, NW, TN, ALDS, false>(qt, sc, zp, A, nch, ntiles, lda, shape, Y, ldy, N, nullptr);
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS>
+__global__ __launch_bounds__(64 * NW) void k_gemv_dec_tl(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, uint32_t* __restrict__ tl) {
+  gemv_dec<BITS, HAS_ZP, SPLIT, U, NW, TN, ALDS, true>(qt, sc, zp, A, nch, ntiles, lda, shape, Y, ldy, N, tl);
 }
 
 // The decode GEMV for one row of A (M = 1), 4- or 8-bit weights whose parameters are constant
@@ -204,11 +223,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
 // that rounding and by f32 summation order.
 // The four lanes of a row and the wavefronts of the workgroup add through LDS in a fixed order.
 // Chunk rounds, launch shapes and buffer addressing are those of k_gemv_dec.
-template <int BITS, bool HAS_ZP, int U, int NW, int TN>
-__global__ __launch_bounds__(64 * NW) void k_gemv_dot(
+// (The body; k_gemv_dot and its stamping build k_gemv_dot_tl below are the kernels.)
+template <int BITS, bool HAS_ZP, int U, int NW, int TN, bool TL>
+__device__ __forceinline__ void gemv_dot(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
-    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, uint32_t* __restrict__ tl) {
+  const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
   static_assert(BITS == 4 || BITS == 8, "4- or 8-bit weights");
   constexpr int CW = 512 / BITS;  // weights per chunk row
   constexpr int GW = CW / 4;      // weights per lane per chunk
@@ -327,6 +348,23 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dot(
     const uint32_t n = (t0 + tn) * 16 + r;
     if (n < N) Y[n] = static_cast<_Float16>(v);
   }
+  if constexpr (TL) tl_stamp(tl, tl0);
+}
+
+template <int BITS, bool HAS_ZP, int U, int NW, int TN>
+__global__ __launch_bounds__(64 * NW) void k_gemv_dot(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
+  gemv_dot<BITS, HAS_ZP, U, NW, TN, false>(qt, sc, zp, A, nch, ntiles, lda, shape, Y, ldy, N, nullptr);
+}
+
+template <int BITS, bool HAS_ZP, int U, int NW, int TN>
+__global__ __launch_bounds__(64 * NW) void k_gemv_dot_tl(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, uint32_t* __restrict__ tl) {
+  gemv_dot<BITS, HAS_ZP, U, NW, TN, true>(qt, sc, zp, A, nch, ntiles, lda, shape, Y, ldy, N, tl);
 }
 
 // The same GEMV over f32 A and f32 weights (the reference's CPU configuration after move/2: f32

@@ -57,6 +57,11 @@ void go(const DecArgs& d, hipStream_t s) {
   constexpr bool A_LDS = ALDS && static_cast<size_t>(NW) * U * 16 * rb * 16 <= kStaticLds;
   static_assert(red <= kStaticLds, "partial sums exceed the static LDS");
   const unsigned grid = (d.ntiles + TN - 1) / TN;
+  if (uint32_t* tl = timeline_slots(TMH_TL_GEMV_DEC, static_cast<int64_t>(grid) * NW)) {
+    k_gemv_dec_tl<BITS, HAS_ZP, SPLIT, U, NW, TN, A_LDS><<<grid, 64 * NW, 0, s>>>(
+        d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles, d.lda, d.shape, d.y, d.ldy, d.n, tl);
+    return;
+  }
   k_gemv_dec<BITS, HAS_ZP, SPLIT, U, NW, TN, A_LDS><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles,
                                                                               d.lda, d.shape, d.y, d.ldy, d.n);
 }
@@ -93,6 +98,11 @@ void streaming(const DecArgs& d, int nw, hipStream_t s) {
 template <int BITS, bool HAS_ZP, int NW, int TN, int U>
 void go_dot(const DecArgs& d, hipStream_t s) {
   const unsigned grid = (d.ntiles + TN - 1) / TN;
+  if (uint32_t* tl = timeline_slots(TMH_TL_GEMV_DOT, static_cast<int64_t>(grid) * NW)) {
+    k_gemv_dot_tl<BITS, HAS_ZP, U, NW, TN><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles, d.lda,
+                                                                     d.shape, d.y, d.ldy, d.n, tl);
+    return;
+  }
   k_gemv_dot<BITS, HAS_ZP, U, NW, TN><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles, d.lda, d.shape,
                                                                 d.y, d.ldy, d.n);
 }

@@ -10,6 +10,16 @@
 
 #include "../../include/transmuter_hip.h"
 
+// Launch timeline of a context (measurement only, tmh_timeline_begin): the instrumented kernels
+// write, per wavefront, the low 32 bits of the GPU's 100 MHz real-time counter and of its shader
+// cycle counter at the wavefront's start and end into consecutive four-word slots of a caller's
+// device buffer, and each launch is logged with its kernel and its first slot.
+struct tmh_timeline_state {
+  uint32_t* d_slots = nullptr;  // 4 words per wavefront
+  int64_t capacity = 0, used = 0, dropped = 0;
+  std::vector<int64_t> log;  // kernel id, first slot, wavefronts: three per launch
+};
+
 struct tmh_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -20,6 +30,7 @@ struct tmh_ctx {
   // Workspaces replaced by a larger one. A graph captured earlier keeps their addresses in its
   // kernel arguments, so they stay allocated until the context is destroyed.
   std::vector<void*> ws_retired;
+  tmh_timeline_state* tl = nullptr;  // while a timeline is recorded
 };
 
 // Tiled device layout of a MatMulNBits weight.
@@ -106,6 +117,22 @@ void launch_decode_gemv_f32(const tmh_weight* w, const void* a, int64_t M, int64
 // Looks up, once per device and with that device current, the device address of the scratch
 // memory tmh_matmul_nbits_noalloc uses (a failure is reported by that call).
 void noalloc_scratch_init(int device);
+
+// Timeline recording. An entry point that launches instrumented kernels holds a TimelineScope
+// for its context; a launcher asks timeline_slots for the slots of a launch of `waves`
+// wavefronts and launches the stamping build of its kernel when it gets some (nullptr: no
+// timeline is on, or its slots ran out and the launch goes unrecorded).
+uint32_t* timeline_slots(int kernel, int64_t waves);
+class TimelineScope {
+ public:
+  explicit TimelineScope(tmh_ctx* ctx);
+  ~TimelineScope();
+  TimelineScope(const TimelineScope&) = delete;
+  TimelineScope& operator=(const TimelineScope&) = delete;
+
+ private:
+  tmh_timeline_state* prev_;
+};
 
 }  // namespace tmh
 

@@ -227,15 +227,17 @@ enum : int { EPI_STORE = 0, EPI_ACT = 1, EPI_GLU = 2 };
 // wavefronts owns one 16-column output tile (and, for EPI_GLU, the matching tile of the second
 // weight) over all of K; the item's A rows pass through LDS one chunk at a time, double
 // buffered, with the next chunk's weights in flight.
-template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT>
-__global__ __launch_bounds__(512) void k_moe_gemm_f16(
+// (The body; k_moe_gemm_f16 and its stamping build k_moe_gemm_f16_tl below are the kernels.)
+template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT, bool TL>
+__device__ __forceinline__ void moe_gemm_f16(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const uint4_t* __restrict__ qt2, const uint16_t* __restrict__ sc2, const uint8_t* __restrict__ zp2,
     int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles,
     const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
     const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
     const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
-    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo) {
+    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo, uint32_t* __restrict__ tl) {
+  const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
   constexpr int CW = 512 / BITS;
   constexpr int GW = CW / 4;
   constexpr int STEPS = GW / 8;
@@ -247,7 +249,10 @@ __global__ __launch_bounds__(512) void k_moe_gemm_f16(
   constexpr int LOADS = (PIECES + 511) / 512;    // per thread
   constexpr int NW = EPI == EPI_GLU ? 2 : 1;
   __shared__ __align__(16) uint8_t lds[2 * ROWS * ROWB];
-  if (static_cast<int>(blockIdx.y) >= *n_items) return;
+  if (static_cast<int>(blockIdx.y) >= *n_items) {
+    if constexpr (TL) tl_stamp(tl, tl0);
+    return;
+  }
   const MoeItem it = moe_item(items, blockIdx.y, offsets, counts, ROWS);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
@@ -362,7 +367,10 @@ __global__ __launch_bounds__(512) void k_moe_gemm_f16(
   } else {
     run(std::integral_constant<int, 1>{});
   }
-  if (!active) return;
+  if (!active) {
+    if constexpr (TL) tl_stamp(tl, tl0);
+    return;
+  }
   // Lane (16g + r) holds rows mt*16 + r and columns lt*16 + 4g .. +3.
   const int n = lt * 16 + 4 * g;
 #pragma unroll
@@ -388,6 +396,35 @@ __global__ __launch_bounds__(512) void k_moe_gemm_f16(
     _Float16* dst = out + static_cast<int64_t>(it.row0 + i) * ldo + n;
     *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
   }
+  if constexpr (TL) tl_stamp(tl, tl0);
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT>
+__global__ __launch_bounds__(512) void k_moe_gemm_f16(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const uint4_t* __restrict__ qt2, const uint16_t* __restrict__ sc2, const uint8_t* __restrict__ zp2,
+    int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles,
+    const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
+    const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
+    const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
+    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo) {
+  moe_gemm_f16<BITS, HAS_ZP, SPLIT, EPI, MT, false>(
+      qt, sc, zp, qt2, sc2, zp2, tile_off2, ntiles, nchunks, nbc, bsc_shift, tiles_per_expert, out_tiles, A, a_rows, lda, perm,
+      perm_div, items, n_items, offsets, counts, bias1, bias2, bias_dt, bias_ld, act, alpha, beta, limit, out, ldo, nullptr);
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT>
+__global__ __launch_bounds__(512) void k_moe_gemm_f16_tl(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const uint4_t* __restrict__ qt2, const uint16_t* __restrict__ sc2, const uint8_t* __restrict__ zp2,
+    int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles,
+    const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
+    const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
+    const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
+    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo, uint32_t* __restrict__ tl) {
+  moe_gemm_f16<BITS, HAS_ZP, SPLIT, EPI, MT, true>(
+      qt, sc, zp, qt2, sc2, zp2, tile_off2, ntiles, nchunks, nbc, bsc_shift, tiles_per_expert, out_tiles, A, a_rows, lda, perm,
+      perm_div, items, n_items, offsets, counts, bias1, bias2, bias_dt, bias_ld, act, alpha, beta, limit, out, ldo, tl);
 }
 
 // The same product for any float types (A in a_dt, weights dequantized in WDT, out in out_dt):
@@ -570,13 +607,18 @@ void launch_moe_f16_e(const tmh_weight* w, int tpe, const void* A, int a_rows, i
                       void* out, int ldo, const MoeEpilogue& ep, hipStream_t s) {
   const tmh_weight* w2 = ep.w2 ? ep.w2 : w;
   const dim3 grid(static_cast<unsigned>((ep.out_tiles + 7) / 8), static_cast<unsigned>(max_items));
-  k_moe_gemm_f16<BITS, HAS_ZP, SPLIT, EPI, MT><<<grid, 512, 0, s>>>(
-      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
-      static_cast<const uint8_t*>(w->d_zero), reinterpret_cast<const uint4_t*>(w2->d_q),
-      static_cast<const uint16_t*>(w2->d_scale), static_cast<const uint8_t*>(w2->d_zero), ep.tile_off2,
-      static_cast<int>(w->ntiles), static_cast<int>(w->nchunks), w->nbc, bsc_shift_moe(w), tpe, ep.out_tiles,
-      static_cast<const _Float16*>(A), a_rows, lda, perm, perm_div, items, n_items, offsets, counts, ep.bias1, ep.bias2,
-      ep.bias_dt, ep.bias_ld, ep.act, ep.alpha, ep.beta, ep.limit, static_cast<_Float16*>(out), ldo);
+#define TMH_MOE_ARGS                                                                                                   \
+  reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),                                 \
+      static_cast<const uint8_t*>(w->d_zero), reinterpret_cast<const uint4_t*>(w2->d_q),                              \
+      static_cast<const uint16_t*>(w2->d_scale), static_cast<const uint8_t*>(w2->d_zero), ep.tile_off2,               \
+      static_cast<int>(w->ntiles), static_cast<int>(w->nchunks), w->nbc, bsc_shift_moe(w), tpe, ep.out_tiles,         \
+      static_cast<const _Float16*>(A), a_rows, lda, perm, perm_div, items, n_items, offsets, counts, ep.bias1,        \
+      ep.bias2, ep.bias_dt, ep.bias_ld, ep.act, ep.alpha, ep.beta, ep.limit, static_cast<_Float16*>(out), ldo
+  if (uint32_t* tl = timeline_slots(TMH_TL_MOE_GEMM, static_cast<int64_t>(grid.x) * grid.y * 8))
+    k_moe_gemm_f16_tl<BITS, HAS_ZP, SPLIT, EPI, MT><<<grid, 512, 0, s>>>(TMH_MOE_ARGS, tl);
+  else
+    k_moe_gemm_f16<BITS, HAS_ZP, SPLIT, EPI, MT><<<grid, 512, 0, s>>>(TMH_MOE_ARGS);
+#undef TMH_MOE_ARGS
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
@@ -763,6 +805,7 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
              int64_t E, int k, const tmh_weight* fc1, const void* d_fc1_bias, const tmh_weight* fc2,
              const void* d_fc2_bias, const tmh_weight* fc3, const void* d_fc3_bias, int bias_dtype, int activation,
              int swiglu_fusion, float alpha, float beta, float limit, void* d_y, void* stream) {
+  TimelineScope timeline(ctx);
   // The sizes are checked before the device is touched (a context-free caller gets the same errors).
   if (!is_float_dtype(x_dtype) || !is_float_dtype(router_dtype))
     return fail(ctx, TMH_ERR_INVALID, "QMoE input and router must be float tensors");

@@ -401,13 +401,15 @@ __device__ __noinline__ void store_quad_any(float4_t v, void* Y, int y_dt, int d
   }
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS>
-__global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
+// (The body; k_gemm_lds and its stamping build k_gemm_lds_tl below are the kernels.)
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS, bool TL>
+__device__ __forceinline__ void gemm_lds(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
     int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
     int64_t nchunks, int nbc, int bsc_shift, int mblocks, int nblocks, int chunks_per_split,
-    float* __restrict__ ws) {
+    float* __restrict__ ws, uint32_t* __restrict__ tl) {
+  const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
   constexpr int CW = 512 / BITS;
   constexpr int GW = CW / 4;
   constexpr int STEPS = GW / 8;
@@ -726,9 +728,13 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
       out_tile(std::integral_constant<int, 4>{});
     else
       out_tile(std::integral_constant<int, 2>{});
+    if constexpr (TL) tl_stamp(tl, tl0);
     return;
   }
-  if (KS == 2 && kh == 1) return;
+  if (KS == 2 && kh == 1) {
+    if constexpr (TL) tl_stamp(tl, tl0);
+    return;
+  }
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt) {
     const int64_t m = m0 + wm * 128 + mt * 16 + r;
@@ -757,13 +763,65 @@ __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
       store_quad_any(v, Y, y_dt, dot_dt, bias, bias_dt, m * ldy, n, N);
     }
   }
+  if constexpr (TL) tl_stamp(tl, tl0);
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS>
+__global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
+    int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
+    int64_t nchunks, int nbc, int bsc_shift, int mblocks, int nblocks, int chunks_per_split,
+    float* __restrict__ ws) {
+  gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS, false>(qt, sc, zp, A, M, K, lda, bias, bias_dt, Y, y_dt, dot_dt, ldy, N,
+                                                   ntiles, nchunks, nbc, bsc_shift, mblocks, nblocks, chunks_per_split,
+                                                   ws, nullptr);
+}
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS>
+__global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds_tl(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
+    int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
+    int64_t nchunks, int nbc, int bsc_shift, int mblocks, int nblocks, int chunks_per_split,
+    float* __restrict__ ws, uint32_t* __restrict__ tl) {
+  gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS, true>(qt, sc, zp, A, M, K, lda, bias, bias_dt, Y, y_dt, dot_dt, ldy, N,
+                                                  ntiles, nchunks, nbc, bsc_shift, mblocks, nblocks, chunks_per_split,
+                                                  ws, tl);
 }
 
 // Split-K epilogue: Y = sum over the splits of ws[split][M][N] (in split order), rounded to the
 // dot type, plus the bias, in Y's type. Four consecutive outputs per thread.
+__device__ __forceinline__ void splitk_reduce_quads(const float* __restrict__ ws, int splits, int64_t M, int64_t N,
+                                                    const void* __restrict__ bias, int bias_dt, void* __restrict__ Y,
+                                                    int y_dt, int dot_dt, int64_t ldy);
+
+template <bool TL>
+__device__ __forceinline__ void splitk_reduce(const float* __restrict__ ws, int splits, int64_t M, int64_t N,
+                                              const void* __restrict__ bias, int bias_dt, void* __restrict__ Y,
+                                              int y_dt, int dot_dt, int64_t ldy, uint32_t* __restrict__ tl) {
+  const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
+  splitk_reduce_quads(ws, splits, M, N, bias, bias_dt, Y, y_dt, dot_dt, ldy);
+  if constexpr (TL) tl_stamp(tl, tl0);
+}
+
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits, int64_t M, int64_t N,
                                                        const void* __restrict__ bias, int bias_dt, void* __restrict__ Y,
                                                        int y_dt, int dot_dt, int64_t ldy) {
+  splitk_reduce<false>(ws, splits, M, N, bias, bias_dt, Y, y_dt, dot_dt, ldy, nullptr);
+}
+
+__global__ __launch_bounds__(256) void k_splitk_reduce_tl(const float* __restrict__ ws, int splits, int64_t M, int64_t N,
+                                                          const void* __restrict__ bias, int bias_dt,
+                                                          void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy,
+                                                          uint32_t* __restrict__ tl) {
+  splitk_reduce<true>(ws, splits, M, N, bias, bias_dt, Y, y_dt, dot_dt, ldy, tl);
+}
+
+// One thread's four consecutive outputs (the body of k_splitk_reduce).
+__device__ __forceinline__ void splitk_reduce_quads(const float* __restrict__ ws, int splits, int64_t M, int64_t N,
+                                                    const void* __restrict__ bias, int bias_dt, void* __restrict__ Y,
+                                                    int y_dt, int dot_dt, int64_t ldy) {
   const int64_t i4 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   const int64_t total = M * N;
   if (i4 >= total) return;
@@ -1038,19 +1096,34 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
   // The entry point provides splitk_bytes() of partial sums whenever the plan splits K.
   float* ws = splits > 1 ? a.ws : nullptr;
   const dim3 grid(static_cast<unsigned>(tiles * splits));
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(gemm_lds_bytes<BITS, BM, KS>()));
+  constexpr int kLds = static_cast<int>(gemm_lds_bytes<BITS, BM, KS>());
+  static const hipError_t attr[2] = {
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kLds),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_lds_tl<BITS, HAS_ZP, SPLIT, WN, BM, KS>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kLds)};
   (void)attr;
-  k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS><<<grid, 128 * WN * KS, gemm_lds_bytes<BITS, BM, KS>(), s>>>(
-      reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
-      static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
-      a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
-      nblocks, cps, ws);
+  if (uint32_t* tl = timeline_slots(TMH_TL_GEMM_LDS, static_cast<int64_t>(grid.x) * 2 * WN * KS)) {
+    k_gemm_lds_tl<BITS, HAS_ZP, SPLIT, WN, BM, KS><<<grid, 128 * WN * KS, kLds, s>>>(
+        reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+        static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
+        a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
+        nblocks, cps, ws, tl);
+  } else {
+    k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS><<<grid, 128 * WN * KS, kLds, s>>>(
+        reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
+        static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
+        a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
+        nblocks, cps, ws);
+  }
   if (ws) {
     const int64_t quads = (a.M * w->N + 3) / 4;
-    k_splitk_reduce<<<static_cast<unsigned>((quads + 255) / 256), 256, 0, s>>>(
-        ws, splits, a.M, w->N, a.bias, a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy);
+    const unsigned rgrid = static_cast<unsigned>((quads + 255) / 256);
+    if (uint32_t* tl = timeline_slots(TMH_TL_SPLITK_REDUCE, static_cast<int64_t>(rgrid) * 4))
+      k_splitk_reduce_tl<<<rgrid, 256, 0, s>>>(ws, splits, a.M, w->N, a.bias, a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy,
+                                              tl);
+    else
+      k_splitk_reduce<<<rgrid, 256, 0, s>>>(ws, splits, a.M, w->N, a.bias, a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy);
   }
 }
 
@@ -1705,6 +1778,7 @@ extern "C" {
 int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
                      int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype,
                      int64_t ldy, void* stream) {
+  TimelineScope timeline(ctx);
   MatArgs a{};
   bool run = false;
   TMH_TRY(prepare_matmul(ctx, w, d_a, a_dtype, M, lda, d_bias, bias_dtype, d_y, y_dtype, ldy, &a, &run));
@@ -1728,6 +1802,7 @@ int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_d
 int tmh_matmul_nbits_noalloc(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dtype, int64_t M,
                              int64_t lda, const void* d_bias, int bias_dtype, void* d_y, int y_dtype, int64_t ldy,
                              void* stream) {
+  TimelineScope timeline(ctx);
   MatArgs a{};
   bool run = false;
   TMH_TRY(prepare_matmul(ctx, w, d_a, a_dtype, M, lda, d_bias, bias_dtype, d_y, y_dtype, ldy, &a, &run));

@@ -149,19 +149,24 @@ void launch_gather_ub(const uint8_t* data, bool sgn, int64_t rows, int64_t row_b
 // hardware drops: no branch, so no slice's loads wait behind another's stores. `spr_magic` is
 // floor(2^32 / slices_per_row) + 1 (slices_per_row > 1): umulhi(sl, spr_magic) equals
 // sl / slices_per_row for every sl < 2^32 / slices_per_row, which the launcher checks.
-template <int DT, int BITS, int S, bool IDS64, bool HAS_ZP>
-__global__ __launch_bounds__(256) void k_gather_bq_rows(
+// (The body; k_gather_bq_rows and its stamping build k_gather_bq_rows_tl below are the kernels.)
+template <int DT, int BITS, int S, bool IDS64, bool HAS_ZP, bool TL>
+__device__ __forceinline__ void gather_bq_rows(
     const uint8_t* __restrict__ data, bool data_signed, uint32_t rows, uint32_t row_bytes,
     const void* __restrict__ ids, uint32_t n_slices, uint32_t slices_per_row, uint32_t spr_magic,
     const void* __restrict__ scales, uint32_t blocks, uint32_t bs_shift, const uint8_t* __restrict__ zp,
-    bool zp_signed, uint32_t zrow, void* __restrict__ out) {
+    bool zp_signed, uint32_t zrow, void* __restrict__ out, uint32_t* __restrict__ tl) {
+  const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
   constexpr int PER = 8 / BITS;
   constexpr int V = 4 * PER;  // values per lane and slice
   constexpr int ES = DT == DT_F32 ? 4 : 2;
   const int lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
   const uint32_t s0 = wave * S;
-  if (s0 >= n_slices) return;
+  if (s0 >= n_slices) {
+    if constexpr (TL) tl_stamp(tl, tl0);
+    return;
+  }
   const uint32_t D = row_bytes * PER;
   const auto d_rsrc = buffer_rsrc(data, rows * row_bytes);
   const auto s_rsrc = buffer_rsrc(scales, rows * blocks * ES);
@@ -293,6 +298,28 @@ __global__ __launch_bounds__(256) void k_gather_bq_rows(
                                                o_rsrc, off + 16 * k, 0, kNonTemporal);
     }
   }
+  if constexpr (TL) tl_stamp(tl, tl0);
+}
+
+template <int DT, int BITS, int S, bool IDS64, bool HAS_ZP>
+__global__ __launch_bounds__(256) void k_gather_bq_rows(
+    const uint8_t* __restrict__ data, bool data_signed, uint32_t rows, uint32_t row_bytes,
+    const void* __restrict__ ids, uint32_t n_slices, uint32_t slices_per_row, uint32_t spr_magic,
+    const void* __restrict__ scales, uint32_t blocks, uint32_t bs_shift, const uint8_t* __restrict__ zp,
+    bool zp_signed, uint32_t zrow, void* __restrict__ out) {
+  gather_bq_rows<DT, BITS, S, IDS64, HAS_ZP, false>(data, data_signed, rows, row_bytes, ids, n_slices, slices_per_row,
+                                                    spr_magic, scales, blocks, bs_shift, zp, zp_signed, zrow, out,
+                                                    nullptr);
+}
+
+template <int DT, int BITS, int S, bool IDS64, bool HAS_ZP>
+__global__ __launch_bounds__(256) void k_gather_bq_rows_tl(
+    const uint8_t* __restrict__ data, bool data_signed, uint32_t rows, uint32_t row_bytes,
+    const void* __restrict__ ids, uint32_t n_slices, uint32_t slices_per_row, uint32_t spr_magic,
+    const void* __restrict__ scales, uint32_t blocks, uint32_t bs_shift, const uint8_t* __restrict__ zp,
+    bool zp_signed, uint32_t zrow, void* __restrict__ out, uint32_t* __restrict__ tl) {
+  gather_bq_rows<DT, BITS, S, IDS64, HAS_ZP, true>(data, data_signed, rows, row_bytes, ids, n_slices, slices_per_row,
+                                                   spr_magic, scales, blocks, bs_shift, zp, zp_signed, zrow, out, tl);
 }
 
 template <int DT, int BITS, bool IDS64, bool HAS_ZP>
@@ -305,10 +332,16 @@ void launch_gather_rows(const uint8_t* data, bool sgn, int64_t rows, int64_t row
   while ((int64_t(1) << shift) < bs) ++shift;
   const int64_t waves = (n_slices + S - 1) / S;
   const auto magic = static_cast<uint32_t>((uint64_t(1) << 32) / static_cast<uint64_t>(spr) + 1);
-  k_gather_bq_rows<DT, BITS, S, IDS64, HAS_ZP><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, s>>>(
-      data, sgn, static_cast<uint32_t>(rows), static_cast<uint32_t>(row_bytes), ids, static_cast<uint32_t>(n_slices),
-      static_cast<uint32_t>(spr), magic, scales, static_cast<uint32_t>(blocks), static_cast<uint32_t>(shift),
-      static_cast<const uint8_t*>(zp), zp_signed, static_cast<uint32_t>(zrow), out);
+  const unsigned grid = static_cast<unsigned>((waves + 3) / 4);
+#define TMH_GATHER_ARGS                                                                                               \
+  data, sgn, static_cast<uint32_t>(rows), static_cast<uint32_t>(row_bytes), ids, static_cast<uint32_t>(n_slices),    \
+      static_cast<uint32_t>(spr), magic, scales, static_cast<uint32_t>(blocks), static_cast<uint32_t>(shift),         \
+      static_cast<const uint8_t*>(zp), zp_signed, static_cast<uint32_t>(zrow), out
+  if (uint32_t* tl = timeline_slots(TMH_TL_GATHER_ROWS, static_cast<int64_t>(grid) * 4))
+    k_gather_bq_rows_tl<DT, BITS, S, IDS64, HAS_ZP><<<grid, 256, 0, s>>>(TMH_GATHER_ARGS, tl);
+  else
+    k_gather_bq_rows<DT, BITS, S, IDS64, HAS_ZP><<<grid, 256, 0, s>>>(TMH_GATHER_ARGS);
+#undef TMH_GATHER_ARGS
 }
 
 template <int DT, int BITS>
@@ -947,6 +980,7 @@ int tmh_gather_block_quantized(tmh_ctx* ctx, const void* d_data, int data_dtype,
                                const void* d_scales, int scales_dtype, int64_t blocks,
                                const void* d_zero_points, int zp_dtype, int bits, void* d_out,
                                void* stream) {
+  TimelineScope timeline(ctx);
   TMH_TRY(use_device(ctx));
   if (bits != 2 && bits != 4 && bits != 8)
     return fail(ctx, TMH_ERR_INVALID, "GatherBlockQuantized bits must be 2, 4 or 8, got %d", bits);

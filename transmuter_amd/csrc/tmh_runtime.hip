@@ -114,6 +114,27 @@ float load_float(const void* p, int dt, size_t i) {
   }
 }
 
+namespace {
+thread_local tmh_timeline_state* t_timeline = nullptr;
+}  // namespace
+
+TimelineScope::TimelineScope(tmh_ctx* ctx) : prev_(t_timeline) { t_timeline = ctx ? ctx->tl : nullptr; }
+
+TimelineScope::~TimelineScope() { t_timeline = prev_; }
+
+uint32_t* timeline_slots(int kernel, int64_t waves) {
+  tmh_timeline_state* tl = t_timeline;
+  if (!tl) return nullptr;
+  if (waves <= 0 || tl->used + waves > tl->capacity) {
+    ++tl->dropped;
+    return nullptr;
+  }
+  uint32_t* slots = tl->d_slots + 4 * tl->used;
+  tl->log.insert(tl->log.end(), {static_cast<int64_t>(kernel), tl->used, waves});
+  tl->used += waves;
+  return slots;
+}
+
 }  // namespace tmh
 
 using namespace tmh;
@@ -173,6 +194,7 @@ void tmh_ctx_destroy(tmh_ctx* ctx) {
   }
   if (ctx->ws) (void)hipFree(ctx->ws);
   for (void* p : ctx->ws_retired) (void)hipFree(p);
+  delete ctx->tl;
   delete ctx;
 }
 
@@ -364,6 +386,32 @@ int tmh_graph_destroy(tmh_ctx* ctx, void* graph_exec) {
   TMH_TRY(use_device(ctx));
   if (!graph_exec) return TMH_OK;
   return check_hip(ctx, hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+}
+
+int tmh_timeline_begin(tmh_ctx* ctx, void* d_slots, int64_t capacity) {
+  TMH_TRY(use_device(ctx));
+  if (!d_slots || capacity < 1) return fail(ctx, TMH_ERR_INVALID, "tmh_timeline_begin: no slots");
+  if (reinterpret_cast<uintptr_t>(d_slots) % 16 != 0)
+    return fail(ctx, TMH_ERR_INVALID, "tmh_timeline_begin: the slots must be 16-byte aligned");
+  if (capacity > (int64_t(1) << 31)) return fail(ctx, TMH_ERR_INVALID, "tmh_timeline_begin: too many slots");
+  delete ctx->tl;
+  ctx->tl = new tmh_timeline_state();
+  ctx->tl->d_slots = static_cast<uint32_t*>(d_slots);
+  ctx->tl->capacity = capacity;
+  return TMH_OK;
+}
+
+int tmh_timeline_end(tmh_ctx* ctx, int64_t* h_log, int64_t max_launches, int64_t* launches, int64_t* dropped) {
+  if (!ctx) return fail(nullptr, TMH_ERR_INVALID, "the context is NULL");
+  if (!ctx->tl) return fail(ctx, TMH_ERR_INVALID, "tmh_timeline_end: no timeline is being recorded");
+  const int64_t n = static_cast<int64_t>(ctx->tl->log.size() / 3);
+  const int64_t copy = std::max<int64_t>(0, std::min(n, max_launches));
+  if (h_log && copy) std::memcpy(h_log, ctx->tl->log.data(), static_cast<size_t>(copy) * 3 * sizeof(int64_t));
+  if (launches) *launches = n;
+  if (dropped) *dropped = ctx->tl->dropped;
+  delete ctx->tl;
+  ctx->tl = nullptr;
+  return TMH_OK;
 }
 
 }  // extern "C"
