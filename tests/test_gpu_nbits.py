@@ -155,6 +155,25 @@ MATMUL_CASES = [
     # whole-GPU 256x256 grid over 4-bit weights
     (8, 32, "packed", 2048, 8192, [300], "f16", "f16", None),
     (4, 128, "packed", 4096, 8192, [2011], "f16", "f16", "f16"),
+    # the bf16 prefill path (bf16 A and weights): K splits, a bias, 8-bit, K off a chunk
+    (4, 128, "packed", 2048, 1000, [65, 260], "bf16", "bf16", "bf16"),
+    (8, 64, "none", 1024, 520, [100, 300], "bf16", "bf16", None),
+    (4, 32, "packed", 200, 40, [70], "bf16", "bf16", None),
+    (2, 64, "packed", 512, 96, [100], "bf16", "bf16", None),
+    # the split path (A and weights as bf16 hi + lo, three MFMAs): f32 A and weights, mixed types,
+    # float zero points, 2- and 8-bit, K off a chunk, ragged M and N
+    (4, 128, "packed", 2048, 2048, [256, 300], "f32", "f32", None),
+    (4, 32, "none", 200, 40, [70, 129], "f32", "f32", "f32"),
+    (4, 32, "float", 1024, 520, [100, 300], "f16", "f16", None),
+    (4, 32, "packed", 1024, 96, [130], "f32", "f16", None),
+    (4, 32, "packed", 1024, 96, [130], "bf16", "f32", None),
+    (4, 32, "packed", 1024, 96, [130], "f16", "bf16", "f16"),
+    (8, 32, "float", 512, 48, [66], "bf16", "bf16", None),
+    (8, 128, "packed", 1024, 200, [300], "f32", "f32", None),
+    (2, 64, "none", 512, 96, [100], "f32", "f32", None),
+    # 2-bit weights on the LDS-tiled f16 GEMM (64- and 128-row tiles; 512-byte rows of A)
+    (2, 32, "packed", 1024, 200, [80, 300], "f16", "f16", None),
+    (2, 64, "none", 512, 96, [100, 257], "f16", "f16", "f16"),
 ]
 
 
@@ -274,6 +293,43 @@ def test_matmul_every_gemm_plan(ctx, monkeypatch, case, plan):
                              weight_dtype="f16")
         err = rel_err(got, np.asarray(ref, np.float64))
         assert err <= TOL["f16"], f"M={m}: relative error {err}"
+    w.free()
+
+
+# The bf16 and split prefill paths run the 128x128 and 64x128 tiles on eight wavefronts, and 2-bit
+# weights the 64- and 128-row f16 tiles: each forced, with and without K splits, over ragged M, N, K.
+MODE_PLAN_CASES = [
+    # bits, block, zp, K, N, M, A type, weight type, bias
+    (4, 32, "packed", 1000, 1000, 200, "bf16", "bf16", "bf16"),
+    (8, 64, "none", 768, 520, 130, "bf16", "bf16", None),
+    (4, 32, "packed", 1000, 1000, 200, "f32", "f32", "f32"),
+    (4, 64, "float", 768, 300, 257, "f32", "f16", None),
+    (8, 32, "packed", 512, 300, 100, "f16", "bf16", None),
+    (2, 64, "packed", 1024, 300, 150, "f16", "f16", None),
+    (2, 16, "none", 512, 200, 100, "f16", "f16", "f16"),
+]
+MODE_PLANS = [(128, 2, 1, 2), (128, 2, 3, 2), (64, 2, 1, 2), (64, 2, 2, 2), (128, 4, 2), (64, 4, 1)]
+
+
+@pytest.mark.parametrize("plan", MODE_PLANS, ids=lambda p: "bm{}_wn{}_s{}".format(*p) + ("_ks2" if len(p) > 3 else ""))
+@pytest.mark.parametrize("case", MODE_PLAN_CASES, ids=lambda c: "b{}_bs{}_{}_K{}_N{}_M{}_{}_{}".format(*c[:8]))
+def test_matmul_float_and_2bit_gemm_plans(ctx, monkeypatch, case, plan):
+    bits, bs, zp, k, n, m, adt, wdt, bias_dt = case
+    monkeypatch.setenv("TMH_GEMM_PLAN", ",".join(map(str, plan)))
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    b, s32, z = nbits_weight(rng, k, n, bits, bs, zp=zp, scale_dtype=np.float32)
+    scales = host_float(s32, wdt)
+    w = PackedWeight.upload(ctx, b, scales, z, k=k, n=n, bits=bits, block_size=bs, weight_dtype=wdt, scales_dtype=wdt)
+    bias = host_float(rng.standard_normal(n).astype(np.float32), bias_dt) if bias_dt else None
+    print(f"matmul mode plan {plan} {case}", flush=True)
+    a = host_float(rng.standard_normal((m, k)).astype(np.float32), adt)
+    y = matmul_nbits(ctx.put(a, adt), w, ctx.put(bias, bias_dt) if bias is not None else None)
+    ref = o.matmul_nbits(a, b, as_f64(scales, wdt).astype(np.float32), z, bias, k=k, n=n, bits=bits, block_size=bs,
+                         weight_dtype=wdt)
+    ref_dtype = "bf16" if ref.dtype == np.uint16 else ("f16" if ref.dtype == np.float16 else "f32")
+    assert y.dtype == ref_dtype
+    err = rel_err(as_f64(y.numpy(), y.dtype), as_f64(ref, ref_dtype))
+    assert err <= TOL[adt], f"relative error {err}"
     w.free()
 
 

@@ -90,6 +90,47 @@ def test_prefill_projection(ctx, proj):
     check_matmul(ctx, name, k, n, 128, [256, 2048], 0.005)
 
 
+@pytest.mark.parametrize("adt", ["f32", "bf16"])
+@pytest.mark.parametrize("proj", SMOLLM3_3B, ids=lambda p: p[0])
+def test_prefill_projection_f32_and_bf16(ctx, proj, adt):
+    """The SmolLM3-3B prefill projections with f32 activations and weights (scales f32: the
+    reference's :compute_type f32 after move/2, lib/transmuter.ex:49-93 and :1230-1233) within 1e-3,
+    and with bf16 activations and weights within 2e-2, at M = 256 and 2048, against the oracle's
+    dequantized weights in that type."""
+    from transmuter_amd.device import bf16_bits_to_f32, f32_to_bf16_bits
+
+    name, k, n = proj
+    rng = np.random.default_rng(zlib.crc32(f"{name}/{k}/{n}/{adt}".encode()))
+    b, s, z = nbits_weight(rng, k, n, 4, 128, zp="packed", scale_mul=0.005, scale_dtype=np.float32)
+    if adt == "bf16":
+        sw = o.bf16_round(s)
+        w = PackedWeight.upload(ctx, b, sw, z, k=k, n=n, bits=4, block_size=128, weight_dtype="bf16",
+                                scales_dtype="bf16")
+        wf = o.dequantize_weight(b, o.bf16_to_f32(sw), z, k, n, 4, 128, o.BF16)  # exact bf16 values
+    else:
+        w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=4, block_size=128, weight_dtype="f32")
+        wf = o.dequantize_weight(b, s, z, k, n, 4, 128, o.F32)
+    wf = np.asarray(wf, np.float64)
+    try:
+        for m in (256, 2048):
+            print(f"{name} {adt} K={k} N={n} block=128 M={m}", flush=True)
+            a32 = rng.standard_normal((m, k)).astype(np.float32)
+            if adt == "bf16":
+                bits = f32_to_bf16_bits(a32)
+                a_d, a64 = ctx.put(bits, "bf16"), bf16_bits_to_f32(bits).astype(np.float64)
+            else:
+                a_d, a64 = ctx.put(a32), a32.astype(np.float64)
+            y = matmul_nbits(a_d, w)
+            assert y.dtype == adt and y.shape == (m, n)
+            got = y.numpy()
+            got = bf16_bits_to_f32(got).astype(np.float64) if adt == "bf16" else got.astype(np.float64)
+            ref = a64 @ wf.T
+            err = rel_err(got, ref)
+            assert err <= (1e-3 if adt == "f32" else 2e-2), f"{name} {adt} M={m}: relative error {err}"
+    finally:
+        w.free()
+
+
 def test_lm_head(ctx):
     check_matmul(ctx, "lm_head", 1024, 151936, 32, [1, 8], 0.01)
 

@@ -372,13 +372,115 @@ __global__ __launch_bounds__(256) void k_gemm_f16(
 // splitting K, and its 64 KiB of LDS lets two workgroups share a CU.
 constexpr int kGemmBM = 256;  // largest tile height: bounds the A rows a launch may touch
 
-// LDS of one workgroup: the double-buffered A tile, or (KS = 2) the partial sums of half the
-// wavefronts after the k-loop, whichever is larger.
-template <int BITS, int BM, int KS = 1>
+// How the prefill GEMM's operands reach the MFMAs (the template argument MODE):
+//  GM_F16   f16 A and f16 weights (q - zero) * scale made exact in f16 registers from the packed
+//           bits (unpack_step), v_mfma_f32_16x16x32_f16;
+//  GM_BF16  bf16 A and bf16 weights: (q - zero) * scale formed exactly in f32 and rounded once to
+//           bf16, as the reference's bf16 dequantization rounds it (packed or no zero points),
+//           v_mfma_f32_16x16x32_bf16;
+//  GM_SPLIT any other float types (f32 A, f32 weights, float zero points, mixed types): A is split
+//           by k_split_a into bf16 hi + lo (hi = bf16(a), lo = bf16(a - hi): 16 significant bits,
+//           f32's exponent range), the weights are dequantized in f32 and rounded to their own type
+//           WT as the reference does, then split the same way, and each product takes three bf16
+//           MFMAs (hi*hi + lo*hi + hi*lo; the dropped lo*lo term is below 2^-16 of each product).
+enum : int { GM_F16 = 0, GM_BF16 = 1, GM_SPLIT = 2 };
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// LDS of one workgroup: the double-buffered A tile (two tiles, hi and lo, for GM_SPLIT), or
+// (KS = 2) the partial sums of half the wavefronts after the k-loop, whichever is larger.
+template <int BITS, int BM, int KS = 1, int MODE = GM_F16>
 constexpr size_t gemm_lds_bytes() {
-  constexpr size_t a_tiles = 2 * static_cast<size_t>(BM) * (512 / BITS) * 2;
+  constexpr size_t a_tiles = 2 * static_cast<size_t>(BM) * (512 / BITS) * 2 * (MODE == GM_SPLIT ? 2 : 1);
   constexpr size_t partial = KS > 1 ? static_cast<size_t>(BM) * 128 * sizeof(float) : 0;
   return a_tiles > partial ? a_tiles : partial;
+}
+
+// One MFMA step of a 16x16 output tile: weights (first operand) times A.
+template <int MODE>
+__device__ __forceinline__ float4_t gm_mma(const uint4_t& b, const uint4_t& a, float4_t c) {
+  if constexpr (MODE == GM_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, b), __builtin_bit_cast(half8_t, a), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, b), __builtin_bit_cast(bf16x8_t, a), c,
+                                                   0, 0, 0);
+}
+
+__device__ __forceinline__ float byte_f32(uint32_t x, int b) { return static_cast<float>((x >> (8 * b)) & 0xFFu); }
+
+// The eight values q of MFMA step i of a lane's 16 weight bytes, in k order, as f32 (in the
+// tiled layout's word order: value 2j at bits j*BITS, value 2j+1 at bits 16 + j*BITS).
+template <int BITS>
+__device__ __forceinline__ void step_values(const uint4_t& w, int i, float (&q)[8]) {
+  if constexpr (BITS == 4) {
+    // Bytes of x & 0x0F0F0F0F hold values 0, 4, 1, 5; of (x >> 4) & 0x0F0F0F0F values 2, 6, 3, 7.
+    const uint32_t x = w[i];
+    const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+    q[0] = byte_f32(lo, 0);
+    q[1] = byte_f32(lo, 2);
+    q[2] = byte_f32(hi, 0);
+    q[3] = byte_f32(hi, 2);
+    q[4] = byte_f32(lo, 1);
+    q[5] = byte_f32(lo, 3);
+    q[6] = byte_f32(hi, 1);
+    q[7] = byte_f32(hi, 3);
+  } else if constexpr (BITS == 8) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) q[4 * h + b] = byte_f32(w[2 * i + h], b);
+  } else {  // 2 bits: step i uses half of word i/2, pair j at bits 2j and 16 + 2j
+    const uint32_t x = w[i >> 1] >> (8 * (i & 1));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t p = (x >> (2 * j)) & 0x00030003u;
+      q[2 * j] = byte_f32(p, 0);
+      q[2 * j + 1] = byte_f32(p, 2);
+    }
+  }
+}
+
+// bf16 bits of two f32 values (round to nearest even) as one word, the first in the low half.
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t p = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// GM_BF16 weights of step i: (q - zero) * scale = fma(q, scale, -zero * scale), exact in f32 (q and
+// zero are integers below 256 and the scale a bf16 value), rounded once to bf16.
+template <int BITS>
+__device__ __forceinline__ uint4_t dequant_bf16(const uint4_t& w, int i, float s, float nzs) {
+  float q[8];
+  step_values<BITS>(w, i, q);
+  uint4_t out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) out[j] = pack_bf16(fmaf(q[2 * j], s, nzs), fmaf(q[2 * j + 1], s, nzs));
+  return out;
+}
+
+// f32 value x rounded to type WT and back (f32: unchanged).
+template <int WT>
+__device__ __forceinline__ float round_wt(float x) {
+  if constexpr (WT == DT_F32) return x;
+  else return round_to<WT>(x);
+}
+
+// GM_SPLIT weights of step i: (q - zero) rounded to the weight type WT, times the scale, rounded
+// to WT (the reference's dequantization in WT), then split into bf16 hi and lo.
+template <int BITS, int WT>
+__device__ __forceinline__ void dequant_split(const uint4_t& w, int i, float s, float z, uint4_t& hi, uint4_t& lo) {
+  float q[8];
+  step_values<BITS>(w, i, q);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float w0 = round_wt<WT>(round_wt<WT>(q[2 * j] - z) * s);
+    const float w1 = round_wt<WT>(round_wt<WT>(q[2 * j + 1] - z) * s);
+    const uint32_t h = pack_bf16(w0, w1);
+    hi[j] = h;
+    lo[j] = pack_bf16(w0 - __builtin_bit_cast(float, h << 16), w1 - __builtin_bit_cast(float, h & 0xFFFF0000u));
+  }
 }
 
 // Slot of 16-byte piece `piece` in LDS row `row` (q4 rows hold 16 pieces, q8 rows 8); its own
@@ -388,6 +490,11 @@ __device__ __forceinline__ int a_slot(int row, int piece) {
   return piece ^ frag_swizzle<BITS == 8 ? 8 : 16>(row);
 }
 
+// An f32 sum rounded to the dot's type (Nx.dot of two f16 or two bf16 operands gives that type).
+__device__ __forceinline__ float round_dot(float x, int dot_dt) {
+  return dot_dt == DT_F16 ? round_to<DT_F16>(x) : (dot_dt == DT_BF16 ? round_to<DT_BF16>(x) : x);
+}
+
 // Four consecutive outputs of row offset `row` (columns n.., those below N) in any float type: the
 // dot type's rounding, then the bias. Kept out of line so that the GEMM epilogue's loops over its
 // accumulator tiles stay small enough to unroll (the tiles then stay in registers).
@@ -395,20 +502,23 @@ __device__ __noinline__ void store_quad_any(float4_t v, void* Y, int y_dt, int d
                                             int64_t row, int64_t n, int64_t N) {
   for (int e = 0; e < 4 && n + e < N; ++e) {
     float x = v[e];
-    if (dot_dt == DT_F16) x = round_to<DT_F16>(x);
+    x = round_dot(x, dot_dt);
     if (bias) x += load_float_rt(bias, bias_dt, n + e);
     store_float_rt(Y, y_dt, row + n + e, x);
   }
 }
 
 // (The body; k_gemm_lds and its stamping build k_gemm_lds_tl below are the kernels.)
-template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS, bool TL>
+// MODE (GM_*) and WT (GM_SPLIT: the weights' type) select the operand path; zk is the zero
+// point kind (TMH_ZP_*) read by GM_SPLIT, whose zero points are u8 (packed) or f32 (float) per
+// parameter entry. For GM_SPLIT, A is the bf16 hi rows [M][lda] followed by the lo rows.
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS, bool TL, int MODE, int WT>
 __device__ __forceinline__ void gemm_lds(
-    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
-    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
+    const uint4_t* __restrict__ qt, const void* __restrict__ sc, const void* __restrict__ zp,
+    const void* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
     int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
     int64_t nchunks, int nbc, int bsc_shift, int mblocks, int nblocks, int chunks_per_split,
-    float* __restrict__ ws, uint32_t* __restrict__ tl) {
+    float* __restrict__ ws, int zk, uint32_t* __restrict__ tl) {
   const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
   constexpr int CW = 512 / BITS;
   constexpr int GW = CW / 4;
@@ -436,6 +546,9 @@ __device__ __forceinline__ void gemm_lds(
   constexpr bool TALL = WN == 4 || BM <= 128;
   constexpr int MTW = TALL ? BM / 16 : 8;
   constexpr int NTW = TALL ? 2 : 4;
+  static_assert(MODE == GM_F16 || (TALL && !SPLIT), "the bf16 paths use the tall layout, one parameter per lane");
+  constexpr int ABUF = BM * ROWB * (MODE == GM_SPLIT ? 2 : 1);  // LDS bytes of one A buffer (hi, then lo)
+  constexpr int SES = MODE == GM_SPLIT && WT == DT_F32 ? 4 : 2;  // bytes per stored scale
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -459,10 +572,14 @@ __device__ __forceinline__ void gemm_lds(
   const uint32_t kb1 = kb0 + chunks_per_split < nch ? kb0 + chunks_per_split : nch;
 
   const auto a_rsrc = buffer_rsrc(A, static_cast<uint32_t>(M * lda * 2));
+  const auto alo_rsrc = buffer_rsrc(static_cast<const uint8_t*>(A) + (MODE == GM_SPLIT ? M * lda * 2 : 0),
+                                    MODE == GM_SPLIT ? static_cast<uint32_t>(M * lda * 2) : 0u);
   const auto q_rsrc = buffer_rsrc(qt, static_cast<uint32_t>(ntiles * nchunks * 1024));
   const uint32_t n_params = static_cast<uint32_t>(ntiles * nchunks * nbc * 16);
-  const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
-  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+  const auto s_rsrc = buffer_rsrc(sc, n_params * SES);
+  const uint32_t z_bytes = MODE == GM_SPLIT ? (zk == TMH_ZP_FLOAT ? n_params * 4 : zk == TMH_ZP_PACKED ? n_params : 0u)
+                                            : (HAS_ZP ? n_params : 0u);
+  const auto z_rsrc = buffer_rsrc(zp, z_bytes);
 
   // A loads of this wavefront: rows wave*RW + s*RPI + lane/PPR, LDS slot lane%PPR. Offsets are
   // formed per load (few live registers); rows at or past M lie outside the buffer range and
@@ -475,12 +592,16 @@ __device__ __forceinline__ void gemm_lds(
     return a_row0 + static_cast<uint32_t>(s2) * a_rstep + piece * 16;
   };
   auto load_a = [&](uint32_t kb, int buf, int s_lo = 0, int s_hi = 1 << 30) {
-    uint8_t* base = lds + buf * (BM * ROWB) + wave * RW * ROWB;
+    uint8_t* base = lds + buf * ABUF + wave * RW * ROWB;
     if (static_cast<int64_t>(kb + 1) * CW <= K) {
 #pragma unroll
       for (int s2 = 0; s2 < LOADS; ++s2)
-        if (s2 >= s_lo && s2 < s_hi) lds_dma16(a_rsrc, base + s2 * RPI * ROWB, a_off(s2), kb * (CW * 2));
+        if (s2 >= s_lo && s2 < s_hi) {
+          lds_dma16(a_rsrc, base + s2 * RPI * ROWB, a_off(s2), kb * (CW * 2));
+          if constexpr (MODE == GM_SPLIT) lds_dma16(alo_rsrc, base + BM * ROWB + s2 * RPI * ROWB, a_off(s2), kb * (CW * 2));
+        }
     } else {
+      // (GM_SPLIT's A is zero-padded to whole chunks by k_split_a, so it never comes here.)
       // A k-block that reaches past K: through registers, zero past K. The whole offset is in
       // the VGPR operand so the buffer range check covers it.
 #pragma unroll
@@ -513,8 +634,15 @@ __device__ __forceinline__ void gemm_lds(
       for (int j = 0; j < NJ; ++j) {
         uint32_t e = p_base + nt * p_tstep;
         if constexpr (SPLIT) e += static_cast<uint32_t>(((g * GW + 8 * j) >> bsc_shift) - ((g * GW) >> bsc_shift)) * 16;
-        st.s[j][nt] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, kofs * 2, 0);
-        if constexpr (HAS_ZP) st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, kofs, 0);
+        if constexpr (SES == 4) st.s[j][nt] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, e * 4, kofs * 4, 0);
+        else st.s[j][nt] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, kofs * 2, 0);
+        if constexpr (MODE == GM_SPLIT) {
+          // Float zero points are f32 per entry, packed ones u8 (a wavefront-uniform choice).
+          if (zk == TMH_ZP_FLOAT) st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b32(z_rsrc, e * 4, kofs * 4, 0);
+          else if (zk == TMH_ZP_PACKED) st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, kofs, 0);
+        } else if constexpr (HAS_ZP) {
+          st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, kofs, 0);
+        }
       }
     }
   };
@@ -548,9 +676,75 @@ __device__ __forceinline__ void gemm_lds(
   // Software pipeline over the k-block's steps: once fragment mt of step i has fed its four
   // MFMAs, the same registers take fragment mt of step i+1 from LDS; step i+1's weights are
   // dequantized (into the other of two register sets) while step i's MFMAs run.
+  // The scale and zero point of a parameter entry as f32 (the bf16 paths).
+  auto scale_of = [&](uint32_t bits) -> float {
+    if constexpr (MODE == GM_SPLIT && WT == DT_F32) return __builtin_bit_cast(float, bits);
+    else if constexpr (MODE == GM_SPLIT && WT == DT_F16) return f16_bits_to_f32(static_cast<uint16_t>(bits));
+    else return __builtin_bit_cast(float, bits << 16);  // bf16
+  };
+  auto zero_of = [&](uint32_t bits) -> float {
+    constexpr float kDefault = static_cast<float>(1 << (BITS - 1));
+    if constexpr (MODE == GM_SPLIT)
+      return zk == TMH_ZP_FLOAT ? __builtin_bit_cast(float, bits)
+                                : (zk == TMH_ZP_PACKED ? static_cast<float>(bits & 0xFFu) : kDefault);
+    else return HAS_ZP ? static_cast<float>(bits & 0xFFu) : kDefault;
+  };
   auto compute = [&](int buf, const BStage& st, bool more, uint32_t kbn, BStage& nst) {
-    const uint8_t* abase = lds + buf * (BM * ROWB) + (wm * 128 + r) * ROWB;
-    if constexpr (TALL) {
+    const uint8_t* abase = lds + buf * ABUF + (wm * 128 + r) * ROWB;
+    if constexpr (MODE != GM_F16) {
+      // The bf16 paths (tall layout): the step pipeline of the f16 path, with the weights
+      // dequantized through f32 and, for GM_SPLIT, the hi and lo parts of A and of the weights
+      // (three MFMAs per product).
+      auto steps = [&](auto khc) {
+        constexpr int KH = decltype(khc)::value;
+#pragma unroll
+        for (int li = 0; li < LSTEPS; ++li) {
+          const int i = KH * LSTEPS + li;
+          if (more) issue(li, kbn, buf ^ 1, nst);
+          uint4_t bh[NTW], bl[NTW];
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt) {
+            const float s = scale_of(st.s[0][nt]), z = zero_of(st.z[0][nt]);
+            if constexpr (MODE == GM_BF16) bh[nt] = dequant_bf16<BITS>(st.w[nt], i, s, -z * s);
+            else dequant_split<BITS, WT>(st.w[nt], i, s, z, bh[nt], bl[nt]);
+          }
+          const int slot = a_slot<BITS>(r, g * (GW / 8) + i) * 16;
+          uint4_t a = *reinterpret_cast<const uint4_t*>(abase + slot), al{};
+          if constexpr (MODE == GM_SPLIT) al = *reinterpret_cast<const uint4_t*>(abase + BM * ROWB + slot);
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt) {
+            uint4_t an{}, aln{};
+            if (mt + 1 < MTW) {
+              an = *reinterpret_cast<const uint4_t*>(abase + (mt + 1) * 16 * ROWB + slot);
+              if constexpr (MODE == GM_SPLIT)
+                aln = *reinterpret_cast<const uint4_t*>(abase + BM * ROWB + (mt + 1) * 16 * ROWB + slot);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) {
+              acc[mt][nt] = gm_mma<MODE>(bh[nt], a, acc[mt][nt]);
+              if constexpr (MODE == GM_SPLIT) {
+                acc[mt][nt] = gm_mma<MODE>(bl[nt], a, acc[mt][nt]);
+                acc[mt][nt] = gm_mma<MODE>(bh[nt], al, acc[mt][nt]);
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (mt + 1 < MTW) {
+              a = an;
+              if constexpr (MODE == GM_SPLIT) al = aln;
+            }
+          }
+        }
+      };
+      if constexpr (KS == 1) {
+        steps(std::integral_constant<int, 0>{});
+      } else if (kh == 0) {
+        steps(std::integral_constant<int, 0>{});
+      } else {
+        steps(std::integral_constant<int, 1>{});
+      }
+      return;
+    } else if constexpr (TALL) {
       // Two wavefronts per SIMD: each keeps few registers live and relies on the other to fill
       // its waits; one set of weight fragments per step, A fragments read one ahead of use.
       // Step i = KH * LSTEPS + li stays a compile-time index (KH is the wavefront's half).
@@ -649,8 +843,16 @@ __device__ __forceinline__ void gemm_lds(
     }
   }
   // Lane (16g + r) holds, for each (mt, nt), row mt*16 + r and the 4 columns nt*16 + 4g ...
-  const bool f16_out = y_dt == DT_F16 && dot_dt == DT_F16 && !bias;
+  // Two-byte outputs without a bias: f16 (the f16 and split paths) or bf16 (the bf16 path).
+  constexpr int HDT = MODE == GM_BF16 ? DT_BF16 : DT_F16;
+  const bool f16_out = y_dt == HDT && dot_dt == HDT && !bias;
   const bool vec_out = (ldy % 4) == 0;
+  auto pack4 = [](float4_t v) -> uint2 {
+    if constexpr (HDT == DT_BF16) return make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+    const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
+    const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+    return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+  };
   // Whole tiles of f32 partial sums, or of f16 outputs with 16-byte aligned rows, go out through
   // LDS: each wavefront writes its accumulators there in the MFMA layout, then every thread
   // stores 16 contiguous bytes of a row, so a store instruction writes whole cache lines (from
@@ -660,7 +862,7 @@ __device__ __forceinline__ void gemm_lds(
   // partial sums that need two passes were slower staged than stored directly, 16 bytes a lane.
   // The f16 rows store non-temporally: 2048 -> 11008 at M = 2048, 45 MB out, 109.8 -> 107.9 us;
   // the partial sums, read back by the reduction, gain nothing from it.)
-  constexpr bool kPartialsFit = static_cast<int>(gemm_lds_bytes<BITS, BM, KS>()) >= BM * 64 * WN * 4;
+  constexpr bool kPartialsFit = static_cast<int>(gemm_lds_bytes<BITS, BM, KS, MODE>()) >= BM * 64 * WN * 4;
   const bool staged = ws ? kPartialsFit && (N % 4) == 0
                          : f16_out && (ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
   if (staged) {
@@ -669,7 +871,7 @@ __device__ __forceinline__ void gemm_lds(
       constexpr int BN = 64 * WN;
       constexpr int RS = BN * ESZ;  // bytes per staged row
       constexpr int UPR = RS / 16;  // 16-byte units per row
-      constexpr int CAP = static_cast<int>(gemm_lds_bytes<BITS, BM, KS>());
+      constexpr int CAP = static_cast<int>(gemm_lds_bytes<BITS, BM, KS, MODE>());
       constexpr int RPP = CAP / RS >= BM ? BM : CAP / RS;  // rows per pass
       static_assert(RPP >= 16 && BM % RPP == 0 && UPR >= 8, "staging shape");
       constexpr int NTHR = 128 * WN * KS;
@@ -690,9 +892,7 @@ __device__ __forceinline__ void gemm_lds(
               if constexpr (ESZ == 4) {
                 *reinterpret_cast<float4_t*>(p) = v;
               } else {
-                const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
-                const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
-                *reinterpret_cast<uint2*>(p) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+                *reinterpret_cast<uint2*>(p) = pack4(v);
               }
             }
           }
@@ -754,10 +954,12 @@ __device__ __forceinline__ void gemm_lds(
         continue;
       }
       if (f16_out && vec_out && n + 4 <= N) {
-        const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
-        const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
-        uint32_t pair[2] = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
-        *reinterpret_cast<uint2*>(static_cast<_Float16*>(Y) + m * ldy + n) = make_uint2(pair[0], pair[1]);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(Y) + m * ldy + n) = pack4(v);
+        continue;
+      }
+      if (MODE == GM_SPLIT && y_dt == DT_F32 && dot_dt == DT_F32 && !bias && vec_out && n + 4 <= N &&
+          (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
+        *reinterpret_cast<float4_t*>(static_cast<float*>(Y) + m * ldy + n) = v;
         continue;
       }
       store_quad_any(v, Y, y_dt, dot_dt, bias, bias_dt, m * ldy, n, N);
@@ -766,28 +968,52 @@ __device__ __forceinline__ void gemm_lds(
   if constexpr (TL) tl_stamp(tl, tl0);
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS>
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS, int MODE = GM_F16, int WT = DT_F16>
 __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds(
-    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
-    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
+    const uint4_t* __restrict__ qt, const void* __restrict__ sc, const void* __restrict__ zp,
+    const void* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
     int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
     int64_t nchunks, int nbc, int bsc_shift, int mblocks, int nblocks, int chunks_per_split,
-    float* __restrict__ ws) {
-  gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS, false>(qt, sc, zp, A, M, K, lda, bias, bias_dt, Y, y_dt, dot_dt, ldy, N,
-                                                   ntiles, nchunks, nbc, bsc_shift, mblocks, nblocks, chunks_per_split,
-                                                   ws, nullptr);
+    float* __restrict__ ws, int zk) {
+  gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS, false, MODE, WT>(qt, sc, zp, A, M, K, lda, bias, bias_dt, Y, y_dt, dot_dt,
+                                                             ldy, N, ntiles, nchunks, nbc, bsc_shift, mblocks, nblocks,
+                                                             chunks_per_split, ws, zk, nullptr);
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS>
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS, int MODE = GM_F16, int WT = DT_F16>
 __global__ __launch_bounds__(128 * WN * KS) void k_gemm_lds_tl(
-    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
-    const _Float16* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
+    const uint4_t* __restrict__ qt, const void* __restrict__ sc, const void* __restrict__ zp,
+    const void* __restrict__ A, int64_t M, int64_t K, int64_t lda, const void* __restrict__ bias,
     int bias_dt, void* __restrict__ Y, int y_dt, int dot_dt, int64_t ldy, int64_t N, int64_t ntiles,
     int64_t nchunks, int nbc, int bsc_shift, int mblocks, int nblocks, int chunks_per_split,
-    float* __restrict__ ws, uint32_t* __restrict__ tl) {
-  gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS, true>(qt, sc, zp, A, M, K, lda, bias, bias_dt, Y, y_dt, dot_dt, ldy, N,
-                                                  ntiles, nchunks, nbc, bsc_shift, mblocks, nblocks, chunks_per_split,
-                                                  ws, tl);
+    float* __restrict__ ws, int zk, uint32_t* __restrict__ tl) {
+  gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS, true, MODE, WT>(qt, sc, zp, A, M, K, lda, bias, bias_dt, Y, y_dt, dot_dt,
+                                                            ldy, N, ntiles, nchunks, nbc, bsc_shift, mblocks, nblocks,
+                                                            chunks_per_split, ws, zk, tl);
+}
+
+// GM_SPLIT's A operand: A [M, K] of type ADT (rows lda apart) as bf16 hi = bf16(a) and lo =
+// bf16(a - hi) (a - hi is exact in f32), each [M, Kp] with the rows zero-padded from K to Kp
+// (whole chunks), the lo rows after all the hi rows. One thread per 8 consecutive values of a row.
+template <int ADT>
+__global__ __launch_bounds__(256) void k_split_a(const void* __restrict__ A, int64_t M, int64_t K, int64_t lda,
+                                                 int64_t Kp, uint16_t* __restrict__ out) {
+  const int64_t per_row = Kp / 8;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= M * per_row) return;
+  const int64_t m = idx / per_row, k0 = (idx - m * per_row) * 8;
+  uint4_t hi, lo;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t k = k0 + 2 * j;
+    const float x0 = k < K ? load_as_f32<ADT>(A, m * lda + k) : 0.f;
+    const float x1 = k + 1 < K ? load_as_f32<ADT>(A, m * lda + k + 1) : 0.f;
+    const uint32_t h = pack_bf16(x0, x1);
+    hi[j] = h;
+    lo[j] = pack_bf16(x0 - __builtin_bit_cast(float, h << 16), x1 - __builtin_bit_cast(float, h & 0xFFFF0000u));
+  }
+  *reinterpret_cast<uint4_t*>(out + m * Kp + k0) = hi;
+  *reinterpret_cast<uint4_t*>(out + (M + m) * Kp + k0) = lo;
 }
 
 // Split-K epilogue: Y = sum over the splits of ws[split][M][N] (in split order), rounded to the
@@ -833,7 +1059,7 @@ __device__ __forceinline__ void splitk_reduce_quads(const float* __restrict__ ws
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float x = v[e];
-      if (dot_dt == DT_F16) x = round_to<DT_F16>(x);
+      x = round_dot(x, dot_dt);
       if (bias) x += load_float_rt(bias, bias_dt, n + e);
       store_float_rt(Y, y_dt, m * ldy + n + e, x);
     }
@@ -843,7 +1069,7 @@ __device__ __forceinline__ void splitk_reduce_quads(const float* __restrict__ ws
     float x = ws[i];
     for (int sp = 1; sp < splits; ++sp) x += ws[sp * total + i];
     const int64_t m = i / N, n = i - m * N;
-    if (dot_dt == DT_F16) x = round_to<DT_F16>(x);
+    x = round_dot(x, dot_dt);
     if (bias) x += load_float_rt(bias, bias_dt, n);
     store_float_rt(Y, y_dt, m * ldy + n, x);
   }
@@ -963,8 +1189,10 @@ struct MatArgs {
   void* y;
   int y_dt, dot_dt;
   int64_t ldy;
-  float* ws = nullptr;  // split-K partial sums (splitk_bytes() of them), resolved by the entry point
-  size_t split_cap = 0;  // most bytes of partial sums the plan may use (0: no limit)
+  float* ws = nullptr;       // split-K partial sums (gemm_scratch), resolved by the entry point
+  void* a_split = nullptr;   // GM_SPLIT's hi and lo rows of A (gemm_scratch)
+  size_t split_cap = SIZE_MAX;  // most bytes of partial sums the plan may use
+  bool no_split_a = false;   // no scratch memory for GM_SPLIT's rows of A: the general kernel runs
 };
 
 int bsc_shift_of(const tmh_weight* w) {
@@ -1044,20 +1272,40 @@ struct GemmPlan {
 
 int cus_of(const tmh_ctx* ctx) { return ctx->num_cus > 0 ? ctx->num_cus : 256; }
 
-// split_cap > 0 bounds the f32 partial sums a split plan keeps (splits * M * N * 4 bytes): plans
-// beyond it are not considered, a forced one included.
-GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bits, int cus, size_t split_cap = 0) {
+// gemm_lds_bytes at run time.
+size_t gemm_lds_bytes_rt(int bits, int bm, int ks, int mode) {
+  const size_t a_tiles = 2 * static_cast<size_t>(bm) * (512 / bits) * 2 * (mode == GM_SPLIT ? 2 : 1);
+  const size_t partial = ks > 1 ? static_cast<size_t>(bm) * 128 * sizeof(float) : 0;
+  return std::max(a_tiles, partial);
+}
+
+// The tile shapes each operand path is built for: every shape for f16 operands; the tall shapes
+// 128x128 and 64x128 on eight wavefronts for the bf16 paths (their 256x256 tile spills registers);
+// none whose A buffers exceed 128 KiB of LDS (2-bit rows are 512 bytes, and GM_SPLIT keeps two tiles).
+bool shape_built(int bits, int bm, int wn, int ks, int mode) {
+  if (gemm_lds_bytes_rt(bits, bm, ks, mode) > 128 * 1024) return false;
+  if (mode != GM_F16) return wn == 2 && ks == 2 && (bm == 128 || bm == 64);
+  return true;
+}
+
+// split_cap bounds the f32 partial sums a split plan keeps (splits * M * N * 4 bytes): plans
+// beyond it are not considered, a forced one included. The bf16 path is priced at the f16 rates
+// and GM_SPLIT at a third of them (three MFMAs per product).
+GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bits, int cus,
+                   size_t split_cap = SIZE_MAX, int mode = GM_F16) {
   auto fits = [&](int64_t splits) {
-    return split_cap == 0 || splits == 1 ||
+    return splits == 1 ||
            static_cast<double>(splits) * static_cast<double>(M) * static_cast<double>(N) * 4.0 <= static_cast<double>(split_cap);
   };
   const double cw = 512.0 / bits;
-  GemmPlan best{256, 2, 1, static_cast<int>(nchunks), 1};
+  const double slow = mode == GM_SPLIT ? 3.0 : 1.0;
+  GemmPlan best{128, 2, 1, static_cast<int>(nchunks), 2};
   double best_t = 1e30;
   for (const GemmShape& sh : kGemmShapes) {
+    if (!shape_built(bits, sh.bm, sh.wn, sh.ks, mode)) continue;
     const int64_t mblocks = (M + sh.bm - 1) / sh.bm;
     const int64_t tiles = mblocks * ((ntiles + 4 * sh.wn - 1) / (4 * sh.wn));
-    const double chunk_s = 2.0 * sh.bm * 64.0 * sh.wn * cw / sh.rate;
+    const double chunk_s = slow * 2.0 * sh.bm * 64.0 * sh.wn * cw / sh.rate;
     for (int64_t splits = 1; splits <= 16; ++splits) {
       if (splits > 1 && 2 * splits > nchunks) break;
       const int64_t cps = (nchunks + splits - 1) / splits;
@@ -1079,7 +1327,7 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
     int bm = 0, wn = 0, sp = 0, ks = 1;
     const int got = sscanf(f, "%d,%d,%d,%d", &bm, &wn, &sp, &ks);
     if ((got == 3 || got == 4) && (bm == 64 || bm == 128 || bm == 256) && (wn == 2 || wn == 4) && sp >= 1 &&
-        sp <= nchunks && (ks == 1 || (ks == 2 && bm <= 128 && wn == 2))) {
+        sp <= nchunks && (ks == 1 || (ks == 2 && bm <= 128 && wn == 2)) && shape_built(bits, bm, wn, ks, mode)) {
       const int cps = static_cast<int>((nchunks + sp - 1) / sp);
       const int used = static_cast<int>((nchunks + cps - 1) / cps);
       if (fits(used)) best = GemmPlan{bm, wn, used, cps, ks};
@@ -1088,34 +1336,37 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t ntiles, int64_t nchunks, int bi
   return best;
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS = 1>
-void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s, int splits, int cps) {
+// A operand of one GEMM launch: the caller's A, or GM_SPLIT's hi/lo rows (K padded to whole chunks).
+struct GemmA {
+  const void* a;
+  int64_t K, lda;
+};
+
+template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS = 1, int MODE = GM_F16, int WT = DT_F16>
+void launch_gemm_lds_wn(const tmh_weight* w, const MatArgs& a, const GemmA& ga, hipStream_t s, int splits, int cps) {
   const int mblocks = static_cast<int>((a.M + BM - 1) / BM);
   const int nblocks = static_cast<int>((w->ntiles + 4 * WN - 1) / (4 * WN));
   const int64_t tiles = static_cast<int64_t>(mblocks) * nblocks;
-  // The entry point provides splitk_bytes() of partial sums whenever the plan splits K.
+  // The entry point provides the partial sums (gemm_scratch) whenever the plan splits K.
   float* ws = splits > 1 ? a.ws : nullptr;
   const dim3 grid(static_cast<unsigned>(tiles * splits));
-  constexpr int kLds = static_cast<int>(gemm_lds_bytes<BITS, BM, KS>());
+  constexpr int kLds = static_cast<int>(gemm_lds_bytes<BITS, BM, KS, MODE>());
+  static_assert(kLds <= 128 * 1024, "the A buffers must fit 128 KiB of LDS");
   static const hipError_t attr[2] = {
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS, MODE, WT>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, kLds),
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_lds_tl<BITS, HAS_ZP, SPLIT, WN, BM, KS>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_lds_tl<BITS, HAS_ZP, SPLIT, WN, BM, KS, MODE, WT>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, kLds)};
   (void)attr;
-  if (uint32_t* tl = timeline_slots(TMH_TL_GEMM_LDS, static_cast<int64_t>(grid.x) * 2 * WN * KS)) {
-    k_gemm_lds_tl<BITS, HAS_ZP, SPLIT, WN, BM, KS><<<grid, 128 * WN * KS, kLds, s>>>(
-        reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
-        static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
-        a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
-        nblocks, cps, ws, tl);
-  } else {
-    k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS><<<grid, 128 * WN * KS, kLds, s>>>(
-        reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),
-        static_cast<const uint8_t*>(w->d_zero), static_cast<const _Float16*>(a.a), a.M, w->K, a.lda, a.bias,
-        a.bias_dt, a.y, a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks,
-        nblocks, cps, ws);
-  }
+#define TMH_GEMM_ARGS                                                                                               \
+  reinterpret_cast<const uint4_t*>(w->d_q), w->d_scale, w->d_zero, ga.a, a.M, ga.K, ga.lda, a.bias, a.bias_dt, a.y, \
+      a.y_dt, a.dot_dt, a.ldy, w->N, w->ntiles, w->nchunks, w->nbc, bsc_shift_of(w), mblocks, nblocks, cps, ws,    \
+      w->zp_kind
+  if (uint32_t* tl = timeline_slots(TMH_TL_GEMM_LDS, static_cast<int64_t>(grid.x) * 2 * WN * KS))
+    k_gemm_lds_tl<BITS, HAS_ZP, SPLIT, WN, BM, KS, MODE, WT><<<grid, 128 * WN * KS, kLds, s>>>(TMH_GEMM_ARGS, tl);
+  else
+    k_gemm_lds<BITS, HAS_ZP, SPLIT, WN, BM, KS, MODE, WT><<<grid, 128 * WN * KS, kLds, s>>>(TMH_GEMM_ARGS);
+#undef TMH_GEMM_ARGS
   if (ws) {
     const int64_t quads = (a.M * w->N + 3) / 4;
     const unsigned rgrid = static_cast<unsigned>((quads + 255) / 256);
@@ -1127,27 +1378,31 @@ void launch_gemm_lds_wn(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hip
   }
 }
 
-template <int BITS, bool HAS_ZP, bool SPLIT>
-void launch_gemm_lds(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
-  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, cus_of(ctx), a.split_cap);
-  if (p.bm == 64) {
-    if (p.ks == 2)
-      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 64, 2>(ctx, w, a, s, p.splits, p.cps);
-    else if (p.wn == 4)
-      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 64>(ctx, w, a, s, p.splits, p.cps);
-    else
-      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 64>(ctx, w, a, s, p.splits, p.cps);
+// Launches the plan's tile shape (only shapes shape_built() allows reach here).
+template <int BITS, bool HAS_ZP, bool SPLIT, int MODE = GM_F16, int WT = DT_F16>
+void launch_gemm_plan(const tmh_weight* w, const MatArgs& a, const GemmA& ga, hipStream_t s, const GemmPlan& p) {
+  if (p.bm == 64 && p.ks == 2) {
+    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 64, 2, MODE, WT>(w, a, ga, s, p.splits, p.cps);
   } else if (p.bm == 128 && p.ks == 2) {
-    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 128, 2>(ctx, w, a, s, p.splits, p.cps);
-  } else if (p.bm == 128) {
-    if (p.wn == 4)
-      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 128>(ctx, w, a, s, p.splits, p.cps);
-    else
-      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 128>(ctx, w, a, s, p.splits, p.cps);
-  } else if (p.wn == 4) {
-    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 256>(ctx, w, a, s, p.splits, p.cps);
-  } else {
-    launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 256>(ctx, w, a, s, p.splits, p.cps);
+    if constexpr (gemm_lds_bytes<BITS, 128, 2, MODE>() <= 128 * 1024)
+      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 128, 2, MODE, WT>(w, a, ga, s, p.splits, p.cps);
+  } else if constexpr (MODE == GM_F16) {
+    if (p.bm == 64) {
+      if (p.wn == 4)
+        launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 64>(w, a, ga, s, p.splits, p.cps);
+      else
+        launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 64>(w, a, ga, s, p.splits, p.cps);
+    } else if (p.bm == 128) {
+      if (p.wn == 4)
+        launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 128>(w, a, ga, s, p.splits, p.cps);
+      else
+        launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 128>(w, a, ga, s, p.splits, p.cps);
+    } else if constexpr (BITS != 2) {
+      if (p.wn == 4)
+        launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 256>(w, a, ga, s, p.splits, p.cps);
+      else
+        launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 256>(w, a, ga, s, p.splits, p.cps);
+    }
   }
 }
 
@@ -1156,20 +1411,47 @@ bool fast_path(const tmh_weight* w, const MatArgs& a) {
   return a.a_dt == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT;
 }
 
-// The LDS-tiled prefill GEMM applies (on the fast path): M > 64, 4 or 8 bits, aligned A, and
-// 32-bit buffer offsets over A (with a tile of rows past M) and the weights.
-bool gemm_lds_ok(const tmh_weight* w, const MatArgs& a) {
-  return a.M > 64 && w->bits != 2 && a.a_vec && (a.M + kGemmBM) * a.lda * 2 < (int64_t(1) << 31) &&
-         w->ntiles * w->nchunks * 1024 + 16 * w->nchunks * 1024 < (int64_t(1) << 31);
+// The operand path of the LDS-tiled prefill GEMM for a call, or -1 where it does not apply: M > 64
+// and 32-bit buffer offsets over the weights; f16 A with f16 weights (GM_F16) and bf16 A with bf16
+// weights (GM_BF16, one parameter entry per lane) without float zero points read A as given and
+// need it aligned, with 32-bit offsets over it (and a tile of rows past M); every other float
+// combination goes through GM_SPLIT (one parameter entry per lane, 32-bit offsets over its hi and
+// lo rows) unless the call cannot give it scratch memory for them (no_split_a).
+int gemm_mode(const tmh_weight* w, const MatArgs& a) {
+  if (a.M <= 64 || w->ntiles * w->nchunks * 1024 + 16 * w->nchunks * 1024 >= (int64_t(1) << 31)) return -1;
+  const bool direct_f16 = a.a_dt == TMH_F16 && w->wdtype == TMH_F16 && w->zp_kind != TMH_ZP_FLOAT;
+  const bool direct_bf16 = a.a_dt == TMH_BF16 && w->wdtype == TMH_BF16 && w->zp_kind != TMH_ZP_FLOAT;
+  if (direct_f16 || direct_bf16) {
+    if (!a.a_vec || (a.M + kGemmBM) * a.lda * 2 >= (int64_t(1) << 31)) return -1;
+    if (direct_bf16 && split_params(w)) return -1;
+    return direct_f16 ? GM_F16 : GM_BF16;
+  }
+  if (split_params(w) || a.no_split_a) return -1;
+  const int64_t kp = w->nchunks * chunk_weights(w->bits);
+  if ((a.M + kGemmBM) * kp * 2 >= (int64_t(1) << 31)) return -1;
+  return GM_SPLIT;
 }
 
-// Bytes of f32 partial sums one call needs: splits * M * N when the prefill GEMM's plan splits
-// K, else 0 (the GEMVs and unsplit GEMMs use no scratch memory).
-size_t splitk_bytes(const tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a) {
-  if (!fast_path(w, a) || !gemm_lds_ok(w, a)) return 0;
-  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, w->bits, cus_of(ctx), a.split_cap);
-  return p.splits > 1 ? static_cast<size_t>(p.splits) * static_cast<size_t>(a.M) * static_cast<size_t>(w->N) * sizeof(float)
-                      : 0;
+// Scratch memory of one call: GM_SPLIT's hi and lo rows of A, then the f32 partial sums of a plan
+// that splits K (splits * M * N), each 256-byte aligned; zeros where the call needs none.
+struct GemmScratch {
+  size_t a_split = 0, partials = 0;
+  size_t total() const { return a_split + partials; }
+};
+
+size_t split_a_bytes(const tmh_weight* w, int64_t M) {
+  const size_t kp = static_cast<size_t>(w->nchunks) * chunk_weights(w->bits);
+  return (2 * static_cast<size_t>(M) * kp * 2 + 255) / 256 * 256;
+}
+
+GemmScratch gemm_scratch(const tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a) {
+  GemmScratch g;
+  const int mode = gemm_mode(w, a);
+  if (mode < 0) return g;
+  if (mode == GM_SPLIT) g.a_split = split_a_bytes(w, a.M);
+  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, w->bits, cus_of(ctx), a.split_cap, mode);
+  if (p.splits > 1) g.partials = static_cast<size_t>(p.splits) * static_cast<size_t>(a.M) * static_cast<size_t>(w->N) * sizeof(float);
+  return g;
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
@@ -1181,10 +1463,7 @@ void launch_fast_variant(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hi
   } else if (a.M <= 64 || BITS == 2) {
     launch_gemv<BITS, 4, HAS_ZP, SPLIT>(w, a, s, ctx->num_cus);
   } else if constexpr (BITS != 2) {
-    if (gemm_lds_ok(w, a))
-      launch_gemm_lds<BITS, HAS_ZP, SPLIT>(ctx, w, a, s);
-    else
-      launch_gemm<BITS, HAS_ZP, SPLIT>(w, a, s);
+    launch_gemm<BITS, HAS_ZP, SPLIT>(w, a, s);
   }
 }
 
@@ -1196,6 +1475,43 @@ void launch_fast_bits(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipSt
   else if (zp) launch_fast_variant<BITS, true, false>(ctx, w, a, s);
   else if (split) launch_fast_variant<BITS, false, true>(ctx, w, a, s);
   else launch_fast_variant<BITS, false, false>(ctx, w, a, s);
+}
+
+// The prefill GEMM on operand path `mode` (gemm_mode), with GM_SPLIT's hi/lo rows of A made first.
+template <int BITS>
+void launch_gemm_bits(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s, int mode) {
+  const GemmPlan p = plan_gemm(a.M, w->N, w->ntiles, w->nchunks, BITS, cus_of(ctx), a.split_cap, mode);
+  const bool zp = w->zp_kind == TMH_ZP_PACKED;
+  if (mode == GM_F16) {
+    const GemmA ga{a.a, w->K, a.lda};
+    const bool split = split_params(w);
+    if (zp && split) launch_gemm_plan<BITS, true, true>(w, a, ga, s, p);
+    else if (zp) launch_gemm_plan<BITS, true, false>(w, a, ga, s, p);
+    else if (split) launch_gemm_plan<BITS, false, true>(w, a, ga, s, p);
+    else launch_gemm_plan<BITS, false, false>(w, a, ga, s, p);
+    return;
+  }
+  if (mode == GM_BF16) {
+    const GemmA ga{a.a, w->K, a.lda};
+    if (zp) launch_gemm_plan<BITS, true, false, GM_BF16, DT_BF16>(w, a, ga, s, p);
+    else launch_gemm_plan<BITS, false, false, GM_BF16, DT_BF16>(w, a, ga, s, p);
+    return;
+  }
+  const int64_t kp = w->nchunks * chunk_weights(BITS);
+  const int64_t quads = a.M * (kp / 8);
+  auto* split_rows = static_cast<uint16_t*>(a.a_split);
+  const unsigned sgrid = static_cast<unsigned>((quads + 255) / 256);
+  switch (a.a_dt) {
+    case TMH_F16: k_split_a<DT_F16><<<sgrid, 256, 0, s>>>(a.a, a.M, w->K, a.lda, kp, split_rows); break;
+    case TMH_BF16: k_split_a<DT_BF16><<<sgrid, 256, 0, s>>>(a.a, a.M, w->K, a.lda, kp, split_rows); break;
+    default: k_split_a<DT_F32><<<sgrid, 256, 0, s>>>(a.a, a.M, w->K, a.lda, kp, split_rows);
+  }
+  const GemmA ga{split_rows, kp, kp};
+  switch (w->wdtype) {
+    case TMH_F16: launch_gemm_plan<BITS, false, false, GM_SPLIT, DT_F16>(w, a, ga, s, p); break;
+    case TMH_BF16: launch_gemm_plan<BITS, false, false, GM_SPLIT, DT_BF16>(w, a, ga, s, p); break;
+    default: launch_gemm_plan<BITS, false, false, GM_SPLIT, DT_F32>(w, a, ga, s, p);
+  }
 }
 
 template <int BITS, int WDT>
@@ -1730,8 +2046,16 @@ int prepare_matmul(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_dty
   return TMH_OK;
 }
 
-// Launches a prepared MatMulNBits call (its split-K partial sums, if any, in a.ws).
+// Launches a prepared MatMulNBits call (its scratch memory, if any, in a.ws and a.a_split).
 int launch_matmul(tmh_ctx* ctx, const tmh_weight* w, const MatArgs& a, hipStream_t s) {
+  if (const int mode = gemm_mode(w, a); mode >= 0) {
+    switch (w->bits) {
+      case 2: launch_gemm_bits<2>(ctx, w, a, s, mode); break;
+      case 4: launch_gemm_bits<4>(ctx, w, a, s, mode); break;
+      default: launch_gemm_bits<8>(ctx, w, a, s, mode);
+    }
+    return check_launch(ctx, "k_gemm_lds");
+  }
   if (fast_path(w, a)) {
     switch (w->bits) {
       case 2: launch_fast_bits<2>(ctx, w, a, s); break;
@@ -1784,17 +2108,20 @@ int tmh_matmul_nbits(tmh_ctx* ctx, const tmh_weight* w, const void* d_a, int a_d
   TMH_TRY(prepare_matmul(ctx, w, d_a, a_dtype, M, lda, d_bias, bias_dtype, d_y, y_dtype, ldy, &a, &run));
   if (!run) return TMH_OK;
   hipStream_t s = pick_stream(ctx, stream);
-  if (const size_t need = splitk_bytes(ctx, w, a)) {
-    // A graph must replay what an eager call computes, so a call that splits K never runs
-    // unsplit instead: without the workspace (it cannot grow while the stream is captured)
-    // the call fails.
-    a.ws = static_cast<float*>(workspace(ctx, need, s));
-    if (!a.ws)
+  const GemmScratch g = gemm_scratch(ctx, w, a);
+  if (const size_t need = g.total()) {
+    // A graph must replay what an eager call computes, so a call that needs scratch memory never
+    // runs another plan instead: without the workspace (it cannot grow while the stream is
+    // captured) the call fails.
+    auto* ws = static_cast<uint8_t*>(workspace(ctx, need, s));
+    if (!ws)
       return fail(ctx, TMH_ERR_UNSUPPORTED,
-                  "MatMulNBits with M=%lld, N=%lld, K=%lld splits K and needs a %zu-byte workspace, which cannot "
-                  "be allocated now (not while the stream is being captured into a graph): run the call once "
-                  "before capture",
+                  "MatMulNBits with M=%lld, N=%lld, K=%lld needs a %zu-byte workspace (split K or the split rows "
+                  "of A), which cannot be allocated now (not while the stream is being captured into a graph): "
+                  "run the call once before capture",
                   (long long)M, (long long)w->N, (long long)w->K, need);
+    a.a_split = g.a_split ? ws : nullptr;
+    a.ws = g.partials ? reinterpret_cast<float*>(ws + g.a_split) : nullptr;
   }
   return launch_matmul(ctx, w, a, s);
 }
@@ -1807,12 +2134,16 @@ int tmh_matmul_nbits_noalloc(tmh_ctx* ctx, const tmh_weight* w, const void* d_a,
   bool run = false;
   TMH_TRY(prepare_matmul(ctx, w, d_a, a_dtype, M, lda, d_bias, bias_dtype, d_y, y_dtype, ldy, &a, &run));
   if (!run) return TMH_OK;
-  // The plan keeps its partial sums within the scratch: where tmh_matmul_nbits's plan would need
-  // more, the best plan with fewer splits of K (or none) runs instead.
-  a.split_cap = kNoallocScratchBytes;
-  if (const size_t need = splitk_bytes(ctx, w, a)) {
+  // The call keeps its scratch memory within the scratch area: GM_SPLIT's rows of A when they fit
+  // (else the general kernel runs), then the partial sums of the best plan that fits in the rest
+  // (where tmh_matmul_nbits's plan would need more: fewer splits of K, or none).
+  if (gemm_mode(w, a) == GM_SPLIT && split_a_bytes(w, a.M) > kNoallocScratchBytes) a.no_split_a = true;
+  const size_t rows_a = gemm_mode(w, a) == GM_SPLIT ? split_a_bytes(w, a.M) : 0;
+  a.split_cap = kNoallocScratchBytes - rows_a;
+  const GemmScratch g = gemm_scratch(ctx, w, a);
+  if (const size_t need = g.total()) {
     if (need > kNoallocScratchBytes)  // the plan honours the cap; kept as a guard on the scratch's bounds
-      return fail(ctx, TMH_ERR_INVALID, "MatMulNBits partial sums of %zu bytes exceed the %zu-byte scratch", need,
+      return fail(ctx, TMH_ERR_INVALID, "MatMulNBits scratch of %zu bytes exceeds the %zu-byte area", need,
                   kNoallocScratchBytes);
     float* p = nullptr;
     hipError_t err = hipErrorInvalidDevice;
@@ -1822,7 +2153,9 @@ int tmh_matmul_nbits_noalloc(tmh_ctx* ctx, const tmh_weight* w, const void* d_a,
       err = g_scratch_err[ctx->device];
     }
     if (!p) return check_hip(ctx, err == hipSuccess ? hipErrorInvalidDevice : err, "the scratch memory of tmh_matmul_nbits_noalloc");
-    a.ws = p;
+    auto* base = reinterpret_cast<uint8_t*>(p);
+    a.a_split = g.a_split ? base : nullptr;
+    a.ws = g.partials ? reinterpret_cast<float*>(base + g.a_split) : nullptr;
   }
   return launch_matmul(ctx, w, a, pick_stream(ctx, stream));
 }
