@@ -136,9 +136,10 @@ GRAPHS_UNDER_TRACER = "graph replays are not run under rocprofv3 (its graph-laun
 
 
 def matmul_call(ctx, w, a, y, m):
-    from transmuter_amd._lib import F16, lib
+    from transmuter_amd._lib import lib
 
-    ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, a.ptr, F16, m, w.k, None, 0, y.ptr, F16, w.n, None))
+    ctx.check(lib().tmh_matmul_nbits(ctx.handle, w.handle, a.ptr, a.tmh_dtype, m, w.k, None, 0, y.ptr, y.tmh_dtype, w.n,
+                                     None))
 
 
 def time_graphs(ctx, graphs, steps, warmup):
@@ -338,30 +339,34 @@ def single_op(ctx, reps, copies=160):
 # ---------------------------------------------------------------- prefill GEMM
 
 
+NP_TYPES = {"f16": np.float16, "f32": np.float32}
 ROTATE_BYTES = 1 << 30  # weight copies a workload's calls rotate over: 4x the 256 MB last-level cache
 
 
-def prefill(ctx, reps, ms_list, per_graph=8, rotate_bytes=ROTATE_BYTES):
+def prefill(ctx, reps, ms_list, per_graph=8, rotate_bytes=ROTATE_BYTES, dtype="f16"):
     """SmolLM3-3B projections, q4 block 128, at each M: `per_graph` calls per graph. Each
     projection's calls rotate over device copies of its weight totalling `rotate_bytes` (four
     times the 256 MB last-level cache), so the weights stream from HBM as a model's would; the
-    graphs are replayed round robin, each at least once per timed run."""
+    graphs are replayed round robin, each at least once per timed run. `dtype` is the type of A,
+    of the weights (their scales converted to it) and of Y: f16, bf16 or f32."""
     from transmuter_amd import PackedWeight
+    from transmuter_amd.device import f32_to_bf16_bits
 
     rng = np.random.default_rng(3)
     out = {}
     ws = []
     for _name, k, n in SMOLLM3_3B:
         b, sc, zp = make_weight_parts(rng, k, n, bs=128, scale_mul=0.005)
-        w = PackedWeight.upload(ctx, b, sc, zp, k=k, n=n, bits=4, block_size=128, weight_dtype="f16")
+        w = PackedWeight.upload(ctx, b, sc, zp, k=k, n=n, bits=4, block_size=128, weight_dtype=dtype)
         copies = max(1, -(-rotate_bytes // w.device_bytes()))
         copies = -(-copies // per_graph) * per_graph
         ws.append([w] + [PackedWeight.concat([w]) for _ in range(copies - 1)])
     for m in ms_list:
         per = []
         for (name, k, n), copies in zip(SMOLLM3_3B, ws):
-            a = ctx.put(rng.standard_normal((m, k), dtype=np.float32).astype(np.float16))
-            y = ctx.empty((m, n), "f16")
+            a32 = rng.standard_normal((m, k), dtype=np.float32)
+            a = ctx.put(f32_to_bf16_bits(a32), "bf16") if dtype == "bf16" else ctx.put(a32.astype(NP_TYPES[dtype]))
+            y = ctx.empty((m, n), dtype)
             matmul_call(ctx, copies[0], a, y, m)  # eager first: sizes the split-K workspace before capture
             ctx.synchronize()
             graphs = [Graph(ctx, lambda i=i, a=a, y=y: [matmul_call(ctx, copies[i + j], a, y, m) for j in range(per_graph)])
@@ -374,7 +379,9 @@ def prefill(ctx, reps, ms_list, per_graph=8, rotate_bytes=ROTATE_BYTES):
             flops = 2 * m * k * n
             per.append({"proj": name, "M": m, "us": us, "tflops": flops / (us * 1e-6) / 1e12,
                         "weight_copies": len(copies)})
-            log(f"prefill {name} M={m}: {us:.1f} us, {per[-1]['tflops']:.1f} TFLOP/s ({len(copies)} weight copies)")
+            log(f"prefill {dtype} {name} M={m}: {us:.1f} us, {per[-1]['tflops']:.1f} TFLOP/s ({len(copies)} weight copies)")
+            a.free()
+            y.free()
         flops = sum(2 * m * k * n for _name, k, n in SMOLLM3_3B)
         us = sum(p["us"] for p in per)
         out[m] = {"tflops": flops / (us * 1e-6) / 1e12, "per_projection": per}
@@ -1214,6 +1221,9 @@ def main():
         extra["single_op"] = single_op(ctx, 10)
     if "prefill" in parts:
         extra["prefill"] = prefill(ctx, 20, [256, 2048])
+        # The other activation types on the same shapes: bf16 (bf16 MFMA) and f32 (hi + lo splits).
+        extra["prefill_bf16"] = prefill(ctx, 10, [256, 2048], dtype="bf16")
+        extra["prefill_f32"] = prefill(ctx, 6, [256, 2048], dtype="f32")
     if "vocab" in parts:
         extra["large_vocab"] = large_vocab(ctx, 50)
     if "moe" in parts:
@@ -1274,6 +1284,9 @@ def main():
         line["prefill"] = {str(m): v for m, v in extra["prefill"].items()}
         line["prefill_tflops_M2048"] = extra["prefill"][2048]["tflops"]
         line["prefill_frac_M2048"] = extra["prefill"][2048]["tflops"] / MFMA_F16_PEAK_TFLOPS
+        for dt in ("bf16", "f32"):
+            line[f"prefill_{dt}"] = {str(m): v for m, v in extra[f"prefill_{dt}"].items()}
+            line[f"prefill_{dt}_over_f16_M2048"] = extra[f"prefill_{dt}"][2048]["tflops"] / extra["prefill"][2048]["tflops"]
     for key, name in (("large_vocab", "large_vocab"), ("single_op", "single_op_f32_k1024_n3072"), ("moe", "moe"),
                       ("int8", "int8")):
         if key in extra:

@@ -1284,7 +1284,9 @@ size_t gemm_lds_bytes_rt(int bits, int bm, int ks, int mode) {
 // none whose A buffers exceed 128 KiB of LDS (2-bit rows are 512 bytes, and GM_SPLIT keeps two tiles).
 bool shape_built(int bits, int bm, int wn, int ks, int mode) {
   if (gemm_lds_bytes_rt(bits, bm, ks, mode) > 128 * 1024) return false;
-  if (mode != GM_F16) return wn == 2 && ks == 2 && (bm == 128 || bm == 64);
+  const bool eight = (bm == 128 || bm == 64) && ((wn == 2 && ks == 2) || (wn == 4 && ks == 1));
+  if (mode == GM_BF16) return eight;
+  if (mode == GM_SPLIT) return eight && wn == 2;
   return true;
 }
 
@@ -1386,6 +1388,13 @@ void launch_gemm_plan(const tmh_weight* w, const MatArgs& a, const GemmA& ga, hi
   } else if (p.bm == 128 && p.ks == 2) {
     if constexpr (gemm_lds_bytes<BITS, 128, 2, MODE>() <= 128 * 1024)
       launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 2, 128, 2, MODE, WT>(w, a, ga, s, p.splits, p.cps);
+  } else if constexpr (MODE == GM_BF16) {
+    if (p.bm == 128) {
+      if constexpr (gemm_lds_bytes<BITS, 128, 1, MODE>() <= 128 * 1024)
+        launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 128, 1, MODE, WT>(w, a, ga, s, p.splits, p.cps);
+    } else {
+      launch_gemm_lds_wn<BITS, HAS_ZP, SPLIT, 4, 64, 1, MODE, WT>(w, a, ga, s, p.splits, p.cps);
+    }
   } else if constexpr (MODE == GM_F16) {
     if (p.bm == 64) {
       if (p.wn == 4)
