@@ -207,6 +207,16 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec_tl(
   gemv_dec<BITS, HAS_ZP, SPLIT, U, NW, TN, ALDS, true>(qt, sc, zp, A, nch, ntiles, lda, shape, Y, ldy, N, tl);
 }
 
+// Piece P of a k-group's A values: the 16 bytes lane P of each row (16 lanes) of the wavefront
+// holds, broadcast to the row (DPP row_newbcast).
+template <int P>
+__device__ __forceinline__ half8_t row_piece(const uint4_t& x) {
+  uint4_t b;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) b[d] = __builtin_amdgcn_update_dpp(0u, x[d], 0x150 + P, 0xF, 0xF, false);
+  return __builtin_bit_cast(half8_t, b);
+}
+
 // The decode GEMV for one row of A (M = 1), 4- or 8-bit weights whose parameters are constant
 // over a lane's GW values (block_size >= GW), f16 A / scales / Y, no bias: dot products instead
 // of MFMAs, which at one row leave 15 of 16 MFMA columns empty while the per-weight scaling
@@ -234,6 +244,7 @@ __device__ __forceinline__ void gemv_dot(
   constexpr int CW = 512 / BITS;  // weights per chunk row
   constexpr int GW = CW / 4;      // weights per lane per chunk
   constexpr int NP = GW / 8;      // 16-byte pieces of A per lane per chunk
+  constexpr bool DEDUP = TN == 1; // one A load per chunk and row broadcasts (resident grids)
   __shared__ __align__(16) float red[NW * TN * 64];
   (void)ldy;
   const uint32_t nbc = (shape >> 8) & 0xFFu, bsc_shift = (shape >> 16) & 0xFFu;
@@ -254,7 +265,7 @@ __device__ __forceinline__ void gemv_dot(
   for (uint32_t base = wave * U; base < nch; base += NW * U) {
     uint4_t w[U][TN];
     uint32_t sv[U][TN], zv[U][TN];
-    half8_t av[U][NP];
+    uint4_t mine[U][DEDUP ? 1 : NP];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t c = base + u < nch ? base + u : nch - 1;
@@ -266,15 +277,37 @@ __device__ __forceinline__ void gemv_dot(
         sv[u][tn] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, 0, 0);
         if constexpr (HAS_ZP) zv[u][tn] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0);
       }
+      if constexpr (DEDUP) {
+        // The chunk's A values of k-group g are NP 16-byte pieces, the same for the group's 16
+        // lanes: lanes (g, r < NP) load piece r, and row broadcasts (a row of the wavefront being
+        // one k-group's 16 lanes) hand every lane the NP pieces below. One A load per wavefront
+        // and chunk instead of NP: 2.88 against 3.00 us per stamped launch at the Qwen3-0.6B
+        // shapes. (Streaming grids, whose A fragments serve several tiles, keep one load per
+        // piece: the broadcasts cost more there, 18.6 against 17.5 us on the 151936 x 1024 lm_head.)
+        const uint32_t k = (base + u) * CW + g * GW + 8 * r;  // a piece lies wholly in or past K
+        mine[u][0] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, base + u < nch && r < NP && k < K ? k * 2 : 0x80000000u, 0, 0);
+      } else {
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        const uint32_t k = (base + u) * CW + g * GW + 8 * p;  // a piece lies wholly in or past K
-        av[u][p] = __builtin_bit_cast(
-            half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, base + u < nch && k < K ? k * 2 : 0x80000000u, 0, 0));
+        for (int p = 0; p < NP; ++p) {
+          const uint32_t k = (base + u) * CW + g * GW + 8 * p;  // a piece lies wholly in or past K
+          mine[u][p] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, base + u < nch && k < K ? k * 2 : 0x80000000u, 0, 0);
+        }
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      half8_t av[1][NP];
+      if constexpr (DEDUP) {
+        av[0][0] = row_piece<0>(mine[u][0]);
+        av[0][1] = row_piece<1>(mine[u][0]);
+        if constexpr (NP > 2) {
+          av[0][2] = row_piece<2>(mine[u][0]);
+          av[0][3] = row_piece<3>(mine[u][0]);
+        }
+      } else {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) av[0][p] = __builtin_bit_cast(half8_t, mine[u][p]);
+      }
       // Sums of this lane's A values, split by the pair form their weights take. (A pieces are
       // held as f16 vectors: pairs are taken by element, since hipcc 7.2 read element 0 of an
       // integer vector for every index under __builtin_bit_cast of one element.)
@@ -283,7 +316,7 @@ __device__ __forceinline__ void gemv_dot(
       for (int p = 0; p < NP; ++p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const half2_t ap = {av[u][p][2 * j], av[u][p][2 * j + 1]};
+          const half2_t ap = {av[0][p][2 * j], av[0][p][2 * j + 1]};
           if (BITS == 4 && (j & 1)) so = __builtin_amdgcn_fdot2(ap, one2, so, false);
           else se = __builtin_amdgcn_fdot2(ap, one2, se, false);
         }
@@ -298,7 +331,7 @@ __device__ __forceinline__ void gemv_dot(
         for (int p = 0; p < NP; ++p) {
           half2_t ap[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) ap[j] = half2_t{av[u][p][2 * j], av[u][p][2 * j + 1]};
+          for (int j = 0; j < 4; ++j) ap[j] = half2_t{av[0][p][2 * j], av[0][p][2 * j + 1]};
           if constexpr (BITS == 4) {
             // Word p holds values 8p .. 8p+7: pairs (0,1) and (4,5) in low-nibble form, (2,3) and
             // (6,7) in high-nibble form, against A pairs 0, 2 and 1, 3 of piece p.
