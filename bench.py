@@ -1076,7 +1076,8 @@ def timeline_prefill(ctx, ms=(256, 2048), per_graph=4):
 
 def timeline_moe(ctx, sets=3, steps=6):
     """The QMoE layer of moe_ffn, one call per step over `sets` rotating copies of its experts:
-    the grouped expert products (fc1 and fc3 with the SwiGLU in one launch, then fc2)."""
+    routing, grouping by expert, the grouped expert products (fc1 and fc3 with the SwiGLU in one
+    launch, then fc2) and the weighted sum over each token's slots."""
     import ctypes
 
     from transmuter_amd._lib import F16, F32, lib
@@ -1111,8 +1112,11 @@ def timeline_moe(ctx, sets=3, steps=6):
     ctx.synchronize()
     wb = experts * hidden * inter * (0.5 + 2 / 32)  # one projection's expert weights and scales
     rows = tokens * k
-    calls = [("fc1 + fc3 (SwiGLU)", 2 * wb + tokens * hidden * 2 + rows * inter * 2, 2 * 2 * rows * hidden * inter),
-             ("fc2", wb + rows * inter * 2 + rows * hidden * 2, 2 * rows * hidden * inter)]
+    calls = [("routing (top-8 of 128)", tokens * experts * 4 + rows * 8, 0),
+             ("grouping by expert", rows * 4 * 4 + experts * 12, 0),
+             ("fc1 + fc3 (SwiGLU)", 2 * wb + tokens * hidden * 2 + rows * inter * 2, 2 * 2 * rows * hidden * inter),
+             ("fc2", wb + rows * inter * 2 + rows * hidden * 2, 2 * rows * hidden * inter),
+             ("weighted sum over the slots", rows * hidden * 2 + tokens * hidden * 2 + rows * 12, 0)]
     res = timeline_steps(ctx, [lambda s=s: call(s) for s in range(steps)], calls)
     for layer in layers:
         for w in layer:

@@ -414,7 +414,10 @@ enum {
   TMH_TL_FLOOR_READ = 7,    /* k_floor_read */
   TMH_TL_GATHER_ROWS = 8,   /* k_gather_bq_rows: GatherBlockQuantized of whole rows */
   TMH_TL_FLOOR_READ_ALL = 9, /* k_floor_read_all */
-  TMH_TL_FLOOR_WRITE = 10   /* k_floor_write */
+  TMH_TL_FLOOR_WRITE = 10,  /* k_floor_write */
+  TMH_TL_MOE_ROUTE = 11,    /* k_moe_route: QMoE top-k routing */
+  TMH_TL_MOE_PLAN = 12,     /* k_moe_plan: QMoE grouping by expert */
+  TMH_TL_MOE_COMBINE = 13   /* k_moe_combine: QMoE weighted sum over each token's experts */
 };
 int tmh_timeline_begin(tmh_ctx* ctx, void* d_slots, int64_t capacity);
 int tmh_timeline_end(tmh_ctx* ctx, int64_t* h_log, int64_t max_launches, int64_t* launches, int64_t* dropped);

@@ -51,6 +51,9 @@ CASES = [
     ("f16", 4, 2, 6, 64, 32, "identity", 0, False, 8, 16, False, True, 0.0),
     ("f16", 128, 8, 16, 512, 256, "swiglu", 0, True, 4, 32, False, False, 0.0),  # 128 experts, top-8
     ("f16", 64, 8, 70, 256, 128, "silu", 0, False, 2, 32, True, False, 0.0),      # 2-bit, rows past 32
+    ("f16", 200, 8, 24, 64, 32, "silu", 0, False, 4, 32, False, False, 0.0),       # 4 router keys per lane
+    ("f32", 600, 16, 8, 32, 16, "relu", 0, False, 4, 32, False, True, 0.0),        # 16 per lane, top-16
+    ("f16", 16, 8, 600, 64, 32, "silu", 0, False, 4, 32, False, False, 0.0),       # 4800 rows: plan reloads ids
 ]
 
 
@@ -153,6 +156,35 @@ def test_qmoe_routing_ties(ctx, dtype):
     scale = np.abs(ref).max()
     tol = 1e-2 * scale if dtype == "f16" else 1e-4 + 1e-3 * scale
     assert np.abs(got - ref).max() <= tol, f"max difference {np.abs(got - ref).max()} (max |ref| {scale})"
+
+
+@pytest.mark.parametrize("e", [200, 1000])
+def test_qmoe_routing_ties_among_many_experts(ctx, e):
+    """Ties across the 64-expert groups that routing holds per lane: equal values at experts far
+    apart, +0 beside -0 over every expert, and a maximum held by the last expert only."""
+    print(f"qmoe routing ties E={e}", flush=True)
+    rng = np.random.default_rng(9)
+    k, h, n1 = 3, 32, 16
+    router = np.full((4, e), -1.0, np.float32)
+    router[0, [e - 1, 130, 65, 64]] = 2.0                       # four-way tie: 64, 65, 130
+    router[1, :] = -0.0
+    router[1, ::7] = 0.0                                        # all equal: 0, 1, 2
+    router[2, e - 1] = 5.0
+    router[2, [3, e // 2]] = 4.0                                # e-1, then 3 before e/2
+    router[3, :] = np.linspace(-1.0, 1.0, e, dtype=np.float32)  # the three last experts, largest first
+    t = router.shape[0]
+    w1, s1, _ = _weights(rng, e, n1, h, 4, 32, False, "f16")
+    w2, s2, _ = _weights(rng, e, h, n1, 4, 32, False, "f16")
+    x = rng.standard_normal((t, h)).astype(np.float16)
+    node = NodeProto(op_type="QMoE", input=[], output=["y"],
+                     attribute=[_attr("k", k), _attr("block_size", 32), _attr("activation_type", "silu")])
+    (y,) = moe.apply(node, [ctx.put(x), ctx.put(router), w1, s1, None, w2, s2, None])
+    got = y.numpy().astype(np.float64)
+    ref = o.qmoe(x, router, w1, s1, w2, s2, k=k, bits=4, block_size=32, activation="silu").astype(np.float64)
+    _vals, idx = o.topk_stable(router, k)
+    assert idx.tolist() == [[64, 65, 130], [0, 1, 2], [e - 1, 3, e // 2], [e - 1, e - 2, e - 3]]
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref).max() <= 1e-2 * scale, f"max difference {np.abs(got - ref).max()} (max |ref| {scale})"
 
 
 def test_qmoe_fc3_without_zero_points_beside_fc1_with_them(ctx):

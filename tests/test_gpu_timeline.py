@@ -1,5 +1,5 @@
 """The launch timeline (tmh_timeline_begin / _end): the stamping builds of the decode GEMVs, the
-prefill GEMM and its split-K sum, the vocabulary gather, the QMoE grouped product and the floors
+prefill GEMM and its split-K sum, the vocabulary gather, the QMoE kernels and the floors
 compute what the ordinary builds compute, bit for bit, and every wavefront of every logged launch
 writes a start no later than its end; launches captured into a graph write their slots again at
 each replay; launches beyond the slots run unstamped and are counted."""
@@ -149,7 +149,7 @@ def test_gather_and_qmoe_stamping_builds(ctx):
     ctx.synchronize()
     print("timeline qmoe", flush=True)
     assert np.array_equal(ys[0].numpy().view(np.uint16), ys[1].numpy().view(np.uint16))
-    _check_launches(tl, ["k_moe_gemm_f16", "k_moe_gemm_f16"])
+    _check_launches(tl, ["k_moe_route", "k_moe_plan", "k_moe_gemm_f16", "k_moe_gemm_f16", "k_moe_combine"])
     tl.free()
     for w in ws:
         w.free()

@@ -27,7 +27,7 @@ ACTIVATIONS = {"relu": 0, "gelu": 1, "silu": 2, "identity": 3, "swiglu": 4}
 # Kernel ids of the launch timeline (TMH_TL_*)
 TIMELINE_KERNELS = {1: "k_gemv_dot", 2: "k_gemv_dec", 3: "k_gemm_lds", 4: "k_splitk_reduce", 5: "k_moe_gemm_f16",
                     6: "k_floor_empty", 7: "k_floor_read", 8: "k_gather_bq_rows", 9: "k_floor_read_all",
-                    10: "k_floor_write"}
+                    10: "k_floor_write", 11: "k_moe_route", 12: "k_moe_plan", 13: "k_moe_combine"}
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int

@@ -14,8 +14,9 @@
 //
 // Layout on the device: the experts of one weight are one tmh_weight of E*N rows (expert e owns
 // rows e*N.. and 16-row tiles e*N/16..). A call sorts its T*k (token, slot) rows by expert, runs
-// each expert's rows against its tiles in work items of up to 32 rows, and keeps every
-// intermediate in expert order; the final sum reads them back per token, slot by slot.
+// each expert's rows against its tiles in work items of up to 32 or 64 rows, and keeps the
+// intermediates in expert order; the last product writes its rows back in (token, slot) order
+// (expert order on the general path), and the final sum reads them per token, slot by slot.
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
@@ -46,80 +47,120 @@ __device__ __forceinline__ float key_value(uint32_t key) {
   return __builtin_bit_cast(float, (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
 }
 
-typedef uint64_t u64x2_t __attribute__((ext_vector_type(2)));
+// The largest of the wavefront's 64 values, in every lane: a running maximum over rows of 16
+// lanes (row_shr 1, 2, 4, 8), across rows (row_bcast 15 and 31), read from lane 63. A lane with no
+// source lane keeps its own value.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  auto step = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+  const int x = static_cast<int>(v);
+  v = step(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(x, x, 0x111, 0xf, 0xf, false)));
+  v = step(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0x112, 0xf, 0xf, false)));
+  v = step(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0x114, 0xf, 0xf, false)));
+  v = step(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0x118, 0xf, 0xf, false)));
+  v = step(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0x142, 0xa, 0xf, false)));
+  v = step(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), 0x143, 0xc, 0xf, false)));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
 
 // One wavefront per token: the k largest router values (lower index first among equals), a
-// softmax over them in f32. Each expert's 64-bit key (value key, then the complement of its
-// index) goes to LDS, so all keys differ and "comes first in the stable descending order" is one
-// unsigned comparison; each lane ranks its experts against all keys and the experts ranked below
-// k are the selection, in rank order.
-template <int RDT>
-__global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ router, int T, int E, int k,
-                                                   int* __restrict__ topi, float* __restrict__ topw) {
-  __shared__ __align__(16) uint64_t keys[4][1024];
-  __shared__ float sel_v[4][32];
-  __shared__ int sel_i[4][32];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + w;
-  const bool live = t < T;
-  const int E2 = (E + 1) & ~1;  // padded with key 0, below every expert's key
-  if (live)
-    for (int e = lane; e < E2; e += 64)
-      keys[w][e] = e < E ? (static_cast<uint64_t>(order_key(load_as_f32<RDT>(router, static_cast<int64_t>(t) * E + e)))
-                            << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(e))
-                         : 0;
-  __syncthreads();
-  if (live)
-    for (int e = lane; e < E; e += 64) {
-      const uint64_t kx = keys[w][e];
-      int rank = 0;
-#pragma unroll 8
-      for (int e2 = 0; e2 < E2; e2 += 2) {
-        const u64x2_t y = *reinterpret_cast<const u64x2_t*>(&keys[w][e2]);
-        rank += (y[0] > kx ? 1 : 0) + (y[1] > kx ? 1 : 0);
-      }
-      if (rank < k) {
-        sel_v[w][rank] = key_value(static_cast<uint32_t>(kx >> 32));
-        sel_i[w][rank] = e;
+// softmax over them in f32. Lane l holds the order keys of experts l, l + 64, ... (EJ of them;
+// key 0, below every expert's key, past E). Round r takes the largest key left (a wavefront
+// maximum), the lowest expert index that holds it (the first 64-expert group whose ballot is not
+// empty, then its lowest lane), and sets that key to 0; lane r keeps the round's value and index.
+// (The body; k_moe_route and its stamping build k_moe_route_tl below are the kernels.)
+template <int RDT, int EJ>
+__device__ __forceinline__ void moe_route(const void* __restrict__ router, int T, int E, int k,
+                                          int* __restrict__ topi, float* __restrict__ topw) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  uint32_t key[EJ];
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) {
+    const int e = lane + 64 * j;
+    key[j] = e < E ? order_key(load_as_f32<RDT>(router, static_cast<int64_t>(t) * E + e)) : 0u;
+  }
+  float sel_v = 0.f;
+  int sel_i = 0;
+  for (int r = 0; r < k; ++r) {
+    uint32_t best = key[0];
+#pragma unroll
+    for (int j = 1; j < EJ; ++j) best = key[j] > best ? key[j] : best;
+    const uint32_t m = wave_max_u32(best);
+    int e = 0;
+    bool found = false;
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) {
+      const uint64_t b = __ballot(key[j] == m);
+      if (!found && b) {
+        e = 64 * j + __builtin_ctzll(b);
+        found = true;
       }
     }
-  __syncthreads();
-  if (!live) return;
-  const float mx = sel_v[w][0];
-  const float ex = lane < k ? expf(sel_v[w][lane] - mx) : 0.f;
+    e = e < E ? e : E - 1;  // (m is a key of an expert, so e < E already)
+#pragma unroll
+    for (int j = 0; j < EJ; ++j)
+      if (e == lane + 64 * j) key[j] = 0u;
+    if (lane == r) {
+      sel_v = key_value(m);
+      sel_i = e;
+    }
+  }
+  const float mx = __shfl(sel_v, 0);
+  const float ex = lane < k ? expf(sel_v - mx) : 0.f;
   float sum = ex;
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   if (lane < k) {
-    topi[t * k + lane] = sel_i[w][lane];
+    topi[t * k + lane] = sel_i;
     topw[t * k + lane] = ex / sum;
   }
+}
+
+// Inclusive prefix sum over the wavefront's 64 lanes: within rows of 16 (row_shr 1, 2, 4, 8),
+// then across rows (row_bcast 15 into rows 1 and 3, row_bcast 31 into rows 2 and 3). A lane with
+// no source lane adds 0.
+__device__ __forceinline__ int wave_inclusive_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
+  return v;
 }
 
 // One workgroup of 1024 threads (thread e for expert e): rows per expert, expert offsets (exclusive
 // prefix of the counts), the list of work items (expert << 16 | item of the expert, `rows` rows
 // each), and the position of every (token, slot) row in expert order (perm) with its inverse
-// (slot_pos). The prefix sums run per wavefront with shuffles, then across the 16 wavefronts.
-__global__ __launch_bounds__(1024) void k_moe_plan(int* __restrict__ counts, int E, int rows, const int* __restrict__ topi,
-                                                   int Tk, int* __restrict__ offsets, int* __restrict__ items,
-                                                   int* __restrict__ n_items, int* __restrict__ perm,
-                                                   int* __restrict__ slot_pos) {
+// (slot_pos). Each thread loads four rows' experts per round before its LDS atomics; up to 4096
+// rows the ids stay in registers from the count to the placement. The prefix sums run per
+// wavefront in DPP steps, then across the 16 wavefronts.
+// (The body; k_moe_plan and k_moe_plan_tl below are the kernels.)
+__device__ __forceinline__ void moe_plan(int* __restrict__ counts, int E, int rows, const int* __restrict__ topi,
+                                         int Tk, int* __restrict__ offsets, int* __restrict__ items,
+                                         int* __restrict__ n_items, int* __restrict__ perm,
+                                         int* __restrict__ slot_pos) {
+  constexpr int R = 4;
   __shared__ int first_s[1024], fill[1024], wsum_r[16], wsum_i[16];
   const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
   fill[e] = 0;
   __syncthreads();
-  for (int idx = e; idx < Tk; idx += 1024) atomicAdd(&fill[topi[idx]], 1);
+  int ex[R];
+  for (int base = 0; base < Tk; base += 1024 * R) {
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const int idx = base + u * 1024 + e;
+      ex[u] = idx < Tk ? topi[idx] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < R; ++u)
+      if (ex[u] >= 0) atomicAdd(&fill[ex[u]], 1);
+  }
   __syncthreads();
   const int c = fill[e];
   const int nb = (c + rows - 1) / rows;
   if (e < E) counts[e] = c;
-  int sr = c, si = nb;  // inclusive prefix sums of rows and items
-  for (int off = 1; off < 64; off <<= 1) {
-    const int r2 = __shfl_up(sr, off), i2 = __shfl_up(si, off);
-    if (lane >= off) {
-      sr += r2;
-      si += i2;
-    }
-  }
+  int sr = wave_inclusive_sum(c), si = wave_inclusive_sum(nb);  // inclusive prefix sums of rows and items
   if (lane == 63) {
     wsum_r[wave] = sr;
     wsum_i[wave] = si;
@@ -139,16 +180,17 @@ __global__ __launch_bounds__(1024) void k_moe_plan(int* __restrict__ counts, int
   first_s[e] = first_row;
   fill[e] = 0;
   __syncthreads();
-  // Four rows per thread and round, their expert ids loaded before the LDS atomics.
-  for (int base = 0; base < Tk; base += 4096) {
-    int ex[4];
+  const bool held = Tk <= 1024 * R;
+  for (int base = 0; base < Tk; base += 1024 * R) {
+    if (!held) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int idx = base + u * 1024 + e;
-      ex[u] = idx < Tk ? topi[idx] : -1;
+      for (int u = 0; u < R; ++u) {
+        const int idx = base + u * 1024 + e;
+        ex[u] = idx < Tk ? topi[idx] : -1;
+      }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < R; ++u) {
       if (ex[u] < 0) continue;
       const int idx = base + u * 1024 + e;
       const int pos = first_s[ex[u]] + atomicAdd(&fill[ex[u]], 1);
@@ -156,6 +198,39 @@ __global__ __launch_bounds__(1024) void k_moe_plan(int* __restrict__ counts, int
       slot_pos[idx] = pos;
     }
   }
+}
+
+// The routing and planning kernels and their stamping builds (each wavefront stamps after the body).
+template <int RDT, int EJ>
+__global__ __launch_bounds__(256) void k_moe_route(const void* __restrict__ router, int T, int E, int k,
+                                                   int* __restrict__ topi, float* __restrict__ topw) {
+  moe_route<RDT, EJ>(router, T, E, k, topi, topw);
+}
+
+template <int RDT, int EJ>
+__global__ __launch_bounds__(256) void k_moe_route_tl(const void* __restrict__ router, int T, int E, int k,
+                                                      int* __restrict__ topi, float* __restrict__ topw,
+                                                      uint32_t* __restrict__ tl) {
+  const TlStart t0 = tl_clock();
+  moe_route<RDT, EJ>(router, T, E, k, topi, topw);
+  tl_stamp(tl, t0);
+}
+
+__global__ __launch_bounds__(1024) void k_moe_plan(int* __restrict__ counts, int E, int rows, const int* __restrict__ topi,
+                                                   int Tk, int* __restrict__ offsets, int* __restrict__ items,
+                                                   int* __restrict__ n_items, int* __restrict__ perm,
+                                                   int* __restrict__ slot_pos) {
+  moe_plan(counts, E, rows, topi, Tk, offsets, items, n_items, perm, slot_pos);
+}
+
+__global__ __launch_bounds__(1024) void k_moe_plan_tl(int* __restrict__ counts, int E, int rows,
+                                                      const int* __restrict__ topi, int Tk, int* __restrict__ offsets,
+                                                      int* __restrict__ items, int* __restrict__ n_items,
+                                                      int* __restrict__ perm, int* __restrict__ slot_pos,
+                                                      uint32_t* __restrict__ tl) {
+  const TlStart t0 = tl_clock();
+  moe_plan(counts, E, rows, topi, Tk, offsets, items, n_items, perm, slot_pos);
+  tl_stamp(tl, t0);
 }
 
 // ------------------------------------------------------------------ activations
@@ -236,7 +311,8 @@ __device__ __forceinline__ void moe_gemm_f16(
     const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
     const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
     const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
-    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo, uint32_t* __restrict__ tl) {
+    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo,
+    const int* __restrict__ out_perm, uint32_t* __restrict__ tl) {
   const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
   constexpr int CW = 512 / BITS;
   constexpr int GW = CW / 4;
@@ -254,7 +330,8 @@ __device__ __forceinline__ void moe_gemm_f16(
     return;
   }
   const MoeItem it = moe_item(items, blockIdx.y, offsets, counts, ROWS);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, one LDS ring base
   const int r = lane & 15, g = lane >> 4;
   const int lt = blockIdx.x * 8 + wave;  // this wavefront's output tile within the expert
   const bool active = lt < out_tiles;
@@ -270,17 +347,18 @@ __device__ __forceinline__ void moe_gemm_f16(
     z_rsrc[v] = buffer_rsrc(v ? zp2 : zp, HAS_ZP ? n_params : 0u);
     tile[v] = static_cast<uint32_t>(it.e * tiles_per_expert + lt + (v ? tile_off2 : 0));
   }
-  // A pieces this thread brings to LDS: row p / PPR, piece p % PPR (rows past the item, and k
-  // past K, read zeros).
+  // A pieces this thread brings to LDS: row p / PPR, piece p % PPR of p = (tid + 512 l) mod
+  // PIECES (rows past the item, and k past K, read zeros). Where 512 * LOADS exceeds PIECES, two
+  // threads store the same piece, the same bytes.
   uint32_t a_src[LOADS];
   int a_dst[LOADS], a_k[LOADS];
 #pragma unroll
   for (int l = 0; l < LOADS; ++l) {
-    const int p = tid + 512 * l;
+    const int p = (tid + 512 * l) % PIECES;
     const int row = p / PPR, piece = p % PPR;
-    const int src = p < PIECES && row < it.rows ? (perm ? perm[it.row0 + row] / perm_div : it.row0 + row) : -1;
+    const int src = row < it.rows ? (perm ? perm[it.row0 + row] / perm_div : it.row0 + row) : -1;
     a_src[l] = src >= 0 ? static_cast<uint32_t>(src) * lda * 2 + piece * 16 : 0x80000000u;
-    a_dst[l] = p < PIECES ? row * ROWB + a_slot_moe<BITS>(row, piece) * 16 : -1;
+    a_dst[l] = row * ROWB + a_slot_moe<BITS>(row, piece) * 16;
     a_k[l] = piece * 8;
   }
   auto load_a = [&](uint32_t c, uint4_t (&v)[LOADS]) {
@@ -292,8 +370,7 @@ __device__ __forceinline__ void moe_gemm_f16(
   };
   auto store_a = [&](int buf, const uint4_t (&v)[LOADS]) {
 #pragma unroll
-    for (int l = 0; l < LOADS; ++l)
-      if (a_dst[l] >= 0) *reinterpret_cast<uint4_t*>(lds + buf * ROWS * ROWB + a_dst[l]) = v[l];
+    for (int l = 0; l < LOADS; ++l) *reinterpret_cast<uint4_t*>(lds + buf * ROWS * ROWB + a_dst[l]) = v[l];
   };
   struct WStage {
     uint4_t w[NW];
@@ -393,7 +470,8 @@ __device__ __forceinline__ void moe_gemm_f16(
     }
     const half2_t lo = {static_cast<_Float16>(y[0]), static_cast<_Float16>(y[1])};
     const half2_t hi = {static_cast<_Float16>(y[2]), static_cast<_Float16>(y[3])};
-    _Float16* dst = out + static_cast<int64_t>(it.row0 + i) * ldo + n;
+    const int orow = out_perm ? out_perm[it.row0 + i] : it.row0 + i;
+    _Float16* dst = out + static_cast<int64_t>(orow) * ldo + n;
     *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
   }
   if constexpr (TL) tl_stamp(tl, tl0);
@@ -407,10 +485,12 @@ __global__ __launch_bounds__(512) void k_moe_gemm_f16(
     const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
     const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
     const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
-    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo) {
+    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo,
+    const int* __restrict__ out_perm) {
   moe_gemm_f16<BITS, HAS_ZP, SPLIT, EPI, MT, false>(
       qt, sc, zp, qt2, sc2, zp2, tile_off2, ntiles, nchunks, nbc, bsc_shift, tiles_per_expert, out_tiles, A, a_rows, lda, perm,
-      perm_div, items, n_items, offsets, counts, bias1, bias2, bias_dt, bias_ld, act, alpha, beta, limit, out, ldo, nullptr);
+      perm_div, items, n_items, offsets, counts, bias1, bias2, bias_dt, bias_ld, act, alpha, beta, limit, out, ldo, out_perm,
+      nullptr);
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT>
@@ -421,10 +501,12 @@ __global__ __launch_bounds__(512) void k_moe_gemm_f16_tl(
     const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
     const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
     const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
-    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo, uint32_t* __restrict__ tl) {
+    int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo,
+    const int* __restrict__ out_perm, uint32_t* __restrict__ tl) {
   moe_gemm_f16<BITS, HAS_ZP, SPLIT, EPI, MT, true>(
       qt, sc, zp, qt2, sc2, zp2, tile_off2, ntiles, nchunks, nbc, bsc_shift, tiles_per_expert, out_tiles, A, a_rows, lda, perm,
-      perm_div, items, n_items, offsets, counts, bias1, bias2, bias_dt, bias_ld, act, alpha, beta, limit, out, ldo, tl);
+      perm_div, items, n_items, offsets, counts, bias1, bias2, bias_dt, bias_ld, act, alpha, beta, limit, out, ldo, out_perm,
+      tl);
 }
 
 // The same product for any float types (A in a_dt, weights dequantized in WDT, out in out_dt):
@@ -525,12 +607,14 @@ __global__ __launch_bounds__(256) void k_moe_activate(const void* __restrict__ h
 }
 
 // y[t][h] = sum over the token's slots j of weight_j * (o[row of (t, j)][h] + fc2 bias), in slot
-// order; a slot of weight 0 adds 0. V consecutive columns per thread.
+// order; a slot of weight 0 adds 0. V consecutive columns per thread. The row of (t, j) is
+// slot_pos[t * k + j] for o in expert order, t * k + j for o in token order (slot_pos null).
+// (The body; k_moe_combine and k_moe_combine_tl below are the kernels.)
 template <int DT, int V>
-__global__ __launch_bounds__(256) void k_moe_combine(const void* __restrict__ o, int H, const void* __restrict__ b2,
-                                                     int bias_dt, const int* __restrict__ topi,
-                                                     const float* __restrict__ topw, const int* __restrict__ slot_pos,
-                                                     int T, int k, void* __restrict__ y, bool y_vec) {
+__device__ __forceinline__ void moe_combine(const void* __restrict__ o, int H, const void* __restrict__ b2,
+                                            int bias_dt, const int* __restrict__ topi,
+                                            const float* __restrict__ topw, const int* __restrict__ slot_pos,
+                                            int T, int k, void* __restrict__ y, bool y_vec) {
   constexpr int JU = 8;  // slots whose loads are in flight together
   const int64_t idx = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * V;
   if (idx >= static_cast<int64_t>(T) * H) return;
@@ -549,7 +633,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const void* __restrict__ o,
       const int j = j0 + u < k ? j0 + u : k - 1;
       wgt[u] = rt<DT>(topw[t * k + j]);
       ex[u] = topi[t * k + j];
-      const int64_t row = slot_pos[t * k + j];
+      const int64_t row = slot_pos ? slot_pos[t * k + j] : t * k + j;
       if constexpr (DT == DT_F16 && V == 8) {
         const half8_t h8 = *reinterpret_cast<const half8_t*>(static_cast<const _Float16*>(o) + row * H + hc);
 #pragma unroll
@@ -581,6 +665,25 @@ __global__ __launch_bounds__(256) void k_moe_combine(const void* __restrict__ o,
   }
 }
 
+template <int DT, int V>
+__global__ __launch_bounds__(256) void k_moe_combine(const void* __restrict__ o, int H, const void* __restrict__ b2,
+                                                     int bias_dt, const int* __restrict__ topi,
+                                                     const float* __restrict__ topw, const int* __restrict__ slot_pos,
+                                                     int T, int k, void* __restrict__ y, bool y_vec) {
+  moe_combine<DT, V>(o, H, b2, bias_dt, topi, topw, slot_pos, T, k, y, y_vec);
+}
+
+template <int DT, int V>
+__global__ __launch_bounds__(256) void k_moe_combine_tl(const void* __restrict__ o, int H, const void* __restrict__ b2,
+                                                        int bias_dt, const int* __restrict__ topi,
+                                                        const float* __restrict__ topw,
+                                                        const int* __restrict__ slot_pos, int T, int k,
+                                                        void* __restrict__ y, bool y_vec, uint32_t* __restrict__ tl) {
+  const TlStart t0 = tl_clock();
+  moe_combine<DT, V>(o, H, b2, bias_dt, topi, topw, slot_pos, T, k, y, y_vec);
+  tl_stamp(tl, t0);
+}
+
 // ------------------------------------------------------------------ launchers
 
 int bsc_shift_moe(const tmh_weight* w) {
@@ -599,6 +702,7 @@ struct MoeEpilogue {
   int bias_dt = TMH_F32, bias_ld = 0, act = ACT_IDENTITY;
   float alpha = 1.f, beta = 0.f, limit = 0.f;
   int rows = 32;                   // rows per work item: 32 or 64
+  const int* out_perm = nullptr;   // output row of each sorted row (else the sorted row itself)
 };
 
 template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT>
@@ -613,7 +717,8 @@ void launch_moe_f16_e(const tmh_weight* w, int tpe, const void* A, int a_rows, i
       static_cast<const uint16_t*>(w2->d_scale), static_cast<const uint8_t*>(w2->d_zero), ep.tile_off2,               \
       static_cast<int>(w->ntiles), static_cast<int>(w->nchunks), w->nbc, bsc_shift_moe(w), tpe, ep.out_tiles,         \
       static_cast<const _Float16*>(A), a_rows, lda, perm, perm_div, items, n_items, offsets, counts, ep.bias1,        \
-      ep.bias2, ep.bias_dt, ep.bias_ld, ep.act, ep.alpha, ep.beta, ep.limit, static_cast<_Float16*>(out), ldo
+      ep.bias2, ep.bias_dt, ep.bias_ld, ep.act, ep.alpha, ep.beta, ep.limit, static_cast<_Float16*>(out), ldo,       \
+      ep.out_perm
   if (uint32_t* tl = timeline_slots(TMH_TL_MOE_GEMM, static_cast<int64_t>(grid.x) * grid.y * 8))
     k_moe_gemm_f16_tl<BITS, HAS_ZP, SPLIT, EPI, MT><<<grid, 512, 0, s>>>(TMH_MOE_ARGS, tl);
   else
@@ -883,12 +988,28 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
   void* o = ws + o_o;
   const int ti = static_cast<int>(T), ki = k, ei = static_cast<int>(E), tki = static_cast<int>(tk);
   const unsigned route_grid = static_cast<unsigned>((T + 3) / 4);
-  switch (router_dtype) {
-    case TMH_F16: k_moe_route<DT_F16><<<route_grid, 256, 0, s>>>(d_router, ti, ei, ki, topi, topw); break;
-    case TMH_BF16: k_moe_route<DT_BF16><<<route_grid, 256, 0, s>>>(d_router, ti, ei, ki, topi, topw); break;
-    default: k_moe_route<DT_F32><<<route_grid, 256, 0, s>>>(d_router, ti, ei, ki, topi, topw);
+  {
+    // Router keys per lane: 2 up to 128 experts, 4 up to 256, 16 up to 1024.
+    uint32_t* tl = timeline_slots(TMH_TL_MOE_ROUTE, static_cast<int64_t>(route_grid) * 4);
+#define TMH_MOE_ROUTE_J(RDT, EJ)                                                                              \
+  if (tl) k_moe_route_tl<RDT, EJ><<<route_grid, 256, 0, s>>>(d_router, ti, ei, ki, topi, topw, tl);             \
+  else k_moe_route<RDT, EJ><<<route_grid, 256, 0, s>>>(d_router, ti, ei, ki, topi, topw)
+#define TMH_MOE_ROUTE(RDT)                 \
+  if (ei <= 128) TMH_MOE_ROUTE_J(RDT, 2);  \
+  else if (ei <= 256) TMH_MOE_ROUTE_J(RDT, 4); \
+  else TMH_MOE_ROUTE_J(RDT, 16)
+    switch (router_dtype) {
+      case TMH_F16: TMH_MOE_ROUTE(DT_F16); break;
+      case TMH_BF16: TMH_MOE_ROUTE(DT_BF16); break;
+      default: TMH_MOE_ROUTE(DT_F32);
+    }
+#undef TMH_MOE_ROUTE
+#undef TMH_MOE_ROUTE_J
   }
-  k_moe_plan<<<1, 1024, 0, s>>>(counts, ei, rows, topi, tki, offsets, items, n_items, perm, slot_pos);
+  if (uint32_t* tl = timeline_slots(TMH_TL_MOE_PLAN, 16))
+    k_moe_plan_tl<<<1, 1024, 0, s>>>(counts, ei, rows, topi, tki, offsets, items, n_items, perm, slot_pos, tl);
+  else
+    k_moe_plan<<<1, 1024, 0, s>>>(counts, ei, rows, topi, tki, offsets, items, n_items, perm, slot_pos);
   TMH_TRY(check_launch(ctx, "k_moe_plan"));
   const int hi = static_cast<int>(H), n1i = static_cast<int>(n1), inti = static_cast<int>(inter);
   // fc1 (and fc3) with the activation in the product's epilogue where the fast path allows it:
@@ -939,15 +1060,25 @@ int tmh_qmoe(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t T, int64_t H, c
 #undef TMH_MOE_ACT
     TMH_TRY(check_launch(ctx, "k_moe_activate"));
   }
+  // fc2 on the fast path writes each row at its (token, slot) index, so the final sum reads a
+  // token's rows in one run; the general path keeps expert order.
+  const bool fc2_fast = moe_fast(fc2, x_dtype, hact, tki, inti);
   MoeEpilogue ep2;
   ep2.rows = rows;
+  ep2.out_perm = fc2_fast ? perm : nullptr;
+  const int* o_rows = fc2_fast ? nullptr : slot_pos;
   moe_gemm(fc2, ei, hact, x_dtype, tki, inti, nullptr, 1, items, n_items, max_items, offsets, counts, o, hi, s, ep2);
   TMH_TRY(check_launch(ctx, "k_moe_gemm (fc2)"));
   // H is a multiple of 16: eight columns per thread.
   const unsigned out_grid = static_cast<unsigned>((T * H / 8 + 255) / 256);
-#define TMH_MOE_SUM(DT) \
-  k_moe_combine<DT, 8><<<out_grid, 256, 0, s>>>(o, hi, d_fc2_bias, bias_dtype, topi, topw, slot_pos, ti, ki, d_y, \
-                                               reinterpret_cast<uintptr_t>(d_y) % 16 == 0)
+  uint32_t* tl_sum = timeline_slots(TMH_TL_MOE_COMBINE, static_cast<int64_t>(out_grid) * 4);
+  const bool y_vec = reinterpret_cast<uintptr_t>(d_y) % 16 == 0;
+#define TMH_MOE_SUM(DT)                                                                                            \
+  if (tl_sum)                                                                                                      \
+    k_moe_combine_tl<DT, 8><<<out_grid, 256, 0, s>>>(o, hi, d_fc2_bias, bias_dtype, topi, topw, o_rows, ti, ki, d_y,   \
+                                                    y_vec, tl_sum);                                                \
+  else                                                                                                             \
+    k_moe_combine<DT, 8><<<out_grid, 256, 0, s>>>(o, hi, d_fc2_bias, bias_dtype, topi, topw, o_rows, ti, ki, d_y, y_vec)
   switch (x_dtype) {
     case TMH_F16: TMH_MOE_SUM(DT_F16); break;
     case TMH_BF16: TMH_MOE_SUM(DT_BF16); break;
