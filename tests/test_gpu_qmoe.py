@@ -131,6 +131,25 @@ def _check_qmoe(ctx, case):
     assert np.abs(got - ref).max() <= tol, f"max difference {np.abs(got - ref).max()} (max |ref| {scale})"
 
 
+# Several groups of eight output tiles per workgroup, one after the other in one chunk pipeline
+# (TMH_MOE_GPW; by default the stored products of 16 groups or more run four): groups that do not
+# divide evenly, a last group with idle wavefronts (tiles per expert not a multiple of 8), every
+# epilogue (swiglu of fc1 and fc3, an activation, the stored fc2).
+GPW_CASES = [
+    ("f16", 16, 4, 40, 176, 64, "swiglu", 0, True, 4, 32, True, False, 0.0),
+    ("f16", 8, 2, 70, 400, 208, "gelu", 0, False, 4, 32, False, True, 0.0),
+    ("f16", 12, 3, 33, 272, 96, "silu", 0, False, 8, 64, True, False, 0.0),
+]
+
+
+@pytest.mark.parametrize("gpw", [2, 3])
+@pytest.mark.parametrize("case", GPW_CASES, ids=lambda c: "{}_E{}_k{}_T{}_H{}_N{}_{}".format(*c[:7]))
+def test_qmoe_several_tile_groups_per_workgroup(ctx, monkeypatch, case, gpw):
+    monkeypatch.setenv("TMH_MOE_GPW", str(gpw))
+    print(f"qmoe {gpw} tile groups per workgroup {case}", flush=True)
+    _check_qmoe(ctx, case)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_qmoe_routing_ties(ctx, dtype):
     """Tied router values, +0 and -0 among them: the lower expert index wins the tie

@@ -21,6 +21,7 @@
 #include <cmath>
 #include <type_traits>
 #include <cstdio>
+#include <cstdlib>
 #include <vector>
 
 #include "tmh_device.h"
@@ -307,7 +308,7 @@ template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT, bool TL>
 __device__ __forceinline__ void moe_gemm_f16(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const uint4_t* __restrict__ qt2, const uint16_t* __restrict__ sc2, const uint8_t* __restrict__ zp2,
-    int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles,
+    int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles, int gpw,
     const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
     const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
     const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
@@ -333,19 +334,23 @@ __device__ __forceinline__ void moe_gemm_f16(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, one LDS ring base
   const int r = lane & 15, g = lane >> 4;
-  const int lt = blockIdx.x * 8 + wave;  // this wavefront's output tile within the expert
-  const bool active = lt < out_tiles;
+  // The workgroup's groups of eight output tiles: g0 .. g0 + ng - 1, one after the other through
+  // one chunk pipeline (the next group's first weights in flight during the last chunk).
+  const int g0 = blockIdx.x * gpw;
+  const int ng = min(gpw, (out_tiles + 7) / 8 - g0);
+  auto lt_of = [&](int gi) { return (g0 + gi) * 8 + wave; };  // this wavefront's output tile within the expert
+  auto active_g = [&](int gi) { return lt_of(gi) < out_tiles; };
   const uint32_t nch = static_cast<uint32_t>(nchunks);
   const uint32_t n_params = static_cast<uint32_t>(ntiles) * nch * nbc * 16;
   const auto a_rsrc = buffer_rsrc(A, static_cast<uint32_t>(a_rows) * lda * 2);
   __amdgpu_buffer_rsrc_t q_rsrc[NW], s_rsrc[NW], z_rsrc[NW];
-  uint32_t tile[NW];
+  uint32_t tile0[NW];  // the weight tiles of group 0; group gi adds 8 gi
 #pragma unroll
   for (int v = 0; v < NW; ++v) {
     q_rsrc[v] = buffer_rsrc(v ? qt2 : qt, static_cast<uint32_t>(ntiles) * nch * 1024);
     s_rsrc[v] = buffer_rsrc(v ? sc2 : sc, n_params * 2);
     z_rsrc[v] = buffer_rsrc(v ? zp2 : zp, HAS_ZP ? n_params : 0u);
-    tile[v] = static_cast<uint32_t>(it.e * tiles_per_expert + lt + (v ? tile_off2 : 0));
+    tile0[v] = static_cast<uint32_t>(it.e * tiles_per_expert + lt_of(0) + (v ? tile_off2 : 0));
   }
   // A pieces this thread brings to LDS: row p / PPR, piece p % PPR of p = (tid + 512 l) mod
   // PIECES (rows past the item, and k past K, read zeros). Where 512 * LOADS exceeds PIECES, two
@@ -376,13 +381,14 @@ __device__ __forceinline__ void moe_gemm_f16(
     uint4_t w[NW];
     uint32_t s[NW][NJ], z[NW][NJ];
   };
-  auto load_w = [&](uint32_t c, WStage& st) {
+  auto load_w = [&](int gi, uint32_t c, WStage& st) {
 #pragma unroll
     for (int v = 0; v < NW; ++v) {
-      st.w[v] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc[v], (tile[v] * nch * 64 + lane) * 16, c * 1024, 0);
+      const uint32_t tile = tile0[v] + 8u * static_cast<uint32_t>(gi);
+      st.w[v] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc[v], (tile * nch * 64 + lane) * 16, c * 1024, 0);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const uint32_t e = ((tile[v] * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
+        const uint32_t e = ((tile * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
         st.s[v][j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc[v], e * 2, 0, 0);
         if constexpr (HAS_ZP) st.z[v][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc[v], e, 0, 0);
       }
@@ -393,24 +399,59 @@ __device__ __forceinline__ void moe_gemm_f16(
   for (int v = 0; v < NW; ++v)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[v][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  // The chunk loop, specialized for the m-tiles that hold rows of this item (MA of MT, uniform
-  // per workgroup): an item of 17-32 rows runs half the MFMAs and LDS reads of a full one.
+  // The epilogue of group gi: lane (16g + r) holds rows mt*16 + r and columns lt*16 + 4g .. +3.
+  auto store_group = [&](int gi) {
+    const int n = lt_of(gi) * 16 + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int i = mt * 16 + r;
+      if (i >= it.rows) continue;
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float h = rt<DT_F16>(acc[0][mt][e]);
+        if (EPI != EPI_STORE && bias1)
+          h = rt<DT_F16>(h + load_float_rt(bias1, bias_dt, static_cast<int64_t>(it.e) * bias_ld + n + e));
+        float l = 0.f;
+        if constexpr (EPI == EPI_GLU) {
+          l = rt<DT_F16>(acc[NW - 1][mt][e]);
+          if (bias2)
+            l = rt<DT_F16>(l + load_float_rt(bias2, bias_dt, static_cast<int64_t>(it.e) * bias_ld + n + e + tile_off2 * 16));
+        }
+        y[e] = EPI == EPI_STORE ? h : activate<DT_F16>(act, h, l, alpha, beta, limit);
+      }
+      const half2_t lo = {static_cast<_Float16>(y[0]), static_cast<_Float16>(y[1])};
+      const half2_t hi = {static_cast<_Float16>(y[2]), static_cast<_Float16>(y[3])};
+      const int orow = out_perm ? out_perm[it.row0 + i] : it.row0 + i;
+      _Float16* dst = out + static_cast<int64_t>(orow) * ldo + n;
+      *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+    }
+  };
+  // The chunk loop over the workgroup's groups (steps s: group s / nch, chunk s % nch),
+  // specialized for the m-tiles that hold rows of this item (MA of MT, uniform per workgroup): an
+  // item of 17-32 rows runs half the MFMAs and LDS reads of a full one.
   auto run = [&](auto ma) {
     constexpr int MA = decltype(ma)::value;
     uint4_t av[LOADS];
     WStage cur, next;
     load_a(0, av);
-    if (active) load_w(0, cur);
+    if (active_g(0)) load_w(0, 0, cur);
     store_a(0, av);
     __syncthreads();
-    for (uint32_t c = 0; c < nch; ++c) {
-      const bool more = c + 1 < nch;
+    const uint32_t total = static_cast<uint32_t>(ng) * nch;
+    uint32_t c = 0;
+    int gi = 0;
+    for (uint32_t s = 0; s < total; ++s) {
+      const bool more = s + 1 < total;
+      const bool last_chunk = c + 1 == nch;
+      const uint32_t c1 = last_chunk ? 0u : c + 1;
+      const int gi1 = last_chunk ? gi + 1 : gi;
       if (more) {
-        load_a(c + 1, av);
-        if (active) load_w(c + 1, next);
+        load_a(c1, av);
+        if (active_g(gi1)) load_w(gi1, c1, next);
       }
-      if (active) {
-        const uint8_t* abase = lds + (c & 1) * ROWS * ROWB;
+      if (active_g(gi)) {
+        const uint8_t* abase = lds + (s & 1) * ROWS * ROWB;
 #pragma unroll
         for (int i = 0; i < STEPS; ++i) {
           const int piece = g * (GW / 8) + i;
@@ -429,10 +470,19 @@ __device__ __forceinline__ void moe_gemm_f16(
               acc[v][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[mt], acc[v][mt], 0, 0, 0);
           }
         }
+        if (last_chunk) {
+          store_group(gi);
+#pragma unroll
+          for (int v = 0; v < NW; ++v)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[v][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+        }
       }
-      if (more) store_a((c + 1) & 1, av);
+      if (more) store_a((s + 1) & 1, av);
       __syncthreads();
       if (more) cur = next;
+      c = c1;
+      gi = gi1;
     }
   };
   const int used = (it.rows + 15) / 16;
@@ -444,36 +494,6 @@ __device__ __forceinline__ void moe_gemm_f16(
   } else {
     run(std::integral_constant<int, 1>{});
   }
-  if (!active) {
-    if constexpr (TL) tl_stamp(tl, tl0);
-    return;
-  }
-  // Lane (16g + r) holds rows mt*16 + r and columns lt*16 + 4g .. +3.
-  const int n = lt * 16 + 4 * g;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int i = mt * 16 + r;
-    if (i >= it.rows) continue;
-    float y[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float h = rt<DT_F16>(acc[0][mt][e]);
-      if (EPI != EPI_STORE && bias1)
-        h = rt<DT_F16>(h + load_float_rt(bias1, bias_dt, static_cast<int64_t>(it.e) * bias_ld + n + e));
-      float l = 0.f;
-      if constexpr (EPI == EPI_GLU) {
-        l = rt<DT_F16>(acc[NW - 1][mt][e]);
-        if (bias2)
-          l = rt<DT_F16>(l + load_float_rt(bias2, bias_dt, static_cast<int64_t>(it.e) * bias_ld + n + e + tile_off2 * 16));
-      }
-      y[e] = EPI == EPI_STORE ? h : activate<DT_F16>(act, h, l, alpha, beta, limit);
-    }
-    const half2_t lo = {static_cast<_Float16>(y[0]), static_cast<_Float16>(y[1])};
-    const half2_t hi = {static_cast<_Float16>(y[2]), static_cast<_Float16>(y[3])};
-    const int orow = out_perm ? out_perm[it.row0 + i] : it.row0 + i;
-    _Float16* dst = out + static_cast<int64_t>(orow) * ldo + n;
-    *reinterpret_cast<uint2*>(dst) = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-  }
   if constexpr (TL) tl_stamp(tl, tl0);
 }
 
@@ -481,14 +501,15 @@ template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT>
 __global__ __launch_bounds__(512) void k_moe_gemm_f16(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const uint4_t* __restrict__ qt2, const uint16_t* __restrict__ sc2, const uint8_t* __restrict__ zp2,
-    int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles,
+    int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles, int gpw,
     const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
     const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
     const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
     int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo,
     const int* __restrict__ out_perm) {
   moe_gemm_f16<BITS, HAS_ZP, SPLIT, EPI, MT, false>(
-      qt, sc, zp, qt2, sc2, zp2, tile_off2, ntiles, nchunks, nbc, bsc_shift, tiles_per_expert, out_tiles, A, a_rows, lda, perm,
+      qt, sc, zp, qt2, sc2, zp2, tile_off2, ntiles, nchunks, nbc, bsc_shift, tiles_per_expert, out_tiles, gpw, A, a_rows,
+      lda, perm,
       perm_div, items, n_items, offsets, counts, bias1, bias2, bias_dt, bias_ld, act, alpha, beta, limit, out, ldo, out_perm,
       nullptr);
 }
@@ -497,14 +518,15 @@ template <int BITS, bool HAS_ZP, bool SPLIT, int EPI, int MT>
 __global__ __launch_bounds__(512) void k_moe_gemm_f16_tl(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const uint4_t* __restrict__ qt2, const uint16_t* __restrict__ sc2, const uint8_t* __restrict__ zp2,
-    int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles,
+    int tile_off2, int ntiles, int nchunks, int nbc, int bsc_shift, int tiles_per_expert, int out_tiles, int gpw,
     const _Float16* __restrict__ A, int a_rows, int lda, const int* __restrict__ perm, int perm_div,
     const int* __restrict__ items, const int* __restrict__ n_items, const int* __restrict__ offsets,
     const int* __restrict__ counts, const void* __restrict__ bias1, const void* __restrict__ bias2, int bias_dt,
     int bias_ld, int act, float alpha, float beta, float limit, _Float16* __restrict__ out, int ldo,
     const int* __restrict__ out_perm, uint32_t* __restrict__ tl) {
   moe_gemm_f16<BITS, HAS_ZP, SPLIT, EPI, MT, true>(
-      qt, sc, zp, qt2, sc2, zp2, tile_off2, ntiles, nchunks, nbc, bsc_shift, tiles_per_expert, out_tiles, A, a_rows, lda, perm,
+      qt, sc, zp, qt2, sc2, zp2, tile_off2, ntiles, nchunks, nbc, bsc_shift, tiles_per_expert, out_tiles, gpw, A, a_rows,
+      lda, perm,
       perm_div, items, n_items, offsets, counts, bias1, bias2, bias_dt, bias_ld, act, alpha, beta, limit, out, ldo, out_perm,
       tl);
 }
@@ -710,12 +732,18 @@ void launch_moe_f16_e(const tmh_weight* w, int tpe, const void* A, int a_rows, i
                       const int* items, const int* n_items, int max_items, const int* offsets, const int* counts,
                       void* out, int ldo, const MoeEpilogue& ep, hipStream_t s) {
   const tmh_weight* w2 = ep.w2 ? ep.w2 : w;
-  const dim3 grid(static_cast<unsigned>((ep.out_tiles + 7) / 8), static_cast<unsigned>(max_items));
+  // Groups of eight output tiles per workgroup, one after the other: the stored products (fc2,
+  // many groups per item) run four, so the workgroups' prologues and the last partial round of
+  // workgroups shrink; the others one.
+  const int groups = (ep.out_tiles + 7) / 8;
+  const char* gpw_env = std::getenv("TMH_MOE_GPW");
+  const int gpw = gpw_env ? std::max(1, std::atoi(gpw_env)) : (EPI == EPI_STORE && groups >= 16 ? 4 : 1);
+  const dim3 grid(static_cast<unsigned>((groups + gpw - 1) / gpw), static_cast<unsigned>(max_items));
 #define TMH_MOE_ARGS                                                                                                   \
   reinterpret_cast<const uint4_t*>(w->d_q), static_cast<const uint16_t*>(w->d_scale),                                 \
       static_cast<const uint8_t*>(w->d_zero), reinterpret_cast<const uint4_t*>(w2->d_q),                              \
       static_cast<const uint16_t*>(w2->d_scale), static_cast<const uint8_t*>(w2->d_zero), ep.tile_off2,               \
-      static_cast<int>(w->ntiles), static_cast<int>(w->nchunks), w->nbc, bsc_shift_moe(w), tpe, ep.out_tiles,         \
+      static_cast<int>(w->ntiles), static_cast<int>(w->nchunks), w->nbc, bsc_shift_moe(w), tpe, ep.out_tiles, gpw,    \
       static_cast<const _Float16*>(A), a_rows, lda, perm, perm_div, items, n_items, offsets, counts, ep.bias1,        \
       ep.bias2, ep.bias_dt, ep.bias_ld, ep.act, ep.alpha, ep.beta, ep.limit, static_cast<_Float16*>(out), ldo,       \
       ep.out_perm
