@@ -117,11 +117,12 @@ bool dot_for_one_row() {
 template <int BITS, bool HAS_ZP, bool SPLIT>
 void launch_bits(const DecArgs& d, int64_t M, int num_cus, hipStream_t s) {
   const int64_t nch = d.nch;
-  // Wavefronts of the one-shot shape per CU up to which a grid counts as resident: 24, or 10 for
-  // one row of A, whose dot-product kernel streams a grid of that size faster (the merged
-  // Qwen3-0.6B gate/up projection, 384 tiles x 8 chunks: 3.01 against 3.03 us per merged launch
-  // on average; at M = 8 and 16 the one-shot shape stays faster there, 3.37 against 3.52 us).
-  const int64_t resident = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * (M == 1 ? 10 : 24);
+  // Wavefronts of the one-shot shape per CU up to which a grid counts as resident: 24, or 16 for
+  // one row of A (the merged Qwen3-0.6B gate/up projection, 384 tiles x 8 chunks, runs the
+  // one-shot shape with its one A load per chunk: merged launches 2.85 against 2.87 us on average
+  // with the streaming shape; at M = 8 and 16 the one-shot shape is faster there too, 3.37
+  // against 3.52 us).
+  const int64_t resident = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * (M == 1 ? 16 : 24);
   const bool resident_grid = static_cast<int64_t>(d.ntiles) * std::min<int64_t>(nch, 16) <= resident;
   if constexpr (BITS != 2 && !SPLIT) {
     // One row of A: the dot-product kernel. Over a streaming grid two chunks per wavefront load
