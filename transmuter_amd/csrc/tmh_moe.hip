@@ -132,7 +132,8 @@ __device__ __forceinline__ int wave_inclusive_sum(int v) {
 
 // One workgroup of 1024 threads (thread e for expert e): rows per expert, expert offsets (exclusive
 // prefix of the counts), the list of work items (expert << 16 | item of the expert, `rows` rows
-// each), and the position of every (token, slot) row in expert order (perm) with its inverse
+// each; the items with the most 16-row m-tiles first), and the position of every (token, slot)
+// row in expert order (perm) with its inverse
 // (slot_pos). Each thread loads four rows' experts per round before its LDS atomics; up to 4096
 // rows the ids stay in registers from the count to the placement. The prefix sums run per
 // wavefront in DPP steps, then across the 16 wavefronts.
@@ -142,9 +143,10 @@ __device__ __forceinline__ void moe_plan(int* __restrict__ counts, int E, int ro
                                          int* __restrict__ n_items, int* __restrict__ perm,
                                          int* __restrict__ slot_pos) {
   constexpr int R = 4;
-  __shared__ int first_s[1024], fill[1024], wsum_r[16], wsum_i[16];
+  __shared__ int first_s[1024], fill[1024], wsum_r[16], wsum_i[16], cls_next[5];
   const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
   fill[e] = 0;
+  if (e < 5) cls_next[e] = 0;
   __syncthreads();
   int ex[R];
   for (int base = 0; base < Tk; base += 1024 * R) {
@@ -161,6 +163,15 @@ __device__ __forceinline__ void moe_plan(int* __restrict__ counts, int E, int ro
   const int c = fill[e];
   const int nb = (c + rows - 1) / rows;
   if (e < E) counts[e] = c;
+  // Work items in descending order of their 16-row m-tiles (the heaviest first: the products'
+  // workgroups run in item order, so the last ones to start are light). An expert's items are
+  // full but its last (q_last m-tiles); the order within a class is the atomics' (any order
+  // computes the same outputs).
+  const int q_full = rows / 16, q_last = nb > 0 ? (c - (nb - 1) * rows + 15) / 16 : 0;
+  if (e < E && nb > 0) {
+    if (nb > 1) atomicAdd(&cls_next[q_full], nb - 1);
+    atomicAdd(&cls_next[q_last], 1);
+  }
   int sr = wave_inclusive_sum(c), si = wave_inclusive_sum(nb);  // inclusive prefix sums of rows and items
   if (lane == 63) {
     wsum_r[wave] = sr;
@@ -172,15 +183,23 @@ __device__ __forceinline__ void moe_plan(int* __restrict__ counts, int E, int ro
     si += wsum_i[w2];
   }
   const int first_row = sr - c;
-  if (e < E) {
-    offsets[e] = first_row;
-    const int first = si - nb;
-    for (int b = 0; b < nb; ++b) items[first + b] = (e << 16) | b;
-  }
+  if (e < E) offsets[e] = first_row;
   if (e == 1023) *n_items = si;
+  if (e == 0) {  // each class's first item position, the classes in descending order
+    int run = 0;
+    for (int q = 4; q >= 1; --q) {
+      const int n = cls_next[q];
+      cls_next[q] = run;
+      run += n;
+    }
+  }
   first_s[e] = first_row;
   fill[e] = 0;
   __syncthreads();
+  if (e < E && nb > 0) {
+    for (int b = 0; b + 1 < nb; ++b) items[atomicAdd(&cls_next[q_full], 1)] = (e << 16) | b;
+    items[atomicAdd(&cls_next[q_last], 1)] = (e << 16) | (nb - 1);
+  }
   const bool held = Tk <= 1024 * R;
   for (int base = 0; base < Tk; base += 1024 * R) {
     if (!held) {
