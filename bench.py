@@ -1162,7 +1162,7 @@ def main():
                    help="print a markdown summary of rocprofv3 output: a kernel_stats.csv, then --pmc directories")
     p.add_argument("--timeline", choices=["decode", "vocab", "prefill", "moe"],
                    help="time a workload's kernels inside its graph replays (stamping builds) and write markdown")
-    p.add_argument("--out", help="file the --timeline markdown goes to (default: gpurun_out/timeline_KIND.md)")
+    p.add_argument("--out", help="file the --timeline markdown goes to (default: timeline_KIND.md in the working directory)")
     p.add_argument("--no-timeline", action="store_true", help="skip the in-graph kernel times of the headline")
     args = p.parse_args()
     if args.traffic:
@@ -1204,8 +1204,9 @@ def main():
                  "vocab": "151936 x 1024 lm_head and vocabulary gather, timed inside the graph replays",
                  "prefill": "SmolLM3-3B q4 prefill projections, timed inside the graph replays",
                  "moe": "Qwen3-30B-A3B QMoE layer (512 tokens), timed inside the graph replays"}[args.timeline]
-        out = args.out or os.path.join(ROOT, "gpurun_out", f"timeline_{args.timeline}.md")
-        os.makedirs(os.path.dirname(out), exist_ok=True)
+        out = args.out or f"timeline_{args.timeline}.md"
+        if os.path.dirname(out):
+            os.makedirs(os.path.dirname(out), exist_ok=True)
         with open(out, "w") as f:
             f.write(timeline_markdown(title, f"python bench.py --timeline {args.timeline}", parts, TIMELINE_NOTES))
         log(f"wrote {out}")
