@@ -14,10 +14,11 @@
 // A fragments: lane (g, r) needs A[r][chunk*CW + g*GW + 8i ..] for step i. With ALDS false each
 // lane loads its own four 16-byte pieces (16 rows x 4 scattered pieces per instruction, cheap
 // while few rows are real). With ALDS true (M > 4) a wavefront loads its chunk's rows as whole
-// 256-byte rows (4 rows per instruction, contiguous), writes them to its own LDS area and reads
-// the fragments back (XOR-swizzled by row, frag_swizzle; no barrier, as a wavefront's LDS accesses
-// stay in order, only a wavefront-scope fence against compiler reordering).
-// At M = 16 that takes a 1024 -> 3072 launch from 3.63 to 3.25 us; at M <= 4 it costs 0.03-0.16 us.
+// 256-byte rows (4 rows per instruction, contiguous) straight into its own LDS area
+// (buffer_load ... lds, XOR-swizzled by row, frag_swizzle), waits for them and reads the fragments
+// back (no barrier: the area is the wavefront's own). At M = 16 that takes a 1024 -> 3072 launch
+// from 3.63 to 3.25 us (through registers and ds_write) and 3.10 us (by DMA); at M <= 4 it costs
+// 0.03-0.16 us.
 //
 // A reads stop at K (a multiple of 8): values past K in a row of A (the next row, or padding
 // when lda > K) read as zeros, since the weights' padding past K is not zero.
@@ -91,30 +92,17 @@ __device__ __forceinline__ void gemv_dec(
         }
       }
       if constexpr (ALDS) {
-        // Rows of the chunk in order: instruction j loads rows (64/RB)*j + lane/RB, piece lane%RB.
+        // The chunk's rows go global -> LDS by buffer_load ... lds, 16 bytes a lane: instruction j
+        // fills rows (64/RB)*j + lane/RB, slot lane%RB, each lane loading the piece that belongs
+        // in its slot of the swizzled layout (the swizzle is its own inverse).
         constexpr int RPI = 64 / RB;
-        uint4_t rows[16 / RPI];
-#pragma unroll
-        for (int j = 0; j < 16 / RPI; ++j) {
-          const uint32_t row = RPI * j + lane / RB, p = lane % RB;
-          const uint32_t k = (base + u) * CW + 8 * p;  // K is a multiple of 8: a piece is in or past K
-          const uint32_t off = (base + u < nch && row < M && k < K) ? row * lda * 2 + k * 2 : 0x80000000u;
-          rows[j] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0);
-        }
         uint4_t* mine = a_lds + wave * A_WAVE + u * 16 * RB;
 #pragma unroll
         for (int j = 0; j < 16 / RPI; ++j) {
-          const uint32_t row = RPI * j + lane / RB, p = lane % RB;
-          mine[row * RB + (p ^ frag_swizzle<RB>(row))] = rows[j];
-        }
-        // Lanes read pieces that other lanes of the wavefront wrote: the fence keeps the compiler
-        // from moving those reads above the writes (the LDS itself serves a wavefront in order).
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int i = 0; i < STEPS; ++i) {
-          const uint32_t p = g * (GW / 8) + i;
-          af[u][i] = __builtin_bit_cast(half8_t, mine[r * RB + (p ^ frag_swizzle<RB>(r))]);
+          const uint32_t row = RPI * j + lane / RB, p = (lane % RB) ^ frag_swizzle<RB>(row);
+          const uint32_t k = (base + u) * CW + 8 * p;  // K is a multiple of 8: a piece is in or past K
+          const uint32_t off = (base + u < nch && row < M && k < K) ? row * lda * 2 + k * 2 : 0x80000000u;
+          lds_dma16(a_rsrc, reinterpret_cast<uint8_t*>(mine + RPI * j * RB), off, 0);
         }
       } else {
 #pragma unroll
@@ -122,6 +110,22 @@ __device__ __forceinline__ void gemv_dec(
           const uint32_t k = (base + u) * CW + g * GW + 8 * i;
           const uint32_t off = base + u < nch && k < K ? a_row + k * 2 : 0x80000000u;
           af[u][i] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
+        }
+      }
+    }
+    if constexpr (ALDS) {
+      // The DMAs have written the chunks' rows once no vector-memory operation is outstanding
+      // (the weights, issued first, are needed next anyway); lanes then read pieces that other
+      // lanes' loads wrote.
+      __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint4_t* mine = a_lds + wave * A_WAVE + u * 16 * RB;
+#pragma unroll
+        for (int i = 0; i < STEPS; ++i) {
+          const uint32_t p = g * (GW / 8) + i;
+          af[u][i] = __builtin_bit_cast(half8_t, mine[r * RB + (p ^ frag_swizzle<RB>(r))]);
         }
       }
     }
