@@ -159,8 +159,9 @@ void tmh_weight_free(tmh_weight* w);
 
 /*
  * The host half of tmh_weight_upload_nbits: validates the same arguments and writes the
- * tiled weights, the per-block scales (weight_dtype) and the zero points (u8 for packed, f32
- * for float zero points) into caller buffers, without touching a device. With all three
+ * tiled weights, the per-block scales (weight_dtype) and the zero points (`bits` bits each for
+ * packed ones, as many a byte as the reference's rows hold; f32 for float zero points) into
+ * caller buffers, without touching a device. With all three
  * buffers NULL it only stores the byte counts; otherwise *q_bytes, *scale_bytes and
  * *zero_bytes give the buffer capacities on entry and the bytes written on return. A NIF can
  * pack on a host thread and upload later. No reference counterpart beyond move/2's

@@ -112,7 +112,8 @@ def reference_layout(b, scales, zp, k, n, bits, bs):
     """The tiled layout written out from its definition: tiles of 16 rows, chunks of 64 bytes
     per row, lane l = 16g + r holding row r's bytes 16g..16g+15 of the chunk, sub-byte value 2j
     of each 32-bit word at bit j*bits and value 2j+1 at bit 16 + j*bits; parameters per
-    (tile, chunk, block-of-chunk j, row)."""
+    (tile, chunk, block-of-chunk j, row), packed zero points `bits` bits each in entry order,
+    lowest bits first (rows 2i and 2i+1 of a block share a byte at 4 bits)."""
     blocks = -(-k // bs)
     row_bytes = blocks * bs * bits // 8
     nchunks = -(-row_bytes // 64)
@@ -149,7 +150,12 @@ def reference_layout(b, scales, zp, k, n, bits, bs):
                         if zp is not None:
                             byte = zp[row * zrow + blk * bits // 8]
                             zz[t, c, j, r] = (byte >> ((blk * bits) % 8)) & ((1 << bits) - 1)
-    return q_bytes, s.view(np.uint8).reshape(-1), zz.reshape(-1)
+    per = 8 // bits
+    entries = zz.reshape(-1, per).astype(np.uint32)
+    packed = np.zeros(entries.shape[0], np.uint32)
+    for i in range(per):
+        packed |= entries[:, i] << np.uint32(i * bits)
+    return q_bytes, s.view(np.uint8).reshape(-1), packed.astype(np.uint8)
 
 
 @pytest.mark.parametrize("bits,bs,k,n", [(4, 32, 1024, 40), (4, 16, 96, 17), (4, 256, 512, 16), (8, 32, 200, 5),

@@ -138,11 +138,12 @@ int tmh_floor_read_all(tmh_ctx* ctx, const tmh_weight* w, void* d_sink, void* st
   TMH_TRY(use_device(ctx));
   if (!w || !d_sink) return fail(ctx, TMH_ERR_INVALID, "tmh_floor_read_all: NULL argument");
   // The stored layout: 1 KiB per (tile, chunk) of weights; nbc * 16 parameter entries per (tile,
-  // chunk), each a scale of the weight type and a zero point (u8, or f32 for float zero points).
+  // chunk), each a scale of the weight type and a zero point (`bits` bits packed, or f32 for float
+  // zero points).
   const int64_t entries = w->ntiles * w->nchunks * w->nbc * 16;
   const int64_t n0 = w->ntiles * w->nchunks * 64;
   const int64_t n1 = entries * dtype_size(w->wdtype) / 16;
-  const int64_t n2 = w->zp_kind == TMH_ZP_PACKED ? entries / 16 : (w->zp_kind == TMH_ZP_FLOAT ? entries * 4 / 16 : 0);
+  const int64_t n2 = w->zp_kind == TMH_ZP_PACKED ? entries * w->bits / 8 / 16 : (w->zp_kind == TMH_ZP_FLOAT ? entries * 4 / 16 : 0);
   if ((n0 + n1 + n2) * 16 >= (int64_t(1) << 32))
     return fail(ctx, TMH_ERR_INVALID, "tmh_floor_read_all: the weight is too large");
   const unsigned grid = static_cast<unsigned>((n0 + n1 + n2 + 255) / 256);

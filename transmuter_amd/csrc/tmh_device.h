@@ -109,6 +109,24 @@ __device__ __forceinline__ uint32_t word_value(uint32_t x, int i) {
   }
 }
 
+// Packed zero points of the tiled layout take BITS bits each, as in the reference's rows of
+// packed zero points (two a byte for 4-bit weights, four for 2-bit, one for 8-bit): parameter
+// entry e sits at bits zp_shift(e) of byte zp_byte(e). Entries are (tile, chunk, block, row r)
+// with r = e % 16, so a lane's shift is that of its row, the same for every entry it reads.
+template <int BITS, typename I>
+__host__ __device__ constexpr I zp_byte(I e) {
+  return e / (8 / BITS);
+}
+template <int BITS>
+__host__ __device__ constexpr uint32_t zp_shift(uint32_t e) {
+  return (e % (8 / BITS)) * BITS;
+}
+template <int BITS>
+__device__ __forceinline__ uint32_t zp_field(uint32_t byte, uint32_t shift) {
+  if constexpr (BITS == 8) return byte & 0xFFu;
+  else return (byte >> shift) & ((1u << BITS) - 1u);
+}
+
 // (x & mask) | orv in one v_and_or_b32: the mask comes from an SGPR and orv from a VGPR, which
 // the one-scalar-operand limit of VOP3 on this target allows (two literals would not).
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t orv) {

@@ -67,7 +67,8 @@ __device__ __forceinline__ void gemv_dec(
   const uint32_t n_params = ntiles * nch * nbc * 16;
   const auto q_rsrc = buffer_rsrc(qt, ntiles * nch * 1024);
   const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
-  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? zp_byte<BITS>(n_params) : 0u);
+  const uint32_t zsh = zp_shift<BITS>(r);
   const auto a_rsrc = buffer_rsrc(A, M * lda * 2);
   const uint32_t a_row = static_cast<uint32_t>(r) < M ? static_cast<uint32_t>(r) * lda * 2 : 0x80000000u;
   float4_t acc[TN];
@@ -88,7 +89,7 @@ __device__ __forceinline__ void gemv_dec(
         for (int j = 0; j < NJ; ++j) {
           const uint32_t e = ((t * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
           sv[u][tn][j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, 0, 0);
-          if constexpr (HAS_ZP) zv[u][tn][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0);
+          if constexpr (HAS_ZP) zv[u][tn][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zp_byte<BITS>(e), 0, 0);
         }
       }
       if constexpr (ALDS) {
@@ -139,7 +140,7 @@ __device__ __forceinline__ void gemv_dec(
         const int j = SPLIT ? i : 0;
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
-          const uint32_t zq = HAS_ZP ? 0x6400u + zv[u][tn][j] : 0x6400u + (1u << (BITS - 1));
+          const uint32_t zq = HAS_ZP ? 0x6400u + zp_field<BITS>(zv[u][tn][j], zsh) : 0x6400u + (1u << (BITS - 1));
           const half8_t b = unpack_step<BITS>(w[u][tn], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
                                               __builtin_bit_cast(half2_t, sv[u][tn][j] | (sv[u][tn][j] << 16)));
           acc[tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, af[u][i], acc[tn], 0, 0, 0);
@@ -260,7 +261,8 @@ __device__ __forceinline__ void gemv_dot(
   const uint32_t n_params = ntiles * nch * nbc * 16;
   const auto q_rsrc = buffer_rsrc(qt, ntiles * nch * 1024);
   const auto s_rsrc = buffer_rsrc(sc, n_params * 2);
-  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? zp_byte<BITS>(n_params) : 0u);
+  const uint32_t zsh = zp_shift<BITS>(r);
   const auto a_rsrc = buffer_rsrc(A, K * 2);
   const half2_t one2 = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
   float acc[TN];
@@ -279,7 +281,7 @@ __device__ __forceinline__ void gemv_dot(
         w[u][tn] = __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, (t * nch * 64 + lane) * 16, c * 1024, 0);
         const uint32_t e = ((t * nch + c) * nbc + ((g * GW) >> bsc_shift)) * 16 + r;
         sv[u][tn] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, 0, 0);
-        if constexpr (HAS_ZP) zv[u][tn] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0);
+        if constexpr (HAS_ZP) zv[u][tn] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zp_byte<BITS>(e), 0, 0);
       }
       if constexpr (DEDUP) {
         // The chunk's A values of k-group g are NP 16-byte pieces, the same for the group's 16
@@ -356,7 +358,7 @@ __device__ __forceinline__ void gemv_dot(
             }
           }
         }
-        const float z = HAS_ZP ? static_cast<float>(zv[u][tn]) : static_cast<float>(1 << (BITS - 1));
+        const float z = HAS_ZP ? static_cast<float>(zp_field<BITS>(zv[u][tn], zsh)) : static_cast<float>(1 << (BITS - 1));
         const float s = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(sv[u][tn])));
         const float dot = BITS == 4 ? fmaf(dq, 0.0625f, de) : de;
         acc[tn] = fmaf(s, dot - fmaf(z, sa, base_sum), acc[tn]);
@@ -428,7 +430,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_f32(
   const uint32_t n_params = ntiles * nch * nbc * 16;
   const auto q_rsrc = buffer_rsrc(qt, ntiles * nch * 1024);
   const auto s_rsrc = buffer_rsrc(sc, n_params * 4);
-  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? n_params : 0u);
+  const auto z_rsrc = buffer_rsrc(zp, HAS_ZP ? zp_byte<BITS>(n_params) : 0u);
+  const uint32_t zsh = zp_shift<BITS>(r);
   const auto a_rsrc = buffer_rsrc(A, M * lda * 4);
   float acc[MM];
 #pragma unroll
@@ -440,7 +443,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_f32(
     for (int j = 0; j < NJ; ++j) {
       const uint32_t e = ((t * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
       sv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, e * 4, 0, 0));
-      zv[j] = HAS_ZP ? static_cast<float>(__builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, 0, 0))
+      zv[j] = HAS_ZP ? static_cast<float>(zp_field<BITS>(__builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zp_byte<BITS>(e), 0, 0), zsh))
                      : static_cast<float>(1 << (BITS - 1));
     }
     // A[m][k0 .. k0 + GW) as 16-byte pieces (zeros past M or K), held as floats: with hipcc 7.2

@@ -48,6 +48,9 @@ struct tmh_ctx {
 //
 // Per (tile, chunk) the scales and zero points of the blocks each row touches are stored as
 // params[tile][chunk][j][r], j < nbc = max(1, CW / block_size): block j of the chunk's row r.
+// Packed zero points take `bits` bits per entry, entry e at bits (e % (8/bits)) * bits of byte
+// e / (8/bits) (two a byte for 4-bit weights: rows 2i and 2i+1 of one block share a byte); float
+// zero points are f32 per entry.
 struct tmh_weight {
   int device = 0;
   int64_t K = 0, N = 0;
@@ -61,7 +64,7 @@ struct tmh_weight {
   int zp_kind = TMH_ZP_NONE;
   uint8_t* d_q = nullptr;   // ntiles*nchunks*1024 bytes
   void* d_scale = nullptr;  // ntiles*nchunks*nbc*16 values of wdtype
-  void* d_zero = nullptr;   // u8 (packed zero points) or f32 (float zero points), same layout
+  void* d_zero = nullptr;   // packed zero points (bits each) or f32 float zero points, same entries
   size_t device_bytes = 0;
 };
 

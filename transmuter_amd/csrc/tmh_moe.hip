@@ -368,7 +368,7 @@ __device__ __forceinline__ void moe_gemm_f16(
   for (int v = 0; v < NW; ++v) {
     q_rsrc[v] = buffer_rsrc(v ? qt2 : qt, static_cast<uint32_t>(ntiles) * nch * 1024);
     s_rsrc[v] = buffer_rsrc(v ? sc2 : sc, n_params * 2);
-    z_rsrc[v] = buffer_rsrc(v ? zp2 : zp, HAS_ZP ? n_params : 0u);
+    z_rsrc[v] = buffer_rsrc(v ? zp2 : zp, HAS_ZP ? zp_byte<BITS>(n_params) : 0u);
     tile0[v] = static_cast<uint32_t>(it.e * tiles_per_expert + lt_of(0) + (v ? tile_off2 : 0));
   }
   // A pieces this thread brings to LDS: row p / PPR, piece p % PPR of p = (tid + 512 l) mod
@@ -409,7 +409,7 @@ __device__ __forceinline__ void moe_gemm_f16(
       for (int j = 0; j < NJ; ++j) {
         const uint32_t e = ((tile * nch + c) * nbc + ((g * GW + 8 * j * (SPLIT ? 1 : 0)) >> bsc_shift)) * 16 + r;
         st.s[v][j] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc[v], e * 2, 0, 0);
-        if constexpr (HAS_ZP) st.z[v][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc[v], e, 0, 0);
+        if constexpr (HAS_ZP) st.z[v][j] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc[v], zp_byte<BITS>(e), 0, 0);
       }
     }
   };
@@ -481,7 +481,7 @@ __device__ __forceinline__ void moe_gemm_f16(
           const int j = SPLIT ? i : 0;
 #pragma unroll
           for (int v = 0; v < NW; ++v) {
-            const uint32_t zq = HAS_ZP ? 0x6400u + cur.z[v][j] : 0x6400u + (1u << (BITS - 1));
+            const uint32_t zq = HAS_ZP ? 0x6400u + zp_field<BITS>(cur.z[v][j], zp_shift<BITS>(r)) : 0x6400u + (1u << (BITS - 1));
             const half8_t b = unpack_step<BITS>(cur.w[v], i, __builtin_bit_cast(half2_t, zq | (zq << 16)),
                                                 __builtin_bit_cast(half2_t, cur.s[v][j] | (cur.s[v][j] << 16)));
 #pragma unroll
@@ -584,7 +584,8 @@ __global__ __launch_bounds__(256) void k_moe_gemm_general(
       const float s = load_as_f32<WDT>(sc, p);
       float z;
       if constexpr (ZK == TMH_ZP_PACKED) {
-        z = static_cast<float>(static_cast<const uint8_t*>(zp)[p]);
+        const uint8_t byte = static_cast<const uint8_t*>(zp)[zp_byte<BITS>(p)];
+        z = static_cast<float>(zp_field<BITS>(byte, zp_shift<BITS>(static_cast<uint32_t>(p))));
       } else {
         z = static_cast<float>(1 << (BITS - 1));
       }

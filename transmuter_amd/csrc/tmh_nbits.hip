@@ -123,7 +123,8 @@ __global__ __launch_bounds__(256) void k_dequant(const uint4_t* __restrict__ qt,
       const float s = round_to<OUT>(load_as_f32<WDT>(sc, p));
       float z;
       if constexpr (ZK == TMH_ZP_PACKED) {
-        z = static_cast<float>(static_cast<const uint8_t*>(zp)[p]);
+        const uint8_t byte = static_cast<const uint8_t*>(zp)[zp_byte<BITS>(p)];
+        z = static_cast<float>(zp_field<BITS>(byte, zp_shift<BITS>(static_cast<uint32_t>(p))));
       } else if constexpr (ZK == TMH_ZP_FLOAT) {
         z = round_to<OUT>(static_cast<const float*>(zp)[p]);
       } else {
@@ -159,7 +160,7 @@ __device__ __forceinline__ void load_params(const uint16_t* __restrict__ sc,
   ss = __builtin_bit_cast(half2_t, s | (s << 16));
   uint32_t z;
   if constexpr (HAS_ZP) {
-    z = 0x6400u + zp[p];
+    z = 0x6400u + zp_field<BITS>(zp[zp_byte<BITS>(p)], zp_shift<BITS>(static_cast<uint32_t>(p)));
   } else {
     z = 0x6400u + (1u << (BITS - 1));
   }
@@ -510,8 +511,8 @@ __device__ __noinline__ void store_quad_any(float4_t v, void* Y, int y_dt, int d
 
 // (The body; k_gemm_lds and its stamping build k_gemm_lds_tl below are the kernels.)
 // MODE (GM_*) and WT (GM_SPLIT: the weights' type) select the operand path; zk is the zero
-// point kind (TMH_ZP_*) read by GM_SPLIT, whose zero points are u8 (packed) or f32 (float) per
-// parameter entry. For GM_SPLIT, A is the bf16 hi rows [M][lda] followed by the lo rows.
+// point kind (TMH_ZP_*) read by GM_SPLIT, whose zero points are packed (BITS bits per parameter
+// entry) or f32 (float) per entry. For GM_SPLIT, A is the bf16 hi rows [M][lda] followed by the lo rows.
 template <int BITS, bool HAS_ZP, bool SPLIT, int WN, int BM, int KS, bool TL, int MODE, int WT>
 __device__ __forceinline__ void gemm_lds(
     const uint4_t* __restrict__ qt, const void* __restrict__ sc, const void* __restrict__ zp,
@@ -577,9 +578,10 @@ __device__ __forceinline__ void gemm_lds(
   const auto q_rsrc = buffer_rsrc(qt, static_cast<uint32_t>(ntiles * nchunks * 1024));
   const uint32_t n_params = static_cast<uint32_t>(ntiles * nchunks * nbc * 16);
   const auto s_rsrc = buffer_rsrc(sc, n_params * SES);
-  const uint32_t z_bytes = MODE == GM_SPLIT ? (zk == TMH_ZP_FLOAT ? n_params * 4 : zk == TMH_ZP_PACKED ? n_params : 0u)
-                                            : (HAS_ZP ? n_params : 0u);
+  const uint32_t z_bytes = MODE == GM_SPLIT ? (zk == TMH_ZP_FLOAT ? n_params * 4 : zk == TMH_ZP_PACKED ? zp_byte<BITS>(n_params) : 0u)
+                                            : (HAS_ZP ? zp_byte<BITS>(n_params) : 0u);
   const auto z_rsrc = buffer_rsrc(zp, z_bytes);
+  const uint32_t zsh = zp_shift<BITS>(r);  // every entry this lane reads is one of row r
 
   // A loads of this wavefront: rows wave*RW + s*RPI + lane/PPR, LDS slot lane%PPR. Offsets are
   // formed per load (few live registers); rows at or past M lie outside the buffer range and
@@ -637,11 +639,11 @@ __device__ __forceinline__ void gemm_lds(
         if constexpr (SES == 4) st.s[j][nt] = __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, e * 4, kofs * 4, 0);
         else st.s[j][nt] = __builtin_amdgcn_raw_buffer_load_b16(s_rsrc, e * 2, kofs * 2, 0);
         if constexpr (MODE == GM_SPLIT) {
-          // Float zero points are f32 per entry, packed ones u8 (a wavefront-uniform choice).
+          // Float zero points are f32 per entry, packed ones BITS bits (a wavefront-uniform choice).
           if (zk == TMH_ZP_FLOAT) st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b32(z_rsrc, e * 4, kofs * 4, 0);
-          else if (zk == TMH_ZP_PACKED) st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, kofs, 0);
+          else if (zk == TMH_ZP_PACKED) st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zp_byte<BITS>(e), zp_byte<BITS>(kofs), 0);
         } else if constexpr (HAS_ZP) {
-          st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, e, kofs, 0);
+          st.z[j][nt] = __builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zp_byte<BITS>(e), zp_byte<BITS>(kofs), 0);
         }
       }
     }
@@ -658,7 +660,7 @@ __device__ __forceinline__ void gemm_lds(
     for (int nt = 0; nt < NTW; ++nt) {
       const int j = SPLIT ? i : 0;
       const uint32_t sv = st.s[j][nt];
-      const uint32_t zv = HAS_ZP ? 0x6400u + st.z[j][nt] : 0x6400u + (1u << (BITS - 1));
+      const uint32_t zv = HAS_ZP ? 0x6400u + zp_field<BITS>(st.z[j][nt], zsh) : 0x6400u + (1u << (BITS - 1));
       bf[nt] = unpack_step<BITS>(st.w[nt], i, __builtin_bit_cast(half2_t, zv | (zv << 16)),
                                  __builtin_bit_cast(half2_t, sv | (sv << 16)));
     }
@@ -686,8 +688,8 @@ __device__ __forceinline__ void gemm_lds(
     constexpr float kDefault = static_cast<float>(1 << (BITS - 1));
     if constexpr (MODE == GM_SPLIT)
       return zk == TMH_ZP_FLOAT ? __builtin_bit_cast(float, bits)
-                                : (zk == TMH_ZP_PACKED ? static_cast<float>(bits & 0xFFu) : kDefault);
-    else return HAS_ZP ? static_cast<float>(bits & 0xFFu) : kDefault;
+                                : (zk == TMH_ZP_PACKED ? static_cast<float>(zp_field<BITS>(bits, zsh)) : kDefault);
+    else return HAS_ZP ? static_cast<float>(zp_field<BITS>(bits, zsh)) : kDefault;
   };
   auto compute = [&](int buf, const BStage& st, bool more, uint32_t kbn, BStage& nst) {
     const uint8_t* abase = lds + buf * ABUF + (wm * 128 + r) * ROWB;
@@ -1106,7 +1108,8 @@ __global__ __launch_bounds__(256) void k_matmul_general(
       const float s = load_as_f32<WDT>(sc, p);
       float z;
       if constexpr (ZK == TMH_ZP_PACKED) {
-        z = static_cast<float>(static_cast<const uint8_t*>(zp)[p]);
+        const uint8_t byte = static_cast<const uint8_t*>(zp)[zp_byte<BITS>(p)];
+        z = static_cast<float>(zp_field<BITS>(byte, zp_shift<BITS>(static_cast<uint32_t>(p))));
       } else if constexpr (ZK == TMH_ZP_FLOAT) {
         z = static_cast<const float*>(zp)[p];
       } else {
@@ -1615,7 +1618,7 @@ int plan_nbits(tmh_ctx* ctx, const uint8_t* h_b, size_t b_bytes, const void* h_s
   const int64_t n_params = p->ntiles * p->nchunks * p->nbc * 16;
   p->q_bytes = static_cast<size_t>(p->ntiles * p->nchunks * 1024);
   p->scale_bytes = static_cast<size_t>(n_params * dtype_size(weight_dtype));
-  p->zero_bytes = zp_kind == TMH_ZP_PACKED ? static_cast<size_t>(n_params)
+  p->zero_bytes = zp_kind == TMH_ZP_PACKED ? static_cast<size_t>(n_params * bits / 8)
                   : zp_kind == TMH_ZP_FLOAT ? static_cast<size_t>(n_params) * sizeof(float) : 0;
   return TMH_OK;
 }
@@ -1647,6 +1650,8 @@ void fill_nbits(const PackPlan& p, const uint8_t* h_b, const void* h_scales, con
   const auto* zp8 = static_cast<const uint8_t*>(h_zero_points);
   auto* zero8 = static_cast<uint8_t*>(zero);
   auto* zerof = static_cast<float*>(zero);
+  const int zper = 8 / p.bits;  // packed zero points per byte
+  if (p.zp_kind == TMH_ZP_PACKED) std::memset(zero8, 0, p.zero_bytes);
   for (int64_t t = 0; t < p.ntiles; ++t) {
     for (int64_t c = 0; c < p.nchunks; ++c) {
       for (int j = 0; j < p.nbc; ++j) {
@@ -1659,8 +1664,9 @@ void fill_nbits(const PackPlan& p, const uint8_t* h_b, const void* h_scales, con
           const float s = valid ? round_host(load_float(h_scales, p.scales_dtype, static_cast<size_t>(n * p.blocks + b)), p.wdtype) : 0.0f;
           store_host(scale, p.wdtype, e, s);
           if (p.zp_kind == TMH_ZP_PACKED) {
-            zero8[e] = !valid ? static_cast<uint8_t>(1 << (p.bits - 1))
-                       : p.bits == 8 ? zp8[n * p.zrow + b] : packed_zero(zp8, p.zrow, p.bits, n, b);
+            const uint8_t z = !valid ? static_cast<uint8_t>(1 << (p.bits - 1))
+                              : p.bits == 8 ? zp8[n * p.zrow + b] : packed_zero(zp8, p.zrow, p.bits, n, b);
+            zero8[e / zper] |= static_cast<uint8_t>(z << ((e % zper) * p.bits));
           } else if (p.zp_kind == TMH_ZP_FLOAT) {
             zerof[e] = valid ? round_host(load_float(h_zero_points, p.zp_dtype, static_cast<size_t>(n * p.blocks + b)), p.wdtype) : 0.0f;
           }
@@ -1681,10 +1687,13 @@ struct ConcatParts {
   int count;
 };
 
+// Packed zero points (zero_bits 2, 4 or 8) move entry by entry: rows r.. of a byte can come from
+// different parts, so lanes r of one (t, c, j) gather their byte by shuffles; float zero points
+// (zero_bits 0, zero_bytes 4) are copied byte for byte with the scales.
 __global__ __launch_bounds__(256) void k_concat_tiles(ConcatParts parts, uint8_t* __restrict__ q,
                                                       uint8_t* __restrict__ scale, uint8_t* __restrict__ zero,
                                                       int64_t nchunks, int nbc, int scale_bytes, int zero_bytes,
-                                                      int64_t lanes_total) {
+                                                      int zero_bits, int64_t lanes_total) {
   const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (id >= lanes_total) return;
   const int lane = static_cast<int>(id & 63);
@@ -1703,15 +1712,26 @@ __global__ __launch_bounds__(256) void k_concat_tiles(ConcatParts parts, uint8_t
   uint4_t v = {0u, 0u, 0u, 0u};
   if (valid) v = reinterpret_cast<const uint4_t*>(parts.q[p])[src_tc * 64 + 16 * g + sr];
   reinterpret_cast<uint4_t*>(q)[id] = v;
-  // Parameters: slot (t, c, j, r) for j < nbc, written by the lanes with g == 0.
+  // Parameters: slot (t, c, j, r) for j < nbc, written by the lanes with g == 0 (lanes 0-15 of
+  // the wavefront; lanes_total is a multiple of 64, so all sixteen are here).
   if (g != 0) return;
   for (int j = 0; j < nbc; ++j) {
     const int64_t dst = (tc * nbc + j) * 16 + r;
     const int64_t src = (src_tc * nbc + j) * 16 + sr;
     for (int b = 0; b < scale_bytes; ++b)
       scale[dst * scale_bytes + b] = valid ? parts.scale[p][src * scale_bytes + b] : 0;
-    for (int b = 0; b < zero_bytes; ++b)
-      zero[dst * zero_bytes + b] = valid ? parts.zero[p][src * zero_bytes + b] : 0;
+    if (zero_bits) {
+      const int per = 8 / zero_bits;
+      uint32_t z = 0u;
+      if (valid) z = (parts.zero[p][src / per] >> ((src % per) * zero_bits)) & ((1u << zero_bits) - 1u);
+      z <<= (r % per) * zero_bits;
+      if (per >= 2) z |= __shfl_xor(z, 1);
+      if (per >= 4) z |= __shfl_xor(z, 2);
+      if (r % per == 0) zero[dst / per] = static_cast<uint8_t>(z);
+    } else {
+      for (int b = 0; b < zero_bytes; ++b)
+        zero[dst * zero_bytes + b] = valid ? parts.zero[p][src * zero_bytes + b] : 0;
+    }
   }
 }
 
@@ -1748,9 +1768,10 @@ __global__ __launch_bounds__(256) void k_pack_tiles(const uint8_t* __restrict__ 
 }
 
 // k_pack_params: entry (t, c, j, r) holds block (c*CW + j*bsc) / block_size of row 16t + r: the
-// scale rounded to the weight type, the packed zero point as one byte, or a float zero point
-// rounded to the weight type (kept as f32); entries past N or past the blocks hold scale 0 and
-// zero point 2^(bits-1) (0 for float zero points).
+// scale rounded to the weight type, the packed zero point in `bits` bits (the thread of the
+// byte's first entry writes the byte: the entries of a byte are rows r.. of one (t, c, j)), or a
+// float zero point rounded to the weight type (kept as f32); entries past N or past the blocks
+// hold scale 0 and zero point 2^(bits-1) (0 for float zero points).
 template <int WDT>
 __global__ __launch_bounds__(256) void k_pack_params(const void* __restrict__ scales, int scales_dt,
                                                      const void* __restrict__ zp, int zp_kind, int zp_dt, int64_t N,
@@ -1770,13 +1791,20 @@ __global__ __launch_bounds__(256) void k_pack_params(const void* __restrict__ sc
   const float sv = valid ? round_to<WDT>(load_float_rt(scales, scales_dt, n * blocks + blk)) : 0.0f;
   store_as<WDT>(scale, e, sv);
   if (zp_kind == TMH_ZP_PACKED) {
-    uint8_t z = static_cast<uint8_t>(1 << (bits - 1));
-    if (valid) {
-      const int64_t bit = blk * bits;
-      const uint8_t byte = static_cast<const uint8_t*>(zp)[n * zrow + bit / 8];
-      z = bits == 8 ? byte : static_cast<uint8_t>((byte >> (bit % 8)) & ((1 << bits) - 1));
+    const int per = 8 / bits;
+    if (r % per != 0) return;
+    uint32_t packed = 0u;
+    for (int i = 0; i < per; ++i) {
+      const int64_t ni = n + i;
+      uint32_t z = 1u << (bits - 1);
+      if (ni < N && blk < blocks) {
+        const int64_t bit = blk * bits;
+        const uint8_t byte = static_cast<const uint8_t*>(zp)[ni * zrow + bit / 8];
+        z = bits == 8 ? byte : (byte >> (bit % 8)) & ((1u << bits) - 1u);
+      }
+      packed |= z << (i * bits);
     }
-    static_cast<uint8_t*>(zero)[e] = z;
+    static_cast<uint8_t*>(zero)[e / per] = static_cast<uint8_t>(packed);
   } else if (zp_kind == TMH_ZP_FLOAT) {
     static_cast<float*>(zero)[e] = valid ? round_to<WDT>(load_float_rt(zp, zp_dt, n * blocks + blk)) : 0.0f;
   }
@@ -1960,10 +1988,11 @@ int tmh_weight_concat_nbits(tmh_ctx* ctx, const tmh_weight* const* parts, int co
   w->ntiles = (total + kTileRows - 1) / kTileRows;
   const int64_t n_params = w->ntiles * w->nchunks * w->nbc * 16;
   const int scale_bytes = dtype_size(w->wdtype);
-  const int zero_bytes = w->zp_kind == TMH_ZP_PACKED ? 1 : w->zp_kind == TMH_ZP_FLOAT ? 4 : 0;
+  const int zero_bytes = w->zp_kind == TMH_ZP_FLOAT ? 4 : 0;
+  const int zero_bits = w->zp_kind == TMH_ZP_PACKED ? w->bits : 0;
   const size_t qb = static_cast<size_t>(w->ntiles * w->nchunks * 1024);
   const size_t sb = static_cast<size_t>(n_params * scale_bytes);
-  const size_t zb = static_cast<size_t>(n_params * zero_bytes);
+  const size_t zb = static_cast<size_t>(zero_bits ? n_params * zero_bits / 8 : n_params * zero_bytes);
   int st = check_hip(ctx, hipMalloc(reinterpret_cast<void**>(&w->d_q), qb), "hipMalloc (weight)");
   if (st == TMH_OK) st = check_hip(ctx, hipMalloc(&w->d_scale, sb), "hipMalloc (weight)");
   if (st == TMH_OK && zb) st = check_hip(ctx, hipMalloc(&w->d_zero, zb), "hipMalloc (weight)");
@@ -1974,7 +2003,7 @@ int tmh_weight_concat_nbits(tmh_ctx* ctx, const tmh_weight* const* parts, int co
   const int64_t lanes = w->ntiles * w->nchunks * 64;
   k_concat_tiles<<<static_cast<unsigned>((lanes + 255) / 256), 256, 0, ctx->stream>>>(
       cp, w->d_q, static_cast<uint8_t*>(w->d_scale), static_cast<uint8_t*>(w->d_zero), w->nchunks, w->nbc,
-      scale_bytes, zero_bytes, lanes);
+      scale_bytes, zero_bytes, zero_bits, lanes);
   st = check_launch(ctx, "k_concat_tiles");
   if (st == TMH_OK) st = check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
   if (st != TMH_OK) {
