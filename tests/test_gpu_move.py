@@ -120,19 +120,24 @@ def test_matmul_nbits_nodes_that_read_one_input_merge(ctx):
         assert np.array_equal(got[name].numpy(), expected[name].numpy()), name
 
 
-@pytest.mark.parametrize("ns", [[2048, 1024, 1024], [40, 8, 24], [17, 5]])
-def test_concat_is_the_rows_of_its_parts(ctx, ns):
-    rng = np.random.default_rng(sum(ns))
+@pytest.mark.parametrize("ns,bits,zp", [([2048, 1024, 1024], 4, "packed"), ([40, 8, 24], 4, "packed"),
+                                        ([17, 5], 4, "packed"), ([17, 5, 3, 1], 2, "packed"),
+                                        ([33, 7, 2], 8, "packed"), ([21, 6], 4, "float"), ([9, 16], 4, "none")])
+def test_concat_is_the_rows_of_its_parts(ctx, ns, bits, zp):
+    """The merged weight holds every part's rows in order; part boundaries off the 16-row tiles
+    move each row's packed zero points (several a byte below 8 bits) to another slot of a byte."""
+    print(f"concat ns={ns} bits={bits} zp={zp}", flush=True)
+    rng = np.random.default_rng(sum(ns) + bits)
     k = 1024
     parts, raw = [], []
     for n in ns:
-        b, s, z = nbits_weight(rng, k, n, 4, 32)
+        b, s, z = nbits_weight(rng, k, n, bits, 32, zp=zp)
         raw.append((b, s, z))
-        parts.append(PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=4, block_size=32, weight_dtype="f16"))
+        parts.append(PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=bits, block_size=32, weight_dtype="f16"))
     merged = PackedWeight.concat(parts)
     assert merged.shape == (sum(ns), k)
     got = merged.dequantize().numpy()
-    want = np.concatenate([o.dequantize_weight(b, s, z, k, n, 4, 32, o.F16) for (b, s, z), n in zip(raw, ns)])
+    want = np.concatenate([o.dequantize_weight(b, s, z, k, n, bits, 32, o.F16) for (b, s, z), n in zip(raw, ns)])
     assert np.array_equal(got, want)
     from transmuter_amd.quantized import matmul_nbits
 
