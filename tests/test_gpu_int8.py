@@ -380,3 +380,79 @@ def test_handlers_defer_freeing_their_uploads(ctx):
     got = y.numpy()  # the download drains the stream: the uploads are freed
     assert ctx.pending_frees() == 0
     assert np.array_equal(got, o.matmul_integer(a, b, None, None))
+
+
+def _dql_call(ctx, x_dev, n, y, s, z):
+    from transmuter_amd._lib import F32, lib
+    ctx.check(lib().tmh_dynamic_quantize_linear(ctx.handle, x_dev.ptr, F32, n, y.ptr, s.ptr, z.ptr, None))
+
+
+def _dql_check(got_y, got_s, got_z, x):
+    ry, rs, rz = o.dynamic_quantize_linear(x)
+    assert np.array_equal(got_y, ry)
+    assert np.float32(got_s).view(np.uint32) == np.float32(rs).view(np.uint32)
+    assert np.uint8(got_z) == rz
+
+
+def test_dynamic_quantize_linear_calls_in_a_row_and_graph_replays():
+    """Calls of different sizes in a row on a fresh context (the partial ranges of one call in
+    the workspace the previous call sized), then one call captured and replayed with calls of
+    other sizes between the replays: every output equals the oracle's."""
+    import ctypes
+    from transmuter_amd import Context
+    from transmuter_amd._lib import lib
+    ctx = Context(0)
+    try:
+        rng = np.random.default_rng(98)
+        sizes = (1, 4096, 8193, 2048 * 2048, 33, 3 * 1024 * 1024 + 7)
+        xs = [_dql_input(rng, "normal", n) * np.float32(1 + i) for i, n in enumerate(sizes)]
+        outs = []
+        for x in xs:
+            print(f"dynamic_quantize_linear in a row n={x.size}", flush=True)
+            xd, y, s, z = ctx.put(x), ctx.empty((x.size,), "u8"), ctx.empty((1,), "f32"), ctx.empty((1,), "u8")
+            _dql_call(ctx, xd, x.size, y, s, z)
+            outs.append((xd, y, s, z))
+        ctx.synchronize()
+        for x, (_, y, s, z) in zip(xs, outs):
+            _dql_check(y.numpy(), s.numpy()[0], z.numpy()[0], x)
+        xd, y, s, z = outs[3]
+        graph = ctypes.c_void_p()
+        ctx.check(lib().tmh_graph_begin(ctx.handle, None))
+        _dql_call(ctx, xd, xs[3].size, y, s, z)
+        ctx.check(lib().tmh_graph_end(ctx.handle, None, ctypes.byref(graph)))
+        for rep in range(3):
+            print(f"dynamic_quantize_linear graph replay {rep}", flush=True)
+            ctx.check(lib().tmh_upload(ctx.handle, y.ptr, np.full(y.size, 3, np.uint8).ctypes.data_as(ctypes.c_void_p),
+                                       y.nbytes))
+            ctx.check(lib().tmh_graph_launch(ctx.handle, graph, None))
+            ctx.synchronize()
+            _dql_check(y.numpy(), s.numpy()[0], z.numpy()[0], xs[3])
+            xo, yo, so, zo = outs[rep % 3]  # an eager call of another size between replays
+            _dql_call(ctx, xo, xs[rep % 3].size, yo, so, zo)
+            ctx.synchronize()
+            _dql_check(yo.numpy(), so.numpy()[0], zo.numpy()[0], xs[rep % 3])
+        ctx.check(lib().tmh_graph_destroy(ctx.handle, graph))
+    finally:
+        ctx.synchronize()
+        ctx.close()
+
+
+def test_dynamic_quantize_linear_large_and_unaligned(ctx):
+    """More values than one grid-stride round of either pass covers (8 M + 5), and x at an
+    offset that is not a multiple of 16 bytes (the scalar paths of both passes)."""
+    from transmuter_amd.device import DeviceTensor
+    rng = np.random.default_rng(99)
+    big = _dql_input(rng, "normal", 2 * 2048 * 2048 + 5)
+    print(f"dynamic_quantize_linear large n={big.size}", flush=True)
+    _check_dql(ctx, big)
+    x = _dql_input(rng, "positive", 300_001)
+    buf = ctx.put(np.concatenate([np.zeros(1, np.float32), x, np.zeros(3, np.float32)]))
+    view = DeviceTensor(ctx, ctypes.c_void_p(buf.ptr.value + 4), x.shape, "f32", x.nbytes)
+    view._owner = False
+    assert view.ptr.value % 16 != 0
+    print("dynamic_quantize_linear offset x", flush=True)
+    y, s, z = ctx.empty(x.shape, "u8"), ctx.empty((1,), "f32"), ctx.empty((1,), "u8")
+    _dql_call(ctx, view, x.size, y, s, z)
+    ctx.synchronize()
+    _dql_check(y.numpy(), s.numpy()[0], z.numpy()[0], x)
+    buf.free()
