@@ -220,9 +220,10 @@ def decode_sweep(ctx, steps, warmup, sets, ms, merged=False, full_step=False):
                                                     for layer in weights[s % sets] for w in layer]
                                        for s in range(2 * sets)], calls, reps=steps, warmup=warmup)
             results[m]["timeline"] = timeline_summary(res)
-        if full_step and m == 1:
+        if (full_step or merged) and m == 1:
             results[m].update(decode_floors(ctx, steps, warmup, weights, lambda s: [
-                matmul_call(ctx, w, a[w.k], y[w.n], m) for layer in range(QWEN3_LAYERS) for w in weights[s][layer]]))
+                matmul_call(ctx, w, a[w.k], y[w.n], m) for layer in range(QWEN3_LAYERS) for w in weights[s][layer]],
+                label="decode merged floors" if merged else "decode floors"))
         if full_step:
             results[m].update(full_decode_step(ctx, steps, warmup, weights, a, y, m))
     for ls in weights:
@@ -232,11 +233,12 @@ def decode_sweep(ctx, steps, warmup, sets, ms, merged=False, full_step=False):
     return results
 
 
-def decode_floors(ctx, steps, warmup, weights, eager_step):
-    """What one launch per projection costs without the GEMV's work, in graphs of the same 196
-    launches rotating over the same weight copies: an empty kernel (the launch floor) and a plain
-    read of each projection's packed weights with the GEMV's load pattern (the read floor). Also
-    the decode step's 196 GEMVs launched eagerly, back to back, with one synchronize at the end."""
+def decode_floors(ctx, steps, warmup, weights, eager_step, label="decode floors"):
+    """What one launch per projection costs without the GEMV's work, in graphs of the same
+    launches (196 per step, 112 with q/k/v and gate/up merged) rotating over the same weight
+    copies: an empty kernel (the launch floor) and a plain read of each projection's packed
+    weights with the GEMV's load pattern (the read floor). Also the decode step's GEMVs launched
+    eagerly, back to back, with one synchronize at the end."""
     from transmuter_amd._lib import lib
 
     per_step = QWEN3_LAYERS * len(weights[0][0])
@@ -259,7 +261,7 @@ def decode_floors(ctx, steps, warmup, weights, eager_step):
         eager_step(i % len(weights))
     ctx.synchronize()
     eager_ms = (time.perf_counter() - t0) * 1e3 / steps
-    log(f"decode floors: empty kernel {launch_us:.2f} us/launch, plain read of the packed weights {read_us:.2f} "
+    log(f"{label}: empty kernel {launch_us:.2f} us/launch, plain read of the packed weights {read_us:.2f} "
         f"us/launch ({q_bytes / (read_us * per_step * 1e-6) / 1e9:.0f} GB/s); eager step {eager_ms * 1e3:.0f} us "
         f"({1e3 / eager_ms:.0f} tokens/s)")
     return {"launch_floor_us": launch_us, "read_floor_us": read_us,
@@ -1280,7 +1282,8 @@ def main():
         "single_launch_us": head.get("single_launch_us"),
         "eager_tokens_per_s": head.get("eager_tokens_per_s"),
         "decode_merged_qkv_gateup": {str(m): {k: v for k, v in r.items() if k in ("gbs", "ms_per_step", "us_per_launch",
-                                                                                  "tokens_per_s")}
+                                                                                  "tokens_per_s", "launch_floor_us",
+                                                                                  "read_floor_us", "read_floor_gbs")}
                                      for m, r in dec_merged.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
