@@ -290,6 +290,8 @@ int tmh_dequantize_linear(tmh_ctx* ctx, const void* d_x, int x_dtype, int64_t ou
  *  d_a_zero NULL, one value or [M] (a_zero_count 1 or M), of a's type
  *  d_b_zero NULL, one value or [N] (b_zero_count 1 or N), of b's type
  *  d_y [batch, M, N] S32
+ * With K = 0, d_a and d_b may be NULL and y is all zeros; with batch, M or N = 0 nothing is read
+ * or written.
  */
 int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d_b, int b_dtype,
                        const void* d_a_zero, int64_t a_zero_count, const void* d_b_zero,

@@ -292,6 +292,21 @@ def test_matmul_integer_prepared_extremes_and_full_size(ctx):
     w.free()
 
 
+@pytest.mark.parametrize("a_shape,b_shape", [((3, 0), (0, 5)), ((2, 3, 0), (0, 5)), ((3, 0), (2, 0, 5)),
+                                             ((0, 7), (2, 7, 5)), ((4, 7), (7, 0))])
+def test_matmul_integer_empty_operands(ctx, a_shape, b_shape):
+    """Empty operands: a contraction over K = 0 gives zeros (A and B hold no device bytes), and no
+    rows or no columns give an empty result, for plain A over a batched B too."""
+    print(f"matmul_integer empty {a_shape} x {b_shape}", flush=True)
+    a = np.zeros(a_shape, np.uint8)
+    b = np.zeros(b_shape, np.int8)
+    node = NodeProto(op_type="MatMulInteger", input=["a", "b"], output=["y"])
+    y = quantized.apply(node, [ctx.put(a), ctx.put(b)])[0]
+    ref = o.matmul_integer(a, b)
+    got = y.numpy()
+    assert got.shape == ref.shape and np.array_equal(got, ref)
+
+
 def test_matmul_integer_prepare_needs_k_in_sixteens(ctx):
     from transmuter_amd._lib import TmhArgumentError
     from transmuter_amd.packed import Int8Weight
@@ -364,6 +379,24 @@ def test_prepared_matmul_integer_offset_view_and_row_blocks(ctx, monkeypatch):
         assert np.array_equal(aligned, ref), limit
     w.free()
     buf.free()
+
+
+def test_prepared_matmul_integer_with_no_rows(ctx):
+    """An A of zero rows (no device buffer behind it) gives a [0, N] result over a prepared B, as
+    the plain MatMulInteger does, and the same B still serves the next call."""
+    from transmuter_amd.packed import Int8Weight
+
+    rng = np.random.default_rng(79)
+    b = _ints(rng, (64, 24), "s8")
+    w = Int8Weight.prepare(ctx, b)
+    node = NodeProto(op_type="MatMulInteger", input=["a", "b"], output=["y"])
+    for batch_shape in ((), (3,)):
+        print(f"prepared MatMulInteger with no rows, batch {batch_shape}", flush=True)
+        got = quantized.apply(node, [ctx.put(np.zeros(batch_shape + (0, 64), np.uint8)), w])[0]
+        assert got.shape == batch_shape + (0, 24) and got.dtype == "s32"
+    a = _ints(rng, (5, 64), "u8")
+    assert np.array_equal(quantized.apply(node, [ctx.put(a), w])[0].numpy(), o.matmul_integer(a, b, None, None))
+    w.free()
 
 
 def test_handlers_defer_freeing_their_uploads(ctx):

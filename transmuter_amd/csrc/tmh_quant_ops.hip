@@ -971,6 +971,12 @@ __global__ __launch_bounds__(256) void k_dql_quantize_reduce(const float* __rest
   }
 }
 
+// The sums of an empty contraction (K = 0): every output is 0. A kernel rather than a memset, so
+// a graph capture records a kernel node.
+__global__ __launch_bounds__(256) void k_zero_s32(int32_t* __restrict__ y, int64_t n) {
+  for (int64_t i = blockIdx.x * int64_t{256} + threadIdx.x; i < n; i += int64_t{gridDim.x} * 256) y[i] = 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1104,6 +1110,14 @@ int tmh_matmul_integer(tmh_ctx* ctx, const void* d_a, int a_dtype, const void* d
   if (d_b_zero && b_zero_count != 1 && b_zero_count != N)
     return fail(ctx, TMH_ERR_INVALID, "MatMulInteger b_zero_point holds %lld values; 1 or N=%lld expected", (long long)b_zero_count, (long long)N);
   if (batch == 0 || M == 0 || N == 0) return TMH_OK;
+  if (K == 0) {
+    // Nothing to contract: the sums are zeros (A and B hold no bytes, and may be NULL).
+    if (!d_y) return fail(ctx, TMH_ERR_INVALID, "MatMulInteger: NULL pointer");
+    const int64_t n = batch * M * N;
+    k_zero_s32<<<static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 4096)), 256, 0, pick_stream(ctx, stream)>>>(
+        static_cast<int32_t*>(d_y), n);
+    return check_launch(ctx, "k_zero_s32");
+  }
   if (!d_a || !d_b || !d_y) return fail(ctx, TMH_ERR_INVALID, "MatMulInteger: NULL pointer");
   if (batch > 65535) return fail(ctx, TMH_ERR_INVALID, "MatMulInteger batch must be below 65536");
   if ((M + kI8Tile - 1) / kI8Tile > 65535)

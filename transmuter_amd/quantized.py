@@ -110,6 +110,8 @@ def _device(ctx: Context, x, dtype: str | None = None) -> tuple[DeviceTensor | N
 def _ptr_offset(t: DeviceTensor, elements: int) -> ctypes.c_void_p:
     item = np.dtype({"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "u8": np.uint8, "s8": np.int8,
                      "s32": np.int32, "s64": np.int64, "u16": np.uint16, "s16": np.int16}[t.dtype]).itemsize
+    if t.ptr.value is None:  # a tensor of no bytes has no buffer; the ABI takes NULL with zero sizes
+        return ctypes.c_void_p(None)
     return ctypes.c_void_p(t.ptr.value + elements * item)
 
 
@@ -143,7 +145,7 @@ def matmul_nbits(a: DeviceTensor, w: PackedWeight, bias=None, stream=None) -> De
             bias_t.tmh_dtype if bias_t is not None else 0, y.ptr, NX_TO_TMH[y_type], w.n, stream))
     finally:
         if own_bias:
-            ctx.defer_free(bias_t)
+            ctx.defer_free(bias_t, stream=stream)
     return y
 
 
@@ -360,7 +362,7 @@ def _matmul_integer_prepared(a, w: "Int8Weight", a_zero, b_zero):
     try:
         out_shape = batch_shape + (m, w.n)
         y = ctx.empty(out_shape, "s32")
-        if a_t.ptr.value % 16:
+        if a_t.ptr.value and a_t.ptr.value % 16:
             # The prepared GEMM streams A 16 bytes at a time: an A that does not start on a 16-byte
             # boundary (an offset view) is copied to a fresh buffer first.
             a_al = ctx.empty(a_t.shape, a_t.dtype)
