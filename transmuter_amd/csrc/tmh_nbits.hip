@@ -865,6 +865,13 @@ __device__ __forceinline__ void gemm_lds(
   // The f16 rows store non-temporally: 2048 -> 11008 at M = 2048, 45 MB out, 109.8 -> 107.9 us;
   // the partial sums, read back by the reduction, gain nothing from it.)
   constexpr bool kPartialsFit = static_cast<int>(gemm_lds_bytes<BITS, BM, KS, MODE>()) >= BM * 64 * WN * 4;
+  // The partial sums go out written through the L2 (kWriteThrough) where one split's M x N fits
+  // a buffer's 32-bit offsets: otherwise they sit dirty in the L2 until the kernel's end, whose
+  // write-back the reduction's launch waits for (2048 -> 2048 at M = 256, 8 MB of partial sums:
+  // 63.4 -> 61.2 us per four calls; 11008 -> 2048, M = 256: 109.7 -> 104.5 us).
+  const bool wt_ok = ws && M * N * 4 < (int64_t(1) << 31);
+  const auto wt_rsrc = buffer_rsrc(ws ? ws + static_cast<int64_t>(split) * M * N : ws,
+                                   wt_ok ? static_cast<uint32_t>(M * N * 4) : 0u);
   const bool staged = ws ? kPartialsFit && (N % 4) == 0
                          : f16_out && (ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
   if (staged) {
@@ -908,7 +915,9 @@ __device__ __forceinline__ void gemm_lds(
           const uint4_t v = *reinterpret_cast<const uint4_t*>(lds + prow * RS + ((unit ^ (prow & 7)) << 4));
           if constexpr (ESZ == 4) {
             float* dst = ws + (static_cast<int64_t>(split) * M + m) * N + n;
-            if (n + 4 <= N) {
+            if (n + 4 <= N && wt_ok) {
+              __builtin_amdgcn_raw_buffer_store_b128(v, wt_rsrc, static_cast<uint32_t>((m * N + n) * 4), 0, kWriteThrough);
+            } else if (n + 4 <= N) {
               *reinterpret_cast<uint4_t*>(dst) = v;
             } else {
               const float4_t f = __builtin_bit_cast(float4_t, v);  // whole vector: hipcc 7.2 miscompiled element casts
@@ -948,7 +957,10 @@ __device__ __forceinline__ void gemm_lds(
       const float4_t v = acc[mt][nt];
       if (ws) {
         float* dst = ws + (static_cast<int64_t>(split) * M + m) * N + n;
-        if (n + 4 <= N && (N % 4) == 0) {
+        if (n + 4 <= N && (N % 4) == 0 && wt_ok) {
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uint4_t, v), wt_rsrc,
+                                                 static_cast<uint32_t>((m * N + n) * 4), 0, kWriteThrough);
+        } else if (n + 4 <= N && (N % 4) == 0) {
           *reinterpret_cast<float4_t*>(dst) = v;
         } else {
           for (int e = 0; e < 4 && n + e < N; ++e) dst[e] = v[e];
@@ -1058,13 +1070,22 @@ __device__ __forceinline__ void splitk_reduce_quads(const float* __restrict__ ws
     float4_t v = *reinterpret_cast<const float4_t*>(ws + i4);
     for (int sp = 1; sp < splits; ++sp) v += *reinterpret_cast<const float4_t*>(ws + sp * total + i4);
     const int64_t m = i4 / N, n = i4 - m * N;
+    float x[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      float x = v[e];
-      x = round_dot(x, dot_dt);
-      if (bias) x += load_float_rt(bias, bias_dt, n + e);
-      store_float_rt(Y, y_dt, m * ldy + n + e, x);
+      x[e] = round_dot(v[e], dot_dt);
+      if (bias) x[e] += load_float_rt(bias, bias_dt, n + e);
     }
+    if (y_dt == DT_F16 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(Y) & 7) == 0) {
+      // Four f16 outputs in one 8-byte store.
+      const uint32_t lo = f32_to_f16_bits(x[0]) | (static_cast<uint32_t>(f32_to_f16_bits(x[1])) << 16);
+      const uint32_t hi = f32_to_f16_bits(x[2]) | (static_cast<uint32_t>(f32_to_f16_bits(x[3])) << 16);
+      *reinterpret_cast<uint64_t*>(static_cast<uint16_t*>(Y) + m * ldy + n) =
+          static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+      return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_float_rt(Y, y_dt, m * ldy + n + e, x[e]);
     return;
   }
   for (int64_t i = i4; i < i4 + 4 && i < total; ++i) {
