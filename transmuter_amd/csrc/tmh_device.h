@@ -209,9 +209,10 @@ __device__ __forceinline__ int frag_swizzle(int r) {
 // Cache policy of a buffer store whose data no later instruction of the kernel reads: the nt
 // bit (streaming), so an output written once does not displace the inputs still being read.
 constexpr int kNonTemporal = 2;
-// Cache policy of a buffer store that the next kernel reads back: sc1 (device scope), which
-// writes the line through the XCD's L2, so no dirty lines are left for the write-back at the
-// end of the kernel, which the next kernel's launch would otherwise wait for.
+// Cache policy sc1 (device scope): the store writes its line through the XCD's L2, so the line
+// is not left dirty there for the write-back at the kernel's end, which the next launch on the
+// stream waits for. It pays where a kernel's stores overlap its later work (split-K partial
+// sums, the row gather); where the stores come last (a GEMV's output) they only finish later.
 constexpr int kWriteThrough = 16;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {

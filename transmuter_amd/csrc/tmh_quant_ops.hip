@@ -142,9 +142,12 @@ void launch_gather_ub(const uint8_t* data, bool sgn, int64_t rows, int64_t row_b
 // loads slice j's id (one vector load for the wavefront) and each row is broadcast from its lane;
 // the data, scale and zero point loads of all S slices then issue before the first value is
 // computed, so a wavefront pays the id latency and the row latency once for S slices instead of
-// once per half row. Each slice's values leave as one 16-byte non-temporal store per lane (1 KiB
-// contiguous per instruction): at the [8, 512] x 1024 f16 lookup the 8 MiB of output cost 1.4 us
-// over an empty launch with ordinary stores and 0.9 us with non-temporal ones. A slice past the
+// once per half row. Each slice's values leave as one 16-byte store per lane (1 KiB contiguous
+// per instruction), written through the L2 (kWriteThrough): at the [8, 512] x 1024 f16 lookup the
+// 8 MiB of output cost 1.4 us over an empty launch with ordinary stores and 0.9 us with
+// non-temporal ones, and written through 3.6 against 3.7 us per lookup in graph replays (the next
+// launch then waits on no write-back of dirty lines; non-temporal and written through, 3.6 us at
+// 3.0 against 3.05 TB/s). A slice past the
 // end (the last wavefront's) stores to an offset beyond the output buffer's range, which the
 // hardware drops: no branch, so no slice's loads wait behind another's stores. `spr_magic` is
 // floor(2^32 / slices_per_row) + 1 (slices_per_row > 1): umulhi(sl, spr_magic) equals
@@ -290,12 +293,12 @@ __device__ __forceinline__ void gather_bq_rows(
     const uint32_t off = sl < n_slices ? o : 0xFFFFFF00u;  // past the range: dropped
     if constexpr (V * ES == 8) {  // 8-bit values in a 2-byte type: 8 bytes per lane
       typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
-      __builtin_amdgcn_raw_buffer_store_b64(uint2_t{words[0], words[1]}, o_rsrc, off, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b64(uint2_t{words[0], words[1]}, o_rsrc, off, 0, kWriteThrough);
     } else {
 #pragma unroll
       for (int k = 0; k < V * ES / 16; ++k)
         __builtin_amdgcn_raw_buffer_store_b128(uint4_t{words[4 * k], words[4 * k + 1], words[4 * k + 2], words[4 * k + 3]},
-                                               o_rsrc, off + 16 * k, 0, kNonTemporal);
+                                               o_rsrc, off + 16 * k, 0, kWriteThrough);
     }
   }
   if constexpr (TL) tl_stamp(tl, tl0);
