@@ -661,6 +661,40 @@ __device__ __forceinline__ void moe_combine(const void* __restrict__ o, int H, c
   const int64_t idx = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * V;
   if (idx >= static_cast<int64_t>(T) * H) return;
   const int t = static_cast<int>(idx / H), hc = static_cast<int>(idx - static_cast<int64_t>(t) * H);
+  if constexpr (DT == DT_F16 && V == 8) {
+    if (!b2) {
+      // f16 rows without a bias: the products and sums in packed f16. Each product of two f16
+      // values is exact in f32 and each sum of two f16 values rounds the same from f32 as
+      // directly, so v_pk_mul_f16 then v_pk_add_f16 give the bits of the f32 steps rounded to
+      // f16 after each one, at an eighth of the instructions.
+#pragma clang fp contract(off)
+      half8_t acc = {};
+      for (int j0 = 0; j0 < k; j0 += JU) {
+        half8_t ov[JU];
+        _Float16 wgt[JU];
+#pragma unroll
+        for (int u = 0; u < JU; ++u) {
+          const int j = j0 + u < k ? j0 + u : k - 1;
+          wgt[u] = static_cast<_Float16>(topw[t * k + j]);
+          const int64_t row = slot_pos ? slot_pos[t * k + j] : t * k + j;
+          ov[u] = *reinterpret_cast<const half8_t*>(static_cast<const _Float16*>(o) + row * H + hc);
+        }
+#pragma unroll
+        for (int u = 0; u < JU; ++u) {
+          if (j0 + u >= k || wgt[u] == static_cast<_Float16>(0.f)) continue;
+          const half8_t prod = ov[u] * wgt[u];
+          acc = acc + prod;
+        }
+      }
+      if (y_vec) {
+        *reinterpret_cast<half8_t*>(static_cast<_Float16*>(y) + idx) = acc;
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v) store_as<DT>(y, idx + v, static_cast<float>(acc[v]));
+      }
+      return;
+    }
+  }
   float sum[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) sum[v] = 0.f;
