@@ -177,10 +177,16 @@ void launch_bits(const DecArgs& d, int64_t M, int num_cus, hipStream_t s) {
   streaming<BITS, HAS_ZP, SPLIT>(d, std::min(8, round_waves((nch + 1) / 2)), s);
 }
 
+// One row of A (the reference's single-op case) takes the one-row build: the four-row build
+// would load and multiply three rows of zeros (C1, 1024 -> 3072 f32).
 template <int BITS, bool HAS_ZP, bool SPLIT, int NW>
 void go_f32(const DecArgs& d, const float* a, float* y, hipStream_t s) {
-  k_gemv_f32<BITS, HAS_ZP, SPLIT, NW, 4><<<d.ntiles, 64 * NW, 0, s>>>(
-      d.qt, reinterpret_cast<const float*>(d.sc), d.zp, a, d.nch, d.ntiles, d.lda, d.shape, y, d.ldy, d.n);
+  if ((d.shape & 0xFFu) == 1)
+    k_gemv_f32<BITS, HAS_ZP, SPLIT, NW, 1><<<d.ntiles, 64 * NW, 0, s>>>(
+        d.qt, reinterpret_cast<const float*>(d.sc), d.zp, a, d.nch, d.ntiles, d.lda, d.shape, y, d.ldy, d.n);
+  else
+    k_gemv_f32<BITS, HAS_ZP, SPLIT, NW, 4><<<d.ntiles, 64 * NW, 0, s>>>(
+        d.qt, reinterpret_cast<const float*>(d.sc), d.zp, a, d.nch, d.ntiles, d.lda, d.shape, y, d.ldy, d.n);
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT>
