@@ -385,6 +385,51 @@ def test_one_row_both_kernels(ctx, monkeypatch, case, plan):
     del ctypes
 
 
+# Decode with an f16 bias (Y = the f16 dot + bias, rounded to f16: quantized.ex:44-45) on the
+# decode GEMVs: one-shot grids with A direct (M <= 4) and through LDS (M > 4), K past one round of
+# wavefronts, streaming grids of two and four tiles per workgroup, a ragged last tile whose last
+# columns store one at a time, and parameters that span two blocks per lane; M = 1 on both the
+# dot-product and the MFMA kernel.
+BIAS_DECODE_CASES = [
+    # bits, block, zp, K, N, M list
+    (4, 32, "packed", 1024, 96, [1, 3, 4, 6, 16]),
+    (4, 32, "packed", 3072, 40, [1, 8]),
+    (4, 32, "packed", 1024, 30008, [1, 7, 16]),
+    (4, 32, "packed", 1024, 16400, [1, 2]),
+    (8, 32, "none", 512, 42, [1, 3, 9]),
+    (4, 16, "packed", 256, 40, [1, 5]),
+]
+
+
+@pytest.mark.parametrize("plan", ["dot", "mfma"])
+@pytest.mark.parametrize("case", BIAS_DECODE_CASES, ids=lambda c: "b{}_bs{}_{}_K{}_N{}".format(*c[:5]))
+def test_decode_gemv_with_bias(ctx, monkeypatch, case, plan):
+    """Against the oracle, and bit for bit against the same kernel's output without the bias with
+    the bias then added on the host in f32 and rounded to f16."""
+    bits, bs, zp, k, n, ms = case
+    if plan == "mfma":
+        monkeypatch.setenv("TMH_GEMV_PLAN", "mfma")
+    else:
+        monkeypatch.delenv("TMH_GEMV_PLAN", raising=False)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()) + 3)
+    b, s, z = nbits_weight(rng, k, n, bits, bs, zp=zp)
+    w = PackedWeight.upload(ctx, b, s, z, k=k, n=n, bits=bits, block_size=bs, weight_dtype="f16")
+    bias = rng.standard_normal(n).astype(np.float16)
+    bias_d = ctx.put(bias)
+    for m in ms:
+        print(f"decode bias {plan} {case} M={m}", flush=True)
+        a = rng.standard_normal((m, k)).astype(np.float16)
+        a_d = ctx.put(a)
+        y = matmul_nbits(a_d, w, bias_d).numpy()
+        y0 = matmul_nbits(a_d, w).numpy()
+        assert np.array_equal(y.view(np.uint16), (y0.astype(np.float32) + bias.astype(np.float32)).astype(np.float16)
+                              .view(np.uint16)), f"M={m}"
+        ref = o.matmul_nbits(a, b, s, z, bias, k=k, n=n, bits=bits, block_size=bs).astype(np.float64)
+        err = rel_err(y.astype(np.float64), ref)
+        assert err <= TOL["f16"], f"M={m}: relative error {err}"
+    w.free()
+
+
 def test_one_row_dot_kernel_is_near_exact(ctx, monkeypatch):
     """The dot-product GEMV (one row of A over more tiles than the GPU holds at once) sums exact
     products (q + 1024) * a in f32 and removes the offsets per lane: against the f64 sum over the

@@ -38,11 +38,12 @@ namespace tmh {
 // values of the last chunks past K. K travels in shape rather than as an argument of its own:
 // one more argument made a launch 0.09-0.17 us slower.
 // (The body; k_gemv_dec and its stamping build k_gemv_dec_tl below are the kernels.)
-template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS, bool TL>
+template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS, bool TL, bool BIAS = false>
 __device__ __forceinline__ void gemv_dec(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
-    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, uint32_t* __restrict__ tl) {
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, uint32_t* __restrict__ tl,
+    const _Float16* __restrict__ bias = nullptr) {
   const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
   constexpr int CW = 512 / BITS;   // weights per chunk row
   constexpr int GW = CW / 4;       // weights per lane per chunk
@@ -71,6 +72,24 @@ __device__ __forceinline__ void gemv_dec(
   const uint32_t zsh = zp_shift<BITS>(r);
   const auto a_rsrc = buffer_rsrc(A, M * lda * 2);
   const uint32_t a_row = static_cast<uint32_t>(r) < M ? static_cast<uint32_t>(r) * lda * 2 : 0x80000000u;
+  // The bias of the lane's four output columns (zeros where the four columns do not all lie
+  // below N: that case stores one column at a time and reads the bias there), loaded right after
+  // the first round's weights: its kernel argument is not preloaded, and loaded ahead of them
+  // its fetch held back the weights' loads.
+  typedef uint32_t u32x2b_t __attribute__((ext_vector_type(2)));
+  u32x2b_t bias_v[TN];
+  bool bias_loaded = false;
+  auto load_bias = [&]() {
+    if constexpr (BIAS) {
+      const auto b_rsrc = buffer_rsrc(bias, N * 2);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t n = (t0 + tn) * 16 + 4 * g;
+        bias_v[tn] = __builtin_amdgcn_raw_buffer_load_b64(b_rsrc, n + 4 <= N ? n * 2 : 0x80000000u, 0, 0);
+      }
+      bias_loaded = true;
+    }
+  };
   float4_t acc[TN];
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) acc[tn] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -114,6 +133,7 @@ __device__ __forceinline__ void gemv_dec(
         }
       }
     }
+    if (BIAS && !bias_loaded) load_bias();
     if constexpr (ALDS) {
       // The DMAs have written the chunks' rows once no vector-memory operation is outstanding
       // (the weights, issued first, are needed next anyway); lanes then read pieces that other
@@ -148,6 +168,7 @@ __device__ __forceinline__ void gemv_dec(
       }
     }
   }
+  if (BIAS && !bias_loaded) load_bias();  // a wavefront that had no chunk
   if constexpr (NW > 1) {
     if constexpr (ALDS) {  // the partial sums overwrite A pieces that other lanes read
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -177,7 +198,21 @@ __device__ __forceinline__ void gemv_dec(
     const uint32_t n = (t0 + tn) * 16 + 4 * g;
     if (n >= N) continue;
     _Float16* dst = Y + r * ldy + n;
-    const float4_t v = acc[tn];
+    float4_t v = acc[tn];
+    if constexpr (BIAS) {
+      // Y = (A . W^T rounded to f16) + bias, rounded to f16 (the reference's Nx.add of the f16 dot).
+      if (n + 4 <= N) {
+        // The whole vector reinterpreted at once: hipcc 7.2 read element 0 of an integer vector
+        // for every index under __builtin_bit_cast of one element.
+        typedef _Float16 half4b_t __attribute__((ext_vector_type(4)));
+        const half4b_t b = __builtin_bit_cast(half4b_t, bias_v[tn]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = static_cast<float>(static_cast<_Float16>(v[e])) + static_cast<float>(b[e]);
+      } else {
+        for (uint32_t e = 0; e < 4 && n + e < N; ++e)
+          v[e] = static_cast<float>(static_cast<_Float16>(v[e])) + static_cast<float>(bias[n + e]);
+      }
+    }
     if (n + 4 <= N && (ldy % 4) == 0) {
       const half2_t lo = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])};
       const half2_t hi = {static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
@@ -202,6 +237,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dec(
     const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
     _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
   gemv_dec<BITS, HAS_ZP, SPLIT, U, NW, TN, ALDS, false>(qt, sc, zp, A, nch, ntiles, lda, shape, Y, ldy, N, nullptr);
+}
+
+// The same GEMV with a bias (an f16 [N] added to the f16 result); a kernel of its own, so the
+// kernels without one keep their argument list (one more argument costs every launch).
+template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS>
+__global__ __launch_bounds__(64 * NW) void k_gemv_dec_bias(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, const _Float16* __restrict__ bias) {
+  gemv_dec<BITS, HAS_ZP, SPLIT, U, NW, TN, ALDS, false, true>(qt, sc, zp, A, nch, ntiles, lda, shape, Y, ldy, N,
+                                                              nullptr, bias);
 }
 
 template <int BITS, bool HAS_ZP, bool SPLIT, int U, int NW, int TN, bool ALDS>
@@ -239,11 +285,12 @@ __device__ __forceinline__ half8_t row_piece(const uint4_t& x) {
 // The four lanes of a row and the wavefronts of the workgroup add through LDS in a fixed order.
 // Chunk rounds, launch shapes and buffer addressing are those of k_gemv_dec.
 // (The body; k_gemv_dot and its stamping build k_gemv_dot_tl below are the kernels.)
-template <int BITS, bool HAS_ZP, int U, int NW, int TN, bool TL>
+template <int BITS, bool HAS_ZP, int U, int NW, int TN, bool TL, bool BIAS = false>
 __device__ __forceinline__ void gemv_dot(
     const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
     const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
-    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, uint32_t* __restrict__ tl) {
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, uint32_t* __restrict__ tl,
+    const _Float16* __restrict__ bias = nullptr) {
   const TlStart tl0 = TL ? tl_clock() : TlStart{0u, 0u};
   static_assert(BITS == 4 || BITS == 8, "4- or 8-bit weights");
   constexpr int CW = 512 / BITS;  // weights per chunk row
@@ -265,6 +312,20 @@ __device__ __forceinline__ void gemv_dot(
   const uint32_t zsh = zp_shift<BITS>(r);
   const auto a_rsrc = buffer_rsrc(A, K * 2);
   const half2_t one2 = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
+  // The bias of the lane's output column (row r of each tile), loaded right after the first
+  // round's weights (as in gemv_dec).
+  _Float16 bias_v[TN];
+  bool bias_loaded = false;
+  auto load_bias = [&]() {
+    if constexpr (BIAS) {
+      const auto b_rsrc = buffer_rsrc(bias, N * 2);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        bias_v[tn] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(
+                                                      b_rsrc, ((t0 + tn) * 16 + r) * 2, 0, 0)));
+      bias_loaded = true;
+    }
+  };
   float acc[TN];
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) acc[tn] = 0.f;
@@ -300,6 +361,7 @@ __device__ __forceinline__ void gemv_dot(
         }
       }
     }
+    if (BIAS && !bias_loaded) load_bias();
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       half8_t av[1][NP];
@@ -365,6 +427,7 @@ __device__ __forceinline__ void gemv_dot(
       }
     }
   }
+  if (BIAS && !bias_loaded) load_bias();  // a wavefront that had no chunk
   // Row r's four lane sums of a wavefront sit together (one 16-byte read each).
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) red[(wave * TN + tn) * 64 + r * 4 + g] = acc[tn];
@@ -385,6 +448,8 @@ __device__ __forceinline__ void gemv_dot(
 #pragma unroll
       for (int g2 = 0; g2 < 4; ++g2) v += part[w2][g2];
     const uint32_t n = (t0 + tn) * 16 + r;
+    // With a bias: the f16 dot plus the bias, rounded to f16 (the reference's Nx.add).
+    if constexpr (BIAS) v = static_cast<float>(static_cast<_Float16>(v)) + static_cast<float>(bias_v[tn]);
     if (n < N) Y[n] = static_cast<_Float16>(v);
   }
   if constexpr (TL) tl_stamp(tl, tl0);
@@ -396,6 +461,15 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_dot(
     const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
     _Float16* __restrict__ Y, uint32_t ldy, uint32_t N) {
   gemv_dot<BITS, HAS_ZP, U, NW, TN, false>(qt, sc, zp, A, nch, ntiles, lda, shape, Y, ldy, N, nullptr);
+}
+
+// The same with a bias (f16 [N]), as k_gemv_dec_bias.
+template <int BITS, bool HAS_ZP, int U, int NW, int TN>
+__global__ __launch_bounds__(64 * NW) void k_gemv_dot_bias(
+    const uint4_t* __restrict__ qt, const uint16_t* __restrict__ sc, const uint8_t* __restrict__ zp,
+    const _Float16* __restrict__ A, uint32_t nch, uint32_t ntiles, uint32_t lda, uint32_t shape,
+    _Float16* __restrict__ Y, uint32_t ldy, uint32_t N, const _Float16* __restrict__ bias) {
+  gemv_dot<BITS, HAS_ZP, U, NW, TN, false, true>(qt, sc, zp, A, nch, ntiles, lda, shape, Y, ldy, N, nullptr, bias);
 }
 
 template <int BITS, bool HAS_ZP, int U, int NW, int TN>

@@ -46,6 +46,7 @@ struct DecArgs {
   uint32_t nch, ntiles, lda, shape;
   _Float16* y;
   uint32_t ldy, n;
+  const _Float16* bias = nullptr;  // f16 [N] added to Y, or none
 };
 
 template <int BITS, bool HAS_ZP, bool SPLIT, int NW, int TN, bool ALDS, int U = 1>
@@ -57,6 +58,11 @@ void go(const DecArgs& d, hipStream_t s) {
   constexpr bool A_LDS = ALDS && static_cast<size_t>(NW) * U * 16 * rb * 16 <= kStaticLds;
   static_assert(red <= kStaticLds, "partial sums exceed the static LDS");
   const unsigned grid = (d.ntiles + TN - 1) / TN;
+  if (d.bias) {  // (the bias build has no stamping build: its launches are not on the timeline)
+    k_gemv_dec_bias<BITS, HAS_ZP, SPLIT, U, NW, TN, A_LDS><<<grid, 64 * NW, 0, s>>>(
+        d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles, d.lda, d.shape, d.y, d.ldy, d.n, d.bias);
+    return;
+  }
   if (uint32_t* tl = timeline_slots(TMH_TL_GEMV_DEC, static_cast<int64_t>(grid) * NW)) {
     k_gemv_dec_tl<BITS, HAS_ZP, SPLIT, U, NW, TN, A_LDS><<<grid, 64 * NW, 0, s>>>(
         d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles, d.lda, d.shape, d.y, d.ldy, d.n, tl);
@@ -98,6 +104,11 @@ void streaming(const DecArgs& d, int nw, hipStream_t s) {
 template <int BITS, bool HAS_ZP, int NW, int TN, int U>
 void go_dot(const DecArgs& d, hipStream_t s) {
   const unsigned grid = (d.ntiles + TN - 1) / TN;
+  if (d.bias) {
+    k_gemv_dot_bias<BITS, HAS_ZP, U, NW, TN><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles, d.lda,
+                                                                       d.shape, d.y, d.ldy, d.n, d.bias);
+    return;
+  }
   if (uint32_t* tl = timeline_slots(TMH_TL_GEMV_DOT, static_cast<int64_t>(grid) * NW)) {
     k_gemv_dot_tl<BITS, HAS_ZP, U, NW, TN><<<grid, 64 * NW, 0, s>>>(d.qt, d.sc, d.zp, d.a, d.nch, d.ntiles, d.lda,
                                                                      d.shape, d.y, d.ldy, d.n, tl);
@@ -255,9 +266,10 @@ bool decode_gemv_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, co
 }
 
 void launch_decode_gemv(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,
-                        hipStream_t s, int num_cus) {
+                        hipStream_t s, int num_cus, const void* bias) {
   const int cw = chunk_weights(w->bits);
-  const DecArgs d = dec_args(w, a, M, lda, y, ldy);
+  DecArgs d = dec_args(w, a, M, lda, y, ldy);
+  d.bias = static_cast<const _Float16*>(bias);
   const bool zp = w->zp_kind == TMH_ZP_PACKED;
   const bool split = w->block_size < cw / 4;  // a lane's k-group spans several blocks
 #define TMH_DEC(B)                                                   \

@@ -106,12 +106,13 @@ float bf16_to_f32(uint16_t h);
 uint16_t f32_to_bf16(float f);
 float load_float(const void* p, int dt, size_t i);  // host read of a float array element
 
-// The decode GEMV of tmh_gemv.hip (k_gemv_dec): Y [M, N] f16 = A [M, K] f16 . W^T for M <= 16,
-// f16 weights, packed or no zero points. decode_gemv_ok tells whether it applies (alignment,
-// 32-bit offsets); launch_decode_gemv picks the launch shape for the size and launches.
+// The decode GEMV of tmh_gemv.hip (k_gemv_dec, k_gemv_dot): Y [M, N] f16 = A [M, K] f16 . W^T
+// (+ an f16 bias [N], or none) for M <= 16, f16 weights, packed or no zero points. decode_gemv_ok
+// tells whether it applies (alignment, 32-bit offsets); launch_decode_gemv picks the launch shape
+// for the size and launches.
 bool decode_gemv_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, const void* a, const void* y);
 void launch_decode_gemv(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,
-                        hipStream_t s, int num_cus);
+                        hipStream_t s, int num_cus, const void* bias = nullptr);
 // The f32 decode GEMV (k_gemv_f32): f32 A and weights, f32 Y without bias, M <= 4.
 bool decode_gemv_f32_ok(const tmh_weight* w, int64_t M, int64_t lda, int64_t ldy, const void* a);
 void launch_decode_gemv_f32(const tmh_weight* w, const void* a, int64_t M, int64_t lda, void* y, int64_t ldy,

@@ -9,7 +9,7 @@
 //
 // Kernels
 //   k_dequant         the {N, K} weights, bit-exact, in any float type
-//   k_gemv_dec        (tmh_gemv.h) decode GEMV for M <= 16, f16 Y without bias
+//   k_gemv_dec        (tmh_gemv.h) decode GEMV for M <= 16, f16 Y (an f16 bias or none)
 //   k_gemv_f16        f16 A and f16 weights, M <= 16*MT per block row: every lane unpacks its
 //                     16 bytes in registers into exact f16 weights (q - zero) * scale and feeds
 //                     v_mfma_f32_16x16x32_f16; four wavefronts split K and add through LDS
@@ -1244,10 +1244,11 @@ void launch_gemv_u(const tmh_weight* w, const MatArgs& a, hipStream_t s, int wav
 template <int BITS, int MT, bool HAS_ZP, bool SPLIT>
 void launch_gemv(const tmh_weight* w, const MatArgs& a, hipStream_t s, int num_cus) {
   const int64_t c = w->nchunks;
-  // The decode GEMV (tmh_gemv.hip): f16 Y without bias, aligned A, 32-bit offsets.
-  if (MT == 1 && a.y_dt == TMH_F16 && a.dot_dt == TMH_F16 && !a.bias &&
+  // The decode GEMV (tmh_gemv.hip): f16 Y without bias or with an f16 one, aligned A, 32-bit
+  // offsets.
+  if (MT == 1 && a.y_dt == TMH_F16 && a.dot_dt == TMH_F16 && (!a.bias || a.bias_dt == TMH_F16) &&
       decode_gemv_ok(w, a.M, a.lda, a.ldy, a.a, a.y)) {
-    launch_decode_gemv(w, a.a, a.M, a.lda, a.y, a.ldy, s, num_cus);
+    launch_decode_gemv(w, a.a, a.M, a.lda, a.y, a.ldy, s, num_cus, a.bias);
     return;
   }
   if (c <= 16) {
