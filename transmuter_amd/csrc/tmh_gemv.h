@@ -1,4 +1,5 @@
-// Decode GEMV kernel (M <= 16): f16 A, f16 weights from the tiled packed layout, f16 Y, no bias.
+// Decode GEMV kernel (M <= 16): f16 A, f16 weights from the tiled packed layout, f16 Y, an
+// optional f16 bias.
 //
 // Reference: MatMulNBits (lib/transmuter/ops/quantized.ex:30-46) after move/2, the dot of
 // quantized.ex:44 over dequantized {N, K} weights (Quantized.dequantize_weight/4, :234-240).
@@ -269,7 +270,7 @@ __device__ __forceinline__ half8_t row_piece(const uint4_t& x) {
 }
 
 // The decode GEMV for one row of A (M = 1), 4- or 8-bit weights whose parameters are constant
-// over a lane's GW values (block_size >= GW), f16 A / scales / Y, no bias: dot products instead
+// over a lane's GW values (block_size >= GW), f16 A / scales / Y, an optional f16 bias: dot products instead
 // of MFMAs, which at one row leave 15 of 16 MFMA columns empty while the per-weight scaling
 // costs the same VALU work.
 //

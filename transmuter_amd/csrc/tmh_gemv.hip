@@ -1,5 +1,5 @@
 // Launch plan of the decode GEMVs (k_gemv_dot for one row of A, k_gemv_dec, tmh_gemv.h):
-// MatMulNBits with M <= 16 rows of f16 A, f16 weights, f16 Y, no bias
+// MatMulNBits with M <= 16 rows of f16 A, f16 weights, f16 Y, no bias or an f16 one
 // (lib/transmuter/ops/quantized.ex:30-46 after move/2).
 //
 // This file is compiled with the kernels' leading arguments preloaded into SGPRs
